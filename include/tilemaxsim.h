@@ -1,0 +1,106 @@
+/*
+ * tilemaxsim C ABI -- fused MaxSim / PQ-ADC scoring on one MI355X (gfx950).
+ *
+ * Every entry point takes device pointers and plain sizes, enqueues its kernels on
+ * `stream` (a hipStream_t passed as void*; NULL = the legacy default stream) and
+ * returns without synchronising. Nothing here allocates device memory.
+ * Arguments are validated before any HIP call; a non-zero return is one of the
+ * TMS_ERR_* codes and tms_last_error() gives the message (per host thread).
+ *
+ * Layouts are row-major and dense: Q (nq, d); D (B, nd, d); D_flat (T, d);
+ * offsets (B + 1) int64; mask (B, nd) bytes (non-zero = real token);
+ * codebook (M, K, dsub); codes (B, nd, M) uint8; lut (nq, M, K) fp32; out (B) fp32.
+ * Element type of Q / D / codebook is given by `dtype` (TMS_DTYPE_*).
+ *
+ * Scores follow the reference: score[b] = sum_i max_j <Q[i], D[b, j]> with fp32
+ * accumulation; a document with no (unmasked) token scores -inf; nq == 0 gives 0.
+ */
+#ifndef TILEMAXSIM_H
+#define TILEMAXSIM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TMS_OK 0
+#define TMS_ERR_INVALID 1     /* bad argument (shape, pointer, offsets) */
+#define TMS_ERR_UNSUPPORTED 2 /* valid but not implemented (dtype, size limit) */
+#define TMS_ERR_HIP 3         /* the HIP runtime reported an error */
+
+#define TMS_DTYPE_F16 0
+#define TMS_DTYPE_BF16 1
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int tms_version(void);
+
+/* Message for the last non-zero status returned on this host thread. */
+const char* tms_last_error(void);
+
+/*
+ * Dense fixed-length MaxSim, every d (the d <= 128 kernel and the d-tiled kernel).
+ * Replaces flash_maxsim_v2_multiquery (src/flash_maxsim_v2.py:227-289) and its two
+ * kernels _flash_maxsim_v2_multiquery_kernel (:73-130) and
+ * _flash_maxsim_v2_mq_dimtile_kernel (:133-190); also serves flash_maxsim_v2
+ * (:193-224), flash_maxsim_batch (src/flash_maxsim_kernel.py:200-245) and
+ * flash_maxsim_single (:167-197), which compute the same scores.
+ */
+int tms_maxsim_dense(const void* Q, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype,
+                     float* out, void* stream);
+
+/*
+ * Dense MaxSim with a per-token validity mask: masked tokens are -inf before the max.
+ * Replaces the masked PyTorch scorer pytorch_maxsim_score(Q, D, D_mask)
+ * (src/e2e_retrieval_quality.py:105-110).
+ */
+int tms_maxsim_masked(const void* Q, int64_t nq, int64_t d, const void* D, const uint8_t* mask, int64_t B,
+                      int64_t nd, int dtype, float* out, void* stream);
+
+/*
+ * Variable-length MaxSim over a flat token buffer: document b is
+ * D_flat[offsets[b] : offsets[b+1]]. Offsets must be non-decreasing within
+ * [0, total_tokens]; a document whose offsets violate that scores NaN.
+ * Replaces flash_maxsim_multi_doc (src/flash_maxsim_kernel.py:248-273).
+ */
+int tms_maxsim_varlen(const void* Q, int64_t nq, int64_t d, const void* D_flat, int64_t total_tokens,
+                      const int64_t* offsets, int64_t B, int dtype, float* out, void* stream);
+
+/*
+ * Batched-query dense MaxSim: nQ queries of nq tokens each (Qs is (nQ, nq, d)) scored
+ * against the same documents in one pass over D; out is (nQ, B), row-major.
+ * Replaces nQ calls of flash_maxsim_v2_multiquery (src/flash_maxsim_v2.py:227-289).
+ */
+int tms_maxsim_dense_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B,
+                             int64_t nd, int dtype, float* out, void* stream);
+
+/*
+ * PQ distance table lut[q, m, k] = sum_j Q[q, m*dsub + j] * codebook[m, k, j] (fp32).
+ * Replaces TileMaxSimPQ.build_distance_table (src/flash_pqsim_kernel.py:190-211) and
+ * _build_distance_table_kernel (:31-67).
+ */
+int tms_pq_build_lut(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
+                     float* lut, void* stream);
+
+/*
+ * PQ MaxSim by table gather: out[b] = sum_q max_t sum_m lut[q, m, codes[b, t, m]].
+ * Replaces _flash_pqsim_batched_score_kernel (src/flash_pqsim_kernel.py:127-173) plus the
+ * host q-sum (:250), i.e. the scoring half of TileMaxSimPQ.score_batch (:213-252).
+ */
+int tms_pq_score_lut(const float* lut, int64_t nq, int64_t M, int64_t K, const uint8_t* codes, int64_t B, int64_t nd,
+                     float* out, void* stream);
+
+/*
+ * PQ MaxSim by codebook gather: each document token is rebuilt from the codebook in
+ * registers (never in HBM) and scored on MFMA; same scores as tms_pq_score_lut up to
+ * fp32 summation order. Replaces TileMaxSimPQ.score_batch (src/flash_pqsim_kernel.py:
+ * 213-252) as a whole.
+ */
+int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
+                 const uint8_t* codes, int64_t B, int64_t nd, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILEMAXSIM_H */

@@ -1,0 +1,260 @@
+"""GPU parity of the dense / masked / variable-length MaxSim kernels against the CPU oracle.
+
+Bar: |score - oracle| <= 1e-3 relative (fp32 accumulation), and
+identical top-100 rankings except for swaps among scores within that tolerance.
+The oracle is the float64 restatement of ``pytorch_maxsim_naive``
+(``src/flash_maxsim_kernel.py:280-288``) on the same fp16/bf16 input values.
+"""
+import numpy as np
+import pytest
+
+from oracle import maxsim_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-3
+ATOL = 1e-3
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _randn(rng, shape, normalize=False, dtype=np.float16):
+    x = rng.standard_normal(shape, dtype=np.float32)
+    if normalize:
+        x /= np.linalg.norm(x, axis=-1, keepdims=True) + 1e-12
+    return x.astype(dtype)
+
+
+def _to_gpu(x, torch_dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(x))
+    if torch_dtype is not None:
+        t = t.to(torch_dtype)
+    return t.cuda()
+
+
+def _assert_scores(got, ref, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    inf_ref = np.isinf(ref)
+    assert np.array_equal(np.isinf(got), inf_ref), f"{what}: -inf pattern differs"
+    assert np.all(got[inf_ref] == ref[inf_ref]), f"{what}: infinite values differ"
+    fin = ~inf_ref
+    np.testing.assert_allclose(got[fin], ref[fin], rtol=RTOL, atol=ATOL, err_msg=what)
+
+
+# exp10 shape grid of the reference (src/run_all_experiments.py:617-626): (Nq, Nd, d, B)
+EXP10_GRID = [
+    (8, 32, 64, 100), (16, 64, 128, 100), (32, 128, 128, 100), (32, 128, 256, 100),
+    (32, 256, 128, 100), (64, 128, 128, 100), (32, 128, 384, 50), (32, 128, 768, 20),
+]
+
+
+@pytest.mark.parametrize("Nq,Nd,d,B", EXP10_GRID)
+def test_exp10_grid_unnormalised(cuda, Nq, Nd, d, B):
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    rng = _rng(1000 + Nq + Nd + d)
+    Q = _randn(rng, (Nq, d))
+    D = _randn(rng, (B, Nd, d))
+    got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(D)).cpu().numpy()
+    _assert_scores(got, orc.maxsim_f64(Q, D), f"exp10 Nq={Nq} Nd={Nd} d={d} B={B}")
+
+
+EDGE = [
+    # (Nq, Nd, d, B)
+    (1, 1, 128, 1), (1, 1, 32, 7), (32, 1, 128, 33), (32, 180, 128, 257), (33, 17, 128, 50),
+    (100, 40, 128, 20), (200, 9, 64, 11), (32, 128, 32, 64), (32, 64, 96, 64), (32, 50, 80, 40),
+    (32, 50, 200, 40), (20, 70, 1000, 9), (32, 33, 512, 30), (5, 300, 128, 3), (32, 31, 136, 17),
+]
+
+
+@pytest.mark.parametrize("Nq,Nd,d,B", EDGE)
+def test_dense_edge_shapes(cuda, Nq, Nd, d, B):
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    rng = _rng(7 * Nq + 13 * Nd + d + B)
+    Q = _randn(rng, (Nq, d), normalize=True)
+    D = _randn(rng, (B, Nd, d), normalize=True)
+    got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(D)).cpu().numpy()
+    _assert_scores(got, orc.maxsim_f64(Q, D), f"Nq={Nq} Nd={Nd} d={d} B={B}")
+
+
+@pytest.mark.parametrize("d", [100, 130, 6])
+def test_dense_unaligned_width(cuda, d):
+    """d not a multiple of 8 takes the element-wise load path."""
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    rng = _rng(d)
+    Q = _randn(rng, (32, d))
+    D = _randn(rng, (40, 37, d))
+    got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(D)).cpu().numpy()
+    _assert_scores(got, orc.maxsim_f64(Q, D), f"d={d}")
+
+
+def test_dense_misaligned_pointer(cuda):
+    """A contiguous view that starts 2 bytes into its storage (not 16-byte aligned)."""
+    import torch
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    rng = _rng(5)
+    Q = _randn(rng, (32, 128))
+    D = _randn(rng, (30 * 20 * 128 + 1,))
+    Dg = _to_gpu(D)[1:].view(30, 20, 128)
+    assert Dg.data_ptr() % 16 != 0
+    got = flash_maxsim_v2_multiquery(_to_gpu(Q), Dg).cpu().numpy()
+    _assert_scores(got, orc.maxsim_f64(Q, D[1:].reshape(30, 20, 128)), "misaligned")
+
+
+def test_empty_documents_and_batch(cuda):
+    import torch
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    Q = _to_gpu(np.ones((4, 64), np.float16))
+    D0 = torch.empty(5, 0, 64, dtype=torch.float16, device="cuda")
+    got = flash_maxsim_v2_multiquery(Q, D0).cpu().numpy()
+    assert np.all(np.isneginf(got)) and got.shape == (5,)
+    DB0 = torch.empty(0, 8, 64, dtype=torch.float16, device="cuda")
+    assert flash_maxsim_v2_multiquery(Q, DB0).shape == (0,)
+    Qe = torch.empty(0, 64, dtype=torch.float16, device="cuda")
+    D = torch.ones(3, 8, 64, dtype=torch.float16, device="cuda")
+    assert np.all(flash_maxsim_v2_multiquery(Qe, D).cpu().numpy() == 0.0)
+
+
+def test_bf16_and_fp32_query(cuda):
+    import torch
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    rng = _rng(11)
+    Q = rng.standard_normal((32, 128), dtype=np.float32)
+    D = rng.standard_normal((64, 70, 128), dtype=np.float32)
+    Qb = torch.from_numpy(Q).to(torch.bfloat16)
+    Db = torch.from_numpy(D).to(torch.bfloat16)
+    got = flash_maxsim_v2_multiquery(Qb.cuda(), Db.cuda()).cpu().numpy()
+    _assert_scores(got, orc.maxsim_f64(Qb.float().numpy(), Db.float().numpy()), "bf16")
+    # fp32 queries are cast to the document dtype on device
+    Dh = D.astype(np.float16)
+    got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(Dh)).cpu().numpy()
+    _assert_scores(got, orc.maxsim_f64(Q.astype(np.float16), Dh), "fp32 Q")
+
+
+def test_c1_ranking_parity(cuda):
+    """1 query x 1000 docs x Nd=128, d=128, L2-normalised fp16.
+    Top-100 must match the oracle except swaps among scores within tolerance."""
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    rng = _rng(0)
+    Q = _randn(rng, (32, 128), normalize=True)
+    D = _randn(rng, (1000, 128, 128), normalize=True)
+    got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(D)).cpu().numpy()
+    ref = orc.maxsim_f64(Q, D)
+    _assert_scores(got, ref, "C1")
+    _assert_topk_equal(got, ref, 100)
+
+
+def _assert_topk_equal(got, ref, k):
+    """Top-k index sets agree except for documents whose oracle score is within
+    tolerance of the k-th oracle score (ties within tolerance)."""
+    ref = np.asarray(ref, np.float64)
+    _, gi = orc.topk(got, k)
+    _, ri = orc.topk(ref, k)
+    kth = np.sort(ref)[::-1][k - 1]
+    tol = RTOL * abs(kth) + ATOL
+    diff = set(gi.tolist()) ^ set(ri.tolist())
+    for i in diff:
+        assert abs(ref[i] - kth) <= tol, f"doc {i} (score {ref[i]}) differs in top-{k}, kth={kth}"
+
+
+def test_determinism(cuda):
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    rng = _rng(3)
+    Q = _to_gpu(_randn(rng, (64, 128)))
+    D = _to_gpu(_randn(rng, (2000, 50, 128)))
+    a = flash_maxsim_v2_multiquery(Q, D).cpu().numpy()
+    for _ in range(3):
+        b = flash_maxsim_v2_multiquery(Q, D).cpu().numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_single_and_batch_entry_points(cuda):
+    from tilemaxsim_amd import flash_maxsim_batch, flash_maxsim_single, flash_maxsim_v2
+    rng = _rng(21)
+    Q = _randn(rng, (32, 128))
+    D = _randn(rng, (16, 128, 128))
+    ref = orc.maxsim_f64(Q, D)
+    _assert_scores(flash_maxsim_batch(_to_gpu(Q), _to_gpu(D)).cpu().numpy(), ref, "batch")
+    _assert_scores(flash_maxsim_v2(_to_gpu(Q), _to_gpu(D)).cpu().numpy(), ref, "v2")
+    s = flash_maxsim_single(_to_gpu(Q), _to_gpu(D[3]))
+    assert s.dim() == 0
+    _assert_scores(np.array([s.item()]), ref[3:4], "single")
+
+
+@pytest.mark.parametrize("dist", ["uniform", "with_empty"])
+def test_varlen(cuda, dist):
+    import torch
+    from tilemaxsim_amd import flash_maxsim_multi_doc
+    rng = _rng(99 if dist == "uniform" else 98)
+    B = 3000
+    lens = rng.integers(32, 301, size=B)
+    if dist == "with_empty":
+        lens = rng.integers(0, 40, size=B)
+        lens[rng.random(B) < 0.2] = 0
+        lens[:3] = 0
+        lens[-2:] = 0
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(offsets[-1])
+    Q = _randn(rng, (32, 128), normalize=True)
+    Dflat = _randn(rng, (T, 128), normalize=True)
+    got = flash_maxsim_multi_doc(_to_gpu(Q), _to_gpu(Dflat), torch.from_numpy(offsets)).cpu().numpy()
+    _assert_scores(got, orc.maxsim_varlen(Q, Dflat, offsets, f64=True), f"varlen {dist}")
+
+
+def test_varlen_equals_fixed(cuda):
+    import torch
+    from tilemaxsim_amd import flash_maxsim_multi_doc, flash_maxsim_v2_multiquery
+    rng = _rng(17)
+    Q = _to_gpu(_randn(rng, (32, 128), normalize=True))
+    D = _to_gpu(_randn(rng, (500, 77, 128), normalize=True))
+    offs = torch.arange(0, 501 * 77, 77, dtype=torch.int64)
+    a = flash_maxsim_v2_multiquery(Q, D).cpu().numpy()
+    b = flash_maxsim_multi_doc(Q, D.view(-1, 128), offs).cpu().numpy()
+    assert np.array_equal(a, b)
+
+
+def test_varlen_bad_offsets(cuda):
+    import torch
+    from tilemaxsim_amd import flash_maxsim_multi_doc
+    Q = torch.ones(4, 64, dtype=torch.float16, device="cuda")
+    D = torch.ones(10, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        flash_maxsim_multi_doc(Q, D, torch.tensor([0, 5, 3, 10]))
+    with pytest.raises(ValueError):
+        flash_maxsim_multi_doc(Q, D, torch.tensor([0, 5, 11]))
+    got = flash_maxsim_multi_doc(Q, D, torch.tensor([0, 5, 3, 10]), validate=False).cpu().numpy()
+    assert np.isnan(got[1]) and got[0] == 4 * 64 and got[2] == 4 * 64
+
+
+def test_masked(cuda):
+    import torch
+    from tilemaxsim_amd import maxsim_score
+    rng = _rng(23)
+    B, Nd, d = 300, 90, 128
+    Q = _randn(rng, (32, d), normalize=True)
+    D = _randn(rng, (B, Nd, d), normalize=True)
+    mask = rng.random((B, Nd)) < 0.6
+    mask[0] = False
+    mask[1, :] = False
+    mask[1, -1] = True
+    got = maxsim_score(_to_gpu(Q), _to_gpu(D), torch.from_numpy(mask).cuda()).cpu().numpy()
+    _assert_scores(got, orc.maxsim_masked(Q, D, mask, f64=True), "masked")
+
+
+def test_batched_queries(cuda):
+    import torch
+    from tilemaxsim_amd import flash_maxsim_batched_queries, flash_maxsim_v2_multiquery
+    rng = _rng(31)
+    for nQ, Nq in [(5, 32), (3, 20), (4, 70)]:
+        Qs = _to_gpu(_randn(rng, (nQ, Nq, 128), normalize=True))
+        D = _to_gpu(_randn(rng, (400, 60, 128), normalize=True))
+        got = flash_maxsim_batched_queries(Qs, D).cpu().numpy()
+        for i in range(nQ):
+            ref = orc.maxsim_f64(Qs[i].cpu().numpy(), D.cpu().numpy())
+            _assert_scores(got[i], ref, f"batched nQ={nQ} Nq={Nq} q={i}")
+            single = flash_maxsim_v2_multiquery(Qs[i], D).cpu().numpy()
+            _assert_scores(got[i], single, "batched vs single")

@@ -1,0 +1,99 @@
+"""ctypes binding of ``libtilemaxsim.so`` (the C ABI declared in ``include/tilemaxsim.h``).
+
+The library is loaded lazily on first use and is REQUIRED: there is no CPU or
+PyTorch fallback, so a missing or unloadable library raises immediately.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libtilemaxsim.so")
+
+TMS_OK = 0
+TMS_ERR_INVALID = 1
+TMS_ERR_UNSUPPORTED = 2
+TMS_ERR_HIP = 3
+
+TMS_DTYPE_F16 = 0
+TMS_DTYPE_BF16 = 1
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+# name -> argtypes (restype is int for every entry point except tms_last_error)
+SIGNATURES = {
+    "tms_version": [],
+    "tms_maxsim_dense": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _int, _c_void_p, _c_void_p],
+    "tms_maxsim_masked": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _i64, _int, _c_void_p, _c_void_p],
+    "tms_maxsim_varlen": [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p, _i64, _int, _c_void_p, _c_void_p],
+    "tms_maxsim_dense_batched": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _int, _c_void_p, _c_void_p],
+    "tms_pq_build_lut": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _c_void_p],
+    "tms_pq_score_lut": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
+    "tms_pq_score": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class TileMaxSimError(RuntimeError):
+    """The HIP runtime reported an error inside the library."""
+
+
+def load() -> ctypes.CDLL:
+    """Load the shared library (once). Raises ImportError if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m tilemaxsim_amd.build` "
+                "(tilemaxsim_amd has no CPU fallback)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name, None)
+            if fn is None:
+                continue  # calling it raises AttributeError
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        lib.tms_last_error.argtypes = []
+        lib.tms_last_error.restype = ctypes.c_char_p
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    """Turn a non-zero C status into the matching Python exception."""
+    if status == TMS_OK:
+        return
+    msg = load().tms_last_error().decode(errors="replace")
+    if status == TMS_ERR_INVALID:
+        raise ValueError(msg)
+    if status == TMS_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise TileMaxSimError(msg)
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float16:
+        return TMS_DTYPE_F16
+    if dt == torch.bfloat16:
+        return TMS_DTYPE_BF16
+    raise TypeError(f"tilemaxsim_amd kernels take float16 or bfloat16 embeddings, got {dt}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """hipStream_t of torch's current stream on the tensor's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,524 @@
+// Dense / masked / variable-length MaxSim on gfx950 MFMA.
+//
+// score[qi][b] = sum_{i < nq} max_{j < len(b)} <Q[qi, i], D_b[j]>, fp32 accumulation.
+//
+// Reference semantics (src/flash_maxsim_v2.py:73-190, src/flash_maxsim_kernel.py:248-273,
+// src/e2e_retrieval_quality.py:105-110): doc rows outside the document are -inf
+// before the max, query rows past nq contribute 0, an empty document scores -inf.
+//
+// Design (one wave = one independent stream of whole documents):
+//  * Query tokens are grouped in blocks of 32 (two 16-column halves). A launch covers
+//    NQB consecutive blocks; their fragments stay in VGPRs (d <= 128) or in LDS
+//    (any other d), and the block -> (query, token) map lets one launch score several
+//    queries against one pass over D.
+//  * Each document token is read from HBM exactly once, straight into MFMA A-operand
+//    registers: lane (r = l%16, g = l/16) loads the 16-byte chunk 4*s + g of token
+//    r at k-step s. Four lanes cover 64 contiguous bytes of a token per instruction,
+//    which streams at the same rate as a fully coalesced copy on this part.
+//  * A tile is 16*NSUB tokens x 128 dims; the next tile's loads are issued before the
+//    current tile's MFMAs (register double buffer). Tokens past the end of a
+//    document are clamped to its last token: a duplicate cannot change a max, so
+//    no -inf masking is needed and nothing outside the document is fetched.
+//  * The per-(query token, row) running max lives in the MFMA accumulator layout; the
+//    cross-lane max and the sum over query tokens happen once per document.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "tms_common.h"
+
+namespace tms {
+
+static thread_local char g_err[512];
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TMS_ERR_HIP, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+  return TMS_OK;
+}
+
+enum { MODE_FIXED = 0, MODE_VARLEN = 1, MODE_MASKED = 2 };
+
+struct DenseArgs {
+  const uint8_t* Q;        // (nQ * nq, d) elements of the input dtype
+  const uint8_t* D;        // fixed / masked: (B, nd, d); varlen: (total_tokens, d)
+  const int64_t* offsets;  // varlen: (B + 1)
+  const uint8_t* mask;     // masked: (B, nd)
+  float* out;              // (nQ, B)
+  int64_t B, nd, total_tokens;
+  int32_t nq;              // tokens per query
+  int32_t nbq;             // 32-token blocks per query = ceil(nq / 32)
+  int32_t blk0;            // first global query block of this launch
+  int32_t nblk;            // blocks in this launch (<= NQB template)
+  int32_t d, nchunk, nstep, nkg;
+  int32_t docs_per_wave;
+};
+
+// 16-byte fragment of row `row`, chunk c (elements 8c .. 8c+7), zero outside [0, d).
+template <bool ALIGNED>
+__device__ __forceinline__ u32x4 load_chunk(const uint8_t* base, int64_t row, int c, int d, int nchunk) {
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if constexpr (ALIGNED) {
+    if (c < nchunk) v = *(const u32x4*)(base + (row * d + 8 * (int64_t)c) * 2);
+  } else {
+    const uint16_t* p = (const uint16_t*)base + row * d;
+    uint16_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      int k = 8 * c + j;
+      e[j] = (k < d) ? p[k] : (uint16_t)0;
+    }
+    v[0] = e[0] | ((uint32_t)e[1] << 16);
+    v[1] = e[2] | ((uint32_t)e[3] << 16);
+    v[2] = e[4] | ((uint32_t)e[5] << 16);
+    v[3] = e[6] | ((uint32_t)e[7] << 16);
+  }
+  return v;
+}
+
+struct Cursor {
+  int64_t b;     // document index
+  int64_t base;  // first token row of the document
+  int64_t len;   // tokens in the document
+  int64_t t0;    // first token of the current tile
+  int32_t kg;    // current 128-dim k-group
+};
+
+// KS_REG > 0: Q fragments in VGPRs, d == 32 * KS_REG (single k-group).
+// KS_REG == 0: Q fragments in LDS, k-groups of 4 steps (128 dims), any d.
+template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, int NSUB>
+__global__ void __launch_bounds__(256) dense_maxsim_kernel(DenseArgs a) {
+  constexpr bool QREG = KS_REG > 0;
+  constexpr int KS = QREG ? KS_REG : 4;
+  constexpr int TT = 16 * NSUB;
+  extern __shared__ u32x4 qlds[];
+
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+
+  // ---- query fragments -------------------------------------------------------
+  // Fragment (block j, step S, half h) for this lane: query row of block j, token
+  // 16h + r, elements of chunk 4S + g.
+  auto q_row = [&](int j, int h, int rr, bool& valid) -> int64_t {
+    int jb = a.blk0 + j;
+    int qi = jb / a.nbq;
+    int tok = (jb - qi * a.nbq) * 32 + 16 * h + rr;
+    valid = (j < a.nblk) && (tok < a.nq);
+    return (int64_t)qi * a.nq + tok;
+  };
+
+  u32x4 qf[QREG ? NQB : 1][QREG ? KS : 1][2];
+  if constexpr (QREG) {
+#pragma unroll
+    for (int j = 0; j < NQB; j++)
+#pragma unroll
+      for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          bool valid;
+          int64_t row = q_row(j, h, r, valid);
+          qf[j][s][h] = valid ? load_chunk<true>(a.Q, row, 4 * s + g, a.d, a.nchunk) : u32x4{0u, 0u, 0u, 0u};
+        }
+  } else {
+    const int nfrag = NQB * a.nstep * 2 * 64;
+    for (int f = threadIdx.x; f < nfrag; f += blockDim.x) {
+      int fl = f & 63, rest = f >> 6;
+      int h = rest & 1;
+      rest >>= 1;
+      int S = rest % a.nstep, j = rest / a.nstep;
+      bool valid;
+      int64_t row = q_row(j, h, fl & 15, valid);
+      qlds[f] = valid ? load_chunk<ALIGNED>(a.Q, row, 4 * S + (fl >> 4), a.d, a.nchunk) : u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+  }
+
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t b_begin = wave * a.docs_per_wave;
+  if (b_begin >= a.B) return;
+  const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
+
+  const float NEG_INF = -__builtin_inff();
+
+  // ---- per-query output ------------------------------------------------------
+  // Block sums are added per query; a query whose first block precedes this launch
+  // accumulates onto the previous launch's partial score.
+  auto write_doc = [&](int64_t b, const float (&blk)[NQB]) {
+    if (lane == 0) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < NQB; j++) {
+        if (j >= a.nblk) break;
+        int jb = a.blk0 + j;
+        int qi = jb / a.nbq;
+        s += blk[j];
+        bool last_of_query = (j == a.nblk - 1) || ((jb + 1) / a.nbq != qi);
+        if (last_of_query) {
+          float* o = a.out + (int64_t)qi * a.B + b;
+          bool cont = (qi * a.nbq) < a.blk0;  // query began in an earlier launch
+          *o = cont ? (*o + s) : s;
+          s = 0.f;
+        }
+      }
+    }
+  };
+
+  auto write_empty = [&](int64_t b, float v) {
+    float blk[NQB];
+#pragma unroll
+    for (int j = 0; j < NQB; j++) {
+      // -inf for every block that holds a real token (all blocks in range do)
+      blk[j] = v;
+    }
+    write_doc(b, blk);
+  };
+
+  // ---- document cursor -------------------------------------------------------
+  auto doc_info = [&](int64_t b, int64_t& base, bool& bad) -> int64_t {
+    bad = false;
+    if constexpr (MODE == MODE_VARLEN) {
+      int64_t s = a.offsets[b], e = a.offsets[b + 1];
+      if (s < 0 || e < s || e > a.total_tokens) {
+        bad = true;
+        base = 0;
+        return 0;
+      }
+      base = s;
+      return e - s;
+    } else {
+      base = b * a.nd;
+      return a.nd;
+    }
+  };
+  // Move to the first document at or after b with at least one token; documents
+  // skipped on the way are written (-inf, or NaN for invalid offsets).
+  auto seek = [&](Cursor& c, int64_t b) {
+    for (; b < b_end; b++) {
+      bool bad;
+      int64_t base;
+      int64_t len = doc_info(b, base, bad);
+      if (len > 0) {
+        c.b = b;
+        c.base = base;
+        c.len = len;
+        c.t0 = 0;
+        c.kg = 0;
+        return;
+      }
+      write_empty(b, bad ? __builtin_nanf("") : NEG_INF);
+    }
+    c.b = b_end;
+  };
+  auto advance = [&](Cursor& c) {
+    if (c.kg + 1 < a.nkg) {
+      c.kg++;
+      return;
+    }
+    c.kg = 0;
+    c.t0 += TT;
+    if (c.t0 >= c.len) seek(c, c.b + 1);
+  };
+
+  // ---- tile buffers ------------------------------------------------------------
+  struct Buf {
+    u32x4 f[NSUB][KS];
+    uint32_t m[NSUB];  // masked mode: validity bits of this lane's 4 output rows
+  };
+  auto load_tile = [&](Buf& buf, const Cursor& c) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; sub++) {
+      int64_t tok = c.t0 + 16 * sub + r;
+      if (tok > c.len - 1) tok = c.len - 1;
+      const int64_t row = c.base + tok;
+#pragma unroll
+      for (int s = 0; s < KS; s++) {
+        const int S = c.kg * KS + s;
+        if (!QREG && S >= a.nstep) {
+          buf.f[sub][s] = u32x4{0u, 0u, 0u, 0u};
+        } else if constexpr (FULL && ALIGNED) {
+          buf.f[sub][s] = *(const u32x4*)(a.D + (row * a.d + 8 * (int64_t)(4 * S + g)) * 2);
+        } else {
+          buf.f[sub][s] = load_chunk<ALIGNED>(a.D, row, 4 * S + g, a.d, a.nchunk);
+        }
+      }
+      if constexpr (MODE == MODE_MASKED) {
+        uint32_t bits = 0;
+        if (c.kg == a.nkg - 1) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            int64_t t = c.t0 + 16 * sub + 4 * g + i;
+            if (t > c.len - 1) t = c.len - 1;
+            bits |= (a.mask[c.b * a.nd + t] != 0 ? 1u : 0u) << i;
+          }
+        }
+        buf.m[sub] = bits;
+      }
+    }
+  };
+
+  f32x4 acc[NSUB][NQB][2];
+  f32x4 rmax[NQB][2];
+#pragma unroll
+  for (int j = 0; j < NQB; j++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      rmax[j][h] = f32x4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+#pragma unroll
+      for (int sub = 0; sub < NSUB; sub++) acc[sub][j][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  auto finish_doc = [&](int64_t b) {
+    float blk[NQB];
+#pragma unroll
+    for (int j = 0; j < NQB; j++) {
+      float s = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        float m = fmaxf(fmaxf(rmax[j][h][0], rmax[j][h][1]), fmaxf(rmax[j][h][2], rmax[j][h][3]));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        bool valid;
+        (void)q_row(j, h, r, valid);
+        s += valid ? m : 0.f;
+      }
+      s += __shfl_xor(s, 8);
+      s += __shfl_xor(s, 4);
+      s += __shfl_xor(s, 2);
+      s += __shfl_xor(s, 1);
+      blk[j] = s;
+      rmax[j][0] = f32x4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+      rmax[j][1] = f32x4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+    }
+    write_doc(b, blk);
+  };
+
+  auto compute_tile = [&](const Buf& buf, const Cursor& c) {
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+      const int S = c.kg * KS + s;
+      if (!QREG && S >= a.nstep) break;
+#pragma unroll
+      for (int j = 0; j < NQB; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          u32x4 qv;
+          if constexpr (QREG) qv = qf[j][s][h];
+          else qv = qlds[((j * a.nstep + S) * 2 + h) * 64 + lane];
+#pragma unroll
+          for (int sub = 0; sub < NSUB; sub++) acc[sub][j][h] = mfma16x16x32<DT>(buf.f[sub][s], qv, acc[sub][j][h]);
+        }
+    }
+    if (c.kg == a.nkg - 1) {
+#pragma unroll
+      for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+        for (int j = 0; j < NQB; j++)
+#pragma unroll
+          for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              float v = acc[sub][j][h][i];
+              if constexpr (MODE == MODE_MASKED) v = ((buf.m[sub] >> i) & 1u) ? v : NEG_INF;
+              rmax[j][h][i] = fmaxf(rmax[j][h][i], v);
+            }
+            acc[sub][j][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+      if (c.t0 + TT >= c.len) finish_doc(c.b);
+    }
+  };
+
+  // ---- pipelined main loop -----------------------------------------------------
+  Cursor cur;
+  seek(cur, b_begin);
+  if (cur.b >= b_end) return;
+  Buf b0, b1;
+  load_tile(b0, cur);
+  while (true) {
+    Cursor nxt = cur;
+    advance(nxt);
+    if (nxt.b < b_end) load_tile(b1, nxt);
+    compute_tile(b0, cur);
+    if (nxt.b >= b_end) break;
+    cur = nxt;
+    advance(nxt);
+    if (nxt.b < b_end) load_tile(b0, nxt);
+    compute_tile(b1, cur);
+    if (nxt.b >= b_end) break;
+    cur = nxt;
+  }
+}
+
+// Writes v into out[0..n).
+__global__ void fill_kernel(float* out, int64_t n, float v) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = v;
+}
+
+static int fill(float* out, int64_t n, float v, hipStream_t st) {
+  if (n <= 0) return TMS_OK;
+  int64_t grid = (n + 255) / 256;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)grid), dim3(256), 0, st, out, n, v);
+  return check_launch("fill");
+}
+
+// ------------------------------------------------------------------------------
+// host dispatch
+// ------------------------------------------------------------------------------
+constexpr int kNSub = 2;
+constexpr int kMaxQldsBytes = 64 * 1024;
+
+template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED>
+static int launch_one(const DenseArgs& a, int64_t grid, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((dense_maxsim_kernel<DT, MODE, NQB, KS_REG, FULL, ALIGNED, kNSub>), dim3((unsigned)grid), dim3(256),
+                     lds, st, a);
+  return check_launch("dense_maxsim_kernel");
+}
+
+template <int DT, int MODE, int NQB>
+static int launch_nqb(const DenseArgs& a, bool aligned, int64_t grid, hipStream_t st) {
+  const bool full = aligned && (a.d % 32 == 0);
+  if (aligned && a.d > 0 && a.d <= 128 && a.d % 32 == 0) {
+    switch (a.d / 32) {
+      case 1: return launch_one<DT, MODE, NQB, 1, true, true>(a, grid, 0, st);
+      case 2: return launch_one<DT, MODE, NQB, 2, true, true>(a, grid, 0, st);
+      case 3: return launch_one<DT, MODE, NQB, 3, true, true>(a, grid, 0, st);
+      default: return launch_one<DT, MODE, NQB, 4, true, true>(a, grid, 0, st);
+    }
+  }
+  size_t lds = (size_t)NQB * a.nstep * 2 * 64 * 16;
+  if (lds == 0) lds = 16;
+  if (full) return launch_one<DT, MODE, NQB, 0, true, true>(a, grid, lds, st);
+  if (aligned) return launch_one<DT, MODE, NQB, 0, false, true>(a, grid, lds, st);
+  return launch_one<DT, MODE, NQB, 0, false, false>(a, grid, lds, st);
+}
+
+// Documents per wave: enough waves to fill the chip several times over, so the
+// hardware dispatcher balances ragged documents, but long enough streams that the
+// per-wave query-fragment load is amortised.
+static int pick_docs_per_wave(int64_t B, int64_t tokens_per_doc_hint) {
+  const int64_t target_waves = 256 * 16 * 8;
+  int64_t dpw = B / target_waves;
+  if (tokens_per_doc_hint > 0 && dpw * tokens_per_doc_hint > 16384) dpw = 16384 / tokens_per_doc_hint;
+  if (dpw < 1) dpw = 1;
+  if (dpw > 64) dpw = 64;
+  return (int)dpw;
+}
+
+template <int DT>
+static int run_dense(DenseArgs a, int64_t nQ, int mode, bool aligned, hipStream_t st) {
+  const int64_t nblocks_total = nQ * (int64_t)a.nbq;
+  const int64_t waves = (a.B + a.docs_per_wave - 1) / a.docs_per_wave;
+  const int64_t grid = (waves + 3) / 4;
+  // Blocks per launch: two when Q fits in VGPRs or its LDS copy stays small.
+  int maxq = 2;
+  if (!(aligned && a.d > 0 && a.d <= 128 && a.d % 32 == 0) && (int64_t)2 * a.nstep * 2 * 1024 > kMaxQldsBytes) maxq = 1;
+  for (int64_t blk0 = 0; blk0 < nblocks_total; blk0 += maxq) {
+    a.blk0 = (int32_t)blk0;
+    a.nblk = (int32_t)((nblocks_total - blk0 < maxq) ? nblocks_total - blk0 : maxq);
+    int rc;
+    if (a.nblk == 2) {
+      if (mode == MODE_FIXED) rc = launch_nqb<DT, MODE_FIXED, 2>(a, aligned, grid, st);
+      else if (mode == MODE_VARLEN) rc = launch_nqb<DT, MODE_VARLEN, 2>(a, aligned, grid, st);
+      else rc = launch_nqb<DT, MODE_MASKED, 2>(a, aligned, grid, st);
+    } else {
+      if (mode == MODE_FIXED) rc = launch_nqb<DT, MODE_FIXED, 1>(a, aligned, grid, st);
+      else if (mode == MODE_VARLEN) rc = launch_nqb<DT, MODE_VARLEN, 1>(a, aligned, grid, st);
+      else rc = launch_nqb<DT, MODE_MASKED, 1>(a, aligned, grid, st);
+    }
+    if (rc != TMS_OK) return rc;
+  }
+  return TMS_OK;
+}
+
+static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B,
+                       int64_t nd, int64_t total_tokens, const int64_t* offsets, const uint8_t* mask, int mode,
+                       int dtype, float* out, void* stream) {
+  if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16) return fail(TMS_ERR_UNSUPPORTED, "%s: unsupported dtype %d", fn, dtype);
+  if (nQ < 0 || nq < 0 || d < 0 || B < 0 || nd < 0 || total_tokens < 0)
+    return fail(TMS_ERR_INVALID, "%s: negative size (nQ=%lld nq=%lld d=%lld B=%lld nd=%lld T=%lld)", fn, (long long)nQ,
+                (long long)nq, (long long)d, (long long)B, (long long)nd, (long long)total_tokens);
+  if (B == 0 || nQ == 0) return TMS_OK;
+  if (!out) return fail(TMS_ERR_INVALID, "%s: out is NULL", fn);
+  hipStream_t st = (hipStream_t)stream;
+  if (nq == 0) return fill(out, nQ * B, 0.f, st);
+  if (!Q) return fail(TMS_ERR_INVALID, "%s: Q is NULL", fn);
+  if (mode == MODE_VARLEN && !offsets) return fail(TMS_ERR_INVALID, "%s: offsets is NULL", fn);
+  if (mode == MODE_MASKED && nd > 0 && !mask) return fail(TMS_ERR_INVALID, "%s: mask is NULL", fn);
+  const int64_t rows = (mode == MODE_VARLEN) ? total_tokens : B * nd;
+  if (rows > 0 && d > 0 && !D) return fail(TMS_ERR_INVALID, "%s: D is NULL", fn);
+  if (d > 1024) return fail(TMS_ERR_UNSUPPORTED, "%s: d=%lld > 1024 is not supported", fn, (long long)d);
+  if (nq > (int64_t)1 << 24 || nQ > (int64_t)1 << 20 || nQ * ((nq + 31) / 32) > ((int64_t)1 << 30))
+    return fail(TMS_ERR_UNSUPPORTED, "%s: too many query tokens", fn);
+
+  DenseArgs a;
+  memset(&a, 0, sizeof(a));
+  a.Q = (const uint8_t*)Q;
+  a.D = (const uint8_t*)D;
+  a.offsets = offsets;
+  a.mask = mask;
+  a.out = out;
+  a.B = B;
+  a.nd = nd;
+  a.total_tokens = total_tokens;
+  a.nq = (int32_t)nq;
+  a.nbq = (int32_t)((nq + 31) / 32);
+  a.d = (int32_t)d;
+  a.nchunk = (int32_t)((d + 7) / 8);
+  a.nstep = (int32_t)((d + 31) / 32);
+  a.nkg = (int32_t)((a.nstep + 3) / 4);
+  if (a.nkg < 1) a.nkg = 1;
+  int64_t hint = (mode == MODE_VARLEN) ? (B > 0 ? total_tokens / B : 0) : nd;
+  a.docs_per_wave = pick_docs_per_wave(B, hint);
+  const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
+  if (dtype == TMS_DTYPE_F16) return run_dense<TMS_DTYPE_F16>(a, nQ, mode, aligned, st);
+  return run_dense<TMS_DTYPE_BF16>(a, nQ, mode, aligned, st);
+}
+
+}  // namespace tms
+
+extern "C" {
+
+int tms_version(void) { return 100; }
+
+const char* tms_last_error(void) { return tms::g_err; }
+
+int tms_maxsim_dense(const void* Q, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype, float* out,
+                     void* stream) {
+  return tms::dense_entry("tms_maxsim_dense", Q, 1, nq, d, D, B, nd, 0, nullptr, nullptr, tms::MODE_FIXED, dtype, out,
+                          stream);
+}
+
+int tms_maxsim_masked(const void* Q, int64_t nq, int64_t d, const void* D, const uint8_t* mask, int64_t B, int64_t nd,
+                      int dtype, float* out, void* stream) {
+  return tms::dense_entry("tms_maxsim_masked", Q, 1, nq, d, D, B, nd, 0, nullptr, mask, tms::MODE_MASKED, dtype, out,
+                          stream);
+}
+
+int tms_maxsim_varlen(const void* Q, int64_t nq, int64_t d, const void* D_flat, int64_t total_tokens,
+                      const int64_t* offsets, int64_t B, int dtype, float* out, void* stream) {
+  return tms::dense_entry("tms_maxsim_varlen", Q, 1, nq, d, D_flat, B, 0, total_tokens, offsets, nullptr,
+                          tms::MODE_VARLEN, dtype, out, stream);
+}
+
+int tms_maxsim_dense_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd,
+                             int dtype, float* out, void* stream) {
+  return tms::dense_entry("tms_maxsim_dense_batched", Qs, nQ, nq, d, D, B, nd, 0, nullptr, nullptr, tms::MODE_FIXED,
+                          dtype, out, stream);
+}
+
+}  // extern "C"
