@@ -1,0 +1,141 @@
+"""GPU parity of the PQ / ADC kernels (``TileMaxSimPQ``) against the CPU oracle.
+
+Oracles: the reference's decompress-then-score baseline ``pytorch_pqsim_baseline``
+(``src/flash_pqsim_kernel.py:283-313``) in float64, and the table-gather form
+(``:127-173``). Bar: |score - oracle| <= 1e-3 relative; identical top-100 up to ties.
+"""
+import numpy as np
+import pytest
+
+from oracle import maxsim_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-3
+ATOL = 1e-3
+
+
+def _mk(seed, M, K, dsub, Nq, B, Nd, normalize_q=True, dtype=np.float16):
+    rng = np.random.default_rng(seed)
+    C = rng.standard_normal((M, K, dsub), dtype=np.float32).astype(dtype)
+    Q = rng.standard_normal((Nq, M * dsub), dtype=np.float32)
+    if normalize_q:
+        Q /= np.linalg.norm(Q, axis=-1, keepdims=True) + 1e-12
+    Q = Q.astype(dtype)
+    codes = rng.integers(0, K, size=(B, Nd, M), dtype=np.uint8) if K <= 256 else None
+    return Q, C, codes
+
+
+def _gpu(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _check(got, ref, what):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    inf = np.isinf(ref)
+    assert np.array_equal(np.isinf(got), inf), what
+    np.testing.assert_allclose(got[~inf], ref[~inf], rtol=RTOL, atol=ATOL, err_msg=what)
+
+
+@pytest.mark.parametrize("method", ["mfma", "lut"])
+def test_reference_selftest_shape(cuda, method):
+    """The reference self-test shape (src/flash_pqsim_kernel.py:320-332)."""
+    from tilemaxsim_amd import TileMaxSimPQ
+    Q, C, codes = _mk(42, 16, 256, 8, 32, 8, 128, normalize_q=False)
+    pq = TileMaxSimPQ(_gpu(C))
+    got = pq.score_batch(_gpu(Q), _gpu(codes), method=method).cpu().numpy()
+    _check(got, orc.pq_decompress_score(Q, C, codes, f64=True), f"selftest {method}")
+    _check(got, orc.pq_score_lut(orc.pq_build_lut(Q, C), codes), f"selftest {method} vs lut oracle")
+
+
+def test_build_distance_table(cuda):
+    from tilemaxsim_amd import TileMaxSimPQ
+    Q, C, _ = _mk(1, 16, 256, 8, 32, 1, 1, normalize_q=False)
+    pq = TileMaxSimPQ(_gpu(C))
+    T = pq.build_distance_table(_gpu(Q)).cpu().numpy()
+    ref = np.einsum("qmj,mkj->qmk", Q.astype(np.float64).reshape(32, 16, 8), C.astype(np.float64))
+    assert T.shape == (32, 16, 256) and T.dtype == np.float32
+    np.testing.assert_allclose(T, ref, rtol=1e-5, atol=1e-5)
+
+
+SHAPES = [
+    # (M, K, dsub, Nq, B, Nd)
+    (16, 256, 8, 32, 200, 128), (16, 256, 8, 1, 50, 1), (16, 256, 8, 33, 60, 17), (16, 256, 8, 64, 40, 70),
+    (16, 256, 8, 100, 20, 33), (32, 256, 4, 32, 100, 40), (64, 256, 2, 32, 100, 40), (8, 256, 16, 32, 100, 40),
+    (4, 256, 32, 32, 100, 40), (8, 256, 8, 32, 100, 40), (12, 256, 8, 32, 100, 40), (4, 256, 8, 32, 100, 40),
+    (16, 16, 8, 32, 100, 40), (16, 100, 8, 20, 100, 50),
+]
+
+
+@pytest.mark.parametrize("method", ["auto", "lut"])
+@pytest.mark.parametrize("M,K,dsub,Nq,B,Nd", SHAPES)
+def test_pq_shapes(cuda, M, K, dsub, Nq, B, Nd, method):
+    from tilemaxsim_amd import TileMaxSimPQ
+    Q, C, codes = _mk(M * 1000 + K + dsub + Nq + B + Nd, M, K, dsub, Nq, B, Nd)
+    pq = TileMaxSimPQ(_gpu(C))
+    got = pq.score_batch(_gpu(Q), _gpu(codes), method=method).cpu().numpy()
+    _check(got, orc.pq_decompress_score(Q, C, codes, f64=True), f"M={M} K={K} dsub={dsub} Nq={Nq} {method}")
+
+
+@pytest.mark.parametrize("M,dsub", [(16, 3), (40, 4), (10, 8), (48, 8)])
+def test_pq_generic_shapes_take_lut_path(cuda, M, dsub):
+    from tilemaxsim_amd import TileMaxSimPQ
+    Q, C, codes = _mk(M + dsub, M, 64, dsub, 32, 50, 30)
+    pq = TileMaxSimPQ(_gpu(C))
+    got = pq.score_batch(_gpu(Q), _gpu(codes)).cpu().numpy()
+    _check(got, orc.pq_decompress_score(Q, C, codes, f64=True), f"generic M={M} dsub={dsub}")
+
+
+def test_pq_bf16_int_codes_and_single(cuda):
+    import torch
+    from tilemaxsim_amd import TileMaxSimPQ
+    rng = np.random.default_rng(8)
+    C = torch.from_numpy(rng.standard_normal((16, 256, 8), dtype=np.float32)).to(torch.bfloat16)
+    Q = torch.from_numpy(rng.standard_normal((32, 128), dtype=np.float32)).to(torch.bfloat16)
+    codes = rng.integers(0, 256, size=(30, 64, 16)).astype(np.int32)
+    pq = TileMaxSimPQ(C.cuda())
+    ref = orc.pq_decompress_score(Q.float().numpy(), C.float().numpy(), codes, f64=True)
+    for method in ("mfma", "lut"):
+        got = pq.score_batch(Q.cuda(), _gpu(codes), method=method).cpu().numpy()
+        _check(got, ref, f"bf16 {method}")
+    s = pq.score_single(Q.cuda(), _gpu(codes[4].astype(np.uint8)))
+    assert s.dim() == 0
+    _check(np.array([s.item()]), ref[4:5], "single")
+
+
+def test_pq_empty_and_invalid(cuda):
+    import torch
+    from tilemaxsim_amd import TileMaxSimPQ
+    Q, C, _ = _mk(3, 16, 256, 8, 32, 1, 1)
+    pq = TileMaxSimPQ(_gpu(C))
+    e = torch.empty(4, 0, 16, dtype=torch.uint8, device="cuda")
+    for method in ("mfma", "lut"):
+        assert np.all(np.isneginf(pq.score_batch(_gpu(Q), e, method=method).cpu().numpy()))
+    assert pq.score_batch(_gpu(Q), torch.empty(0, 5, 16, dtype=torch.uint8, device="cuda")).shape == (0,)
+    pq16 = TileMaxSimPQ(_gpu(C[:, :16]))
+    bad = torch.full((2, 3, 16), 20, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):
+        pq16.score_batch(_gpu(Q), bad)
+    with pytest.raises(AssertionError):
+        pq.score_batch(_gpu(Q), torch.zeros(2, 3, 8, dtype=torch.uint8, device="cuda"))
+
+
+def test_pq_methods_agree_and_rank(cuda):
+    """C5 shape at a bounded size: MFMA path vs table path (two algorithms) and the
+    float64 oracle; top-100 identical up to ties within tolerance."""
+    from tilemaxsim_amd import TileMaxSimPQ
+    Q, C, codes = _mk(5, 16, 256, 8, 32, 6000, 128)
+    pq = TileMaxSimPQ(_gpu(C))
+    a = pq.score_batch(_gpu(Q), _gpu(codes), method="mfma").cpu().numpy()
+    b = pq.score_batch(_gpu(Q), _gpu(codes), method="lut").cpu().numpy()
+    ref = orc.pq_decompress_score(Q, C, codes, f64=True)
+    _check(a, ref, "mfma")
+    _check(b, ref, "lut")
+    _check(a, b, "mfma vs lut")
+    kth = np.sort(ref)[::-1][99]
+    for got in (a, b):
+        diff = set(orc.topk(got, 100)[1].tolist()) ^ set(orc.topk(ref, 100)[1].tolist())
+        for i in diff:
+            assert abs(ref[i] - kth) <= RTOL * abs(kth) + ATOL

@@ -12,3 +12,6 @@ __all__ = [
     "flash_maxsim_v2_multiquery", "flash_maxsim_v2", "flash_maxsim_batched_queries",
     "flash_maxsim_single", "flash_maxsim_batch", "flash_maxsim_multi_doc", "maxsim_score",
 ]
+from .flash_pqsim_kernel import TileMaxSimPQ
+
+__all__.append("TileMaxSimPQ")

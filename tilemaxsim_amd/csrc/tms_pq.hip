@@ -1,0 +1,545 @@
+// Product-quantised (PQ / ADC) MaxSim on gfx950.
+//
+// Reference: src/flash_pqsim_kernel.py. Documents are (B, nd, M) uint8 codes into a
+// codebook (M, K, dsub); token t decodes to concat_m codebook[m, codes[t, m]].
+//   score[b] = sum_q max_t sum_m lut[q, m, codes[b, t, m]],
+//   lut[q, m, k] = sum_j Q[q, m*dsub + j] * codebook[m, k, j]          (:31-67, :127-173)
+// which equals MaxSim of Q against the decoded vectors (:283-313).
+//
+// Three kernels:
+//  * pq_build_lut_kernel  -- the fp32 distance table (TileMaxSimPQ.build_distance_table).
+//  * pq_lut_score_kernel  -- the reference algorithm: gathers from the fp32 table held
+//    in LDS (a slice of QG query tokens at a time), fp32 adds in ascending m.
+//    Any M, K <= 256, dsub. LDS-gather bound: 4 bytes of LDS per (token, q, m).
+//  * pq_mfma_score_kernel -- the fast path: the codebook (64 KiB at M=16, K=256,
+//    dsub=8, fp16) lives in LDS; each lane rebuilds its MFMA A-operand fragment
+//    (8 dims of one token) with one 16-byte LDS gather per (token, 8 dims), and the
+//    q . token dots run on MFMA with fp32 accumulation, exactly like the dense
+//    kernel. 256 bytes of LDS per token instead of the table's 2 KiB, and the
+//    decoded vectors never touch HBM.
+#include <string.h>
+
+#include "tms_common.h"
+
+namespace tms {
+
+template <int DT>
+__device__ __forceinline__ float elem_to_f32(uint16_t bits) {
+  if constexpr (DT == TMS_DTYPE_F16) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+  } else {
+    return __builtin_bit_cast(float, (uint32_t)bits << 16);
+  }
+}
+
+// ------------------------------------------------------------------------------
+// distance table
+// ------------------------------------------------------------------------------
+template <int DT>
+__global__ void __launch_bounds__(256) pq_build_lut_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ C,
+                                                           float* __restrict__ lut, int64_t total, int M, int K,
+                                                           int dsub) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int k = (int)(i % K);
+  const int m = (int)((i / K) % M);
+  const int64_t q = i / ((int64_t)K * M);
+  const uint16_t* qp = Q + (q * M + m) * dsub;
+  const uint16_t* cp = C + ((int64_t)m * K + k) * dsub;
+  float s = 0.f;
+  for (int j = 0; j < dsub; j++) s += elem_to_f32<DT>(qp[j]) * elem_to_f32<DT>(cp[j]);
+  lut[i] = s;
+}
+
+// ------------------------------------------------------------------------------
+// table-gather scoring (reference algorithm)
+// ------------------------------------------------------------------------------
+struct LutArgs {
+  const float* lut;      // (nq, M, K)
+  const uint8_t* codes;  // (B, nd, M)
+  float* out;            // (B)
+  int64_t B, nd;
+  int32_t nq, M, K;
+  int32_t docs_per_wave;  // <= 64
+};
+
+// LDS slice layout: [m][k][QG] fp32 for query tokens q0 .. q0+QG-1 (zero past nq).
+template <int QG>
+__global__ void __launch_bounds__(256) pq_lut_score_kernel(LutArgs a) {
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t b_begin = wave * a.docs_per_wave;
+  const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
+  const int64_t MK = (int64_t)a.M * a.K;
+  const float NEG_INF = -__builtin_inff();
+
+  float partial = 0.f;  // lane j: running score of document b_begin + j
+  for (int q0 = 0; q0 < a.nq; q0 += QG) {
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < MK * QG; i += blockDim.x) {
+      const int qq = (int)(i % QG);
+      const int64_t mk = i / QG;
+      const int q = q0 + qq;
+      lds[i] = (q < a.nq) ? a.lut[(int64_t)q * MK + mk] : 0.f;
+    }
+    __syncthreads();
+    if (b_begin >= a.B) continue;
+    for (int64_t b = b_begin; b < b_end; b++) {
+      float mx[QG];
+#pragma unroll
+      for (int j = 0; j < QG; j++) mx[j] = NEG_INF;
+      for (int64_t t0 = 0; t0 < a.nd; t0 += 64) {
+        int64_t t = t0 + lane;
+        if (t > a.nd - 1) t = a.nd - 1;  // duplicate of the last token: max unchanged
+        const uint8_t* cp = a.codes + (b * a.nd + t) * a.M;
+        float s[QG];
+#pragma unroll
+        for (int j = 0; j < QG; j++) s[j] = 0.f;
+        for (int m = 0; m < a.M; m++) {
+          const int code = min((int)cp[m], a.K - 1);
+          const float* row = lds + ((int64_t)m * a.K + code) * QG;
+#pragma unroll
+          for (int j = 0; j < QG; j++) s[j] += row[j];
+        }
+#pragma unroll
+        for (int j = 0; j < QG; j++) mx[j] = fmaxf(mx[j], s[j]);
+      }
+      float tot = 0.f;
+#pragma unroll
+      for (int j = 0; j < QG; j++) {
+        float v = mx[j];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+        tot += (q0 + j < a.nq) ? v : 0.f;
+      }
+      if (a.nd == 0) tot = NEG_INF;
+      if (lane == (int)(b - b_begin)) partial += tot;
+    }
+  }
+  if (b_begin < a.B && lane < b_end - b_begin) a.out[b_begin + lane] = partial;
+}
+
+// ------------------------------------------------------------------------------
+// codebook-gather + MFMA scoring (fast path)
+// ------------------------------------------------------------------------------
+struct PqArgs {
+  const uint8_t* Q;         // (nq, d) elements of the input dtype
+  const uint8_t* codebook;  // (M, K, DSUB)
+  const uint8_t* codes;     // (B, nd, M)
+  float* out;               // (B)
+  int64_t B, nd;
+  int32_t nq, nbq, blk0, nblk, K;
+  int32_t docs_per_wave;
+};
+
+// Lane (r = l%16, g = l/16) owns chunks c = g*KS + s (s < KS) of every token, i.e.
+// dims [8*g*KS, 8*(g+1)*KS): a contiguous run of CB = 8*KS/DSUB subspaces whose
+// codes are CB contiguous bytes of the token's code row.
+constexpr int kPqThreads = 512;  // 8 waves: two workgroups per CU next to a 64 KiB codebook
+
+template <int DT, int DSUB, int KS, int NQB, int UT>
+__global__ void __launch_bounds__(kPqThreads) pq_mfma_score_kernel(PqArgs a) {
+  constexpr int D = 32 * KS;
+  constexpr int M = D / DSUB;
+  constexpr int CB = M / 4;                  // code bytes per lane per token
+  constexpr int CW = (CB + 3) / 4;           // ... in 32-bit words
+  extern __shared__ u32x4 cb_lds[];          // codebook, M*K*DSUB elements
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int K = a.K;
+
+  {  // codebook -> LDS (16-byte units; M*K*DSUB*2 is a multiple of 16 since D % 32 == 0)
+    const int64_t n16 = (int64_t)M * K * DSUB * 2 / 16;
+    const u32x4* src = (const u32x4*)a.codebook;
+    for (int64_t i = threadIdx.x; i < n16; i += blockDim.x) cb_lds[i] = src[i];
+  }
+
+  // Query fragments: block j, half h, step s -> row token 16h + r, chunk g*KS + s.
+  auto q_row = [&](int j, int h, int rr, bool& valid) -> int64_t {
+    int jb = a.blk0 + j;
+    int tok = jb * 32 + 16 * h + rr;
+    valid = (j < a.nblk) && (tok < a.nq);
+    return tok;
+  };
+  u32x4 qf[NQB][KS][2];
+#pragma unroll
+  for (int j = 0; j < NQB; j++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      bool valid;
+      int64_t row = q_row(j, h, r, valid);
+#pragma unroll
+      for (int s = 0; s < KS; s++)
+        qf[j][s][h] = valid ? *(const u32x4*)(a.Q + (row * D + 8 * (g * KS + s)) * 2) : u32x4{0u, 0u, 0u, 0u};
+    }
+  __syncthreads();
+
+  const int64_t wave = (int64_t)blockIdx.x * (kPqThreads / 64) + (threadIdx.x >> 6);
+  const int64_t b_begin = wave * a.docs_per_wave;
+  if (b_begin >= a.B) return;
+  const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
+  const float NEG_INF = -__builtin_inff();
+  const int64_t nd = a.nd;
+
+  f32x4 rmax[NQB][2];
+#pragma unroll
+  for (int j = 0; j < NQB; j++) rmax[j][0] = rmax[j][1] = f32x4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+
+  auto write_doc = [&](int64_t b, float s_total) {
+    if (lane == 0) {
+      float* o = a.out + b;
+      *o = (a.blk0 > 0) ? (*o + s_total) : s_total;
+    }
+  };
+  auto finish_doc = [&](int64_t b) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NQB; j++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        float m = fmaxf(fmaxf(rmax[j][h][0], rmax[j][h][1]), fmaxf(rmax[j][h][2], rmax[j][h][3]));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        bool valid;
+        (void)q_row(j, h, r, valid);
+        s += valid ? m : 0.f;
+        rmax[j][h] = f32x4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+      }
+    s += __shfl_xor(s, 8);
+    s += __shfl_xor(s, 4);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 1);
+    write_doc(b, s);
+  };
+
+  // Code words of this lane for UT subtiles of 16 tokens starting at token t0 of doc b.
+  struct Codes {
+    uint32_t w[UT][CW];
+  };
+  auto load_codes = [&](Codes& c, int64_t b, int64_t t0) {
+#pragma unroll
+    for (int u = 0; u < UT; u++) {
+      int64_t t = t0 + 16 * u + r;
+      if (t > nd - 1) t = nd - 1;
+      const uint8_t* p = a.codes + (b * nd + t) * M + g * CB;
+      if constexpr (CB == 4) {
+        c.w[u][0] = *(const uint32_t*)p;
+      } else if constexpr (CB == 8) {
+        uint2 v = *(const uint2*)p;
+        c.w[u][0] = v.x;
+        c.w[u][1] = v.y;
+      } else if constexpr (CB == 16) {
+        uint4 v = *(const uint4*)p;
+        c.w[u][0] = v.x;
+        c.w[u][1] = v.y;
+        c.w[u][2] = v.z;
+        c.w[u][3] = v.w;
+      } else if constexpr (CB == 2) {
+        c.w[u][0] = *(const uint16_t*)p;
+      } else {
+#pragma unroll
+        for (int i = 0; i < CW; i++) c.w[u][i] = 0;
+#pragma unroll
+        for (int i = 0; i < CB; i++) c.w[u][i / 4] |= (uint32_t)p[i] << (8 * (i % 4));
+      }
+    }
+  };
+  // codes >= K (invalid input) are clamped so the gather stays inside the table
+  auto code_byte = [&](const Codes& c, int u, int i) -> uint32_t {
+    return min((c.w[u][i / 4] >> (8 * (i % 4))) & 0xffu, (uint32_t)(K - 1));
+  };
+
+  // Decoded A fragment for chunk g*KS + s of the token held in subtile u.
+  auto gather = [&](const Codes& c, int u, int s) -> u32x4 {
+    const int cidx = g * KS + s;
+    if constexpr (DSUB >= 8) {
+      constexpr int P = DSUB / 8;  // 16-byte pieces per sub-vector
+      const int m = cidx / P;
+      const uint32_t code = code_byte(c, u, s / P);
+      return cb_lds[((int64_t)m * K + code) * P + (cidx % P)];
+    } else {
+      constexpr int P = 8 / DSUB;  // sub-vectors per chunk
+      u32x4 v;
+      if constexpr (DSUB == 4) {
+        const uint2* cb8 = (const uint2*)cb_lds;
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+          const int m = cidx * P + p;
+          uint2 x = cb8[(int64_t)m * K + code_byte(c, u, s * P + p)];
+          v[2 * p] = x.x;
+          v[2 * p + 1] = x.y;
+        }
+      } else {  // DSUB == 2
+        const uint32_t* cb4 = (const uint32_t*)cb_lds;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+          const int m = cidx * P + p;
+          v[p] = cb4[(int64_t)m * K + code_byte(c, u, s * P + p)];
+        }
+      }
+      return v;
+    }
+  };
+
+  auto compute = [&](const Codes& c, int64_t t0) {
+#pragma unroll
+    for (int u = 0; u < UT; u++) {
+      if (t0 + 16 * u >= nd) break;  // whole subtile past the document (uniform)
+      u32x4 fr[KS];
+#pragma unroll
+      for (int s = 0; s < KS; s++) fr[s] = gather(c, u, s);
+#pragma unroll
+      for (int j = 0; j < NQB; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < KS; s++) acc = mfma16x16x32<DT>(fr[s], qf[j][s][h], acc);
+#pragma unroll
+          for (int i = 0; i < 4; i++) rmax[j][h][i] = fmaxf(rmax[j][h][i], acc[i]);
+        }
+    }
+  };
+
+  if (nd == 0) {
+    for (int64_t b = b_begin; b < b_end; b++) write_doc(b, NEG_INF);
+    return;
+  }
+  constexpr int TT = 16 * UT;
+  // Pipeline over (doc, t0) units of TT tokens: codes of the next unit are in flight
+  // while the current unit is decoded and scored.
+  int64_t cb = b_begin, ct = 0;
+  Codes c0, c1;
+  load_codes(c0, cb, ct);
+  auto step = [&](int64_t& b, int64_t& t) {
+    t += TT;
+    if (t >= nd) {
+      t = 0;
+      b++;
+    }
+  };
+  while (true) {
+    int64_t nb = cb, nt = ct;
+    step(nb, nt);
+    if (nb < b_end) load_codes(c1, nb, nt);
+    compute(c0, ct);
+    if (ct + TT >= nd) finish_doc(cb);
+    if (nb >= b_end) break;
+    cb = nb;
+    ct = nt;
+    step(nb, nt);
+    if (nb < b_end) load_codes(c0, nb, nt);
+    compute(c1, ct);
+    if (ct + TT >= nd) finish_doc(cb);
+    if (nb >= b_end) break;
+    cb = nb;
+    ct = nt;
+  }
+}
+
+// ------------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------------
+template <int DT>
+static int build_lut(const void* Q, int64_t nq, const void* C, int64_t M, int64_t K, int64_t dsub, float* lut,
+                     hipStream_t st) {
+  const int64_t total = nq * M * K;
+  if (total == 0) return TMS_OK;
+  const int64_t grid = (total + 255) / 256;
+  hipLaunchKernelGGL(pq_build_lut_kernel<DT>, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
+                     (const uint16_t*)C, lut, total, (int)M, (int)K, (int)dsub);
+  return check_launch("pq_build_lut_kernel");
+}
+
+static int fill_scores(float* out, int64_t n, float v, hipStream_t st);
+
+template <int QG>
+static int launch_lut_score(const LutArgs& a, hipStream_t st) {
+  const int64_t waves = (a.B + a.docs_per_wave - 1) / a.docs_per_wave;
+  const int64_t grid = (waves + 3) / 4;
+  const size_t lds = (size_t)a.M * a.K * QG * 4;
+  hipLaunchKernelGGL(pq_lut_score_kernel<QG>, dim3((unsigned)grid), dim3(256), lds, st, a);
+  return check_launch("pq_lut_score_kernel");
+}
+
+constexpr int kPqUT = 4;
+
+template <int DT, int DSUB, int KS, int NQB>
+static int launch_mfma_one(const PqArgs& a, int64_t grid, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((pq_mfma_score_kernel<DT, DSUB, KS, NQB, kPqUT>), dim3((unsigned)grid), dim3(kPqThreads), lds, st,
+                     a);
+  return check_launch("pq_mfma_score_kernel");
+}
+
+template <int DT, int DSUB, int KS>
+static int launch_mfma_nqb(const PqArgs& a, int64_t grid, size_t lds, hipStream_t st) {
+  if (a.nblk == 2) return launch_mfma_one<DT, DSUB, KS, 2>(a, grid, lds, st);
+  return launch_mfma_one<DT, DSUB, KS, 1>(a, grid, lds, st);
+}
+
+template <int DT, int DSUB>
+static int launch_mfma_ks(const PqArgs& a, int ks, int64_t grid, size_t lds, hipStream_t st) {
+  switch (ks) {
+    case 1: return launch_mfma_nqb<DT, DSUB, 1>(a, grid, lds, st);
+    case 2: return launch_mfma_nqb<DT, DSUB, 2>(a, grid, lds, st);
+    case 3: return launch_mfma_nqb<DT, DSUB, 3>(a, grid, lds, st);
+    default: return launch_mfma_nqb<DT, DSUB, 4>(a, grid, lds, st);
+  }
+}
+
+template <int DT>
+static int launch_mfma_dsub(const PqArgs& a, int dsub, int ks, int64_t grid, size_t lds, hipStream_t st) {
+  switch (dsub) {
+    case 2: return launch_mfma_ks<DT, 2>(a, ks, grid, lds, st);
+    case 4: return launch_mfma_ks<DT, 4>(a, ks, grid, lds, st);
+    case 8: return launch_mfma_ks<DT, 8>(a, ks, grid, lds, st);
+    case 16: return launch_mfma_ks<DT, 16>(a, ks, grid, lds, st);
+    default: return launch_mfma_ks<DT, 32>(a, ks, grid, lds, st);
+  }
+}
+
+// The fast kernel needs: d = M*dsub in {32, 64, 96, 128}, dsub in {2, 4, 8, 16, 32}
+// with M a multiple of 4, K <= 256, a codebook that fits 64 KiB of LDS, and
+// 16-byte aligned Q / codebook / code rows.
+static bool mfma_supported(const void* Q, const void* C, const uint8_t* codes, int64_t M, int64_t K, int64_t dsub) {
+  const int64_t d = M * dsub;
+  if (!(dsub == 2 || dsub == 4 || dsub == 8 || dsub == 16 || dsub == 32)) return false;
+  if (d % 32 != 0 || d > 128 || d == 0 || M % 4 != 0) return false;
+  if (K > 256 || K < 1 || d * K * 2 > 64 * 1024) return false;
+  if (((uintptr_t)Q & 15) || ((uintptr_t)C & 15) || ((uintptr_t)codes & 15)) return false;
+  return true;
+}
+
+static int score_lut(const float* lut, int64_t nq, int64_t M, int64_t K, const uint8_t* codes, int64_t B, int64_t nd,
+                     float* out, hipStream_t st) {
+  LutArgs a;
+  memset(&a, 0, sizeof(a));
+  a.lut = lut;
+  a.codes = codes;
+  a.out = out;
+  a.B = B;
+  a.nd = nd;
+  a.nq = (int32_t)nq;
+  a.M = (int32_t)M;
+  a.K = (int32_t)K;
+  a.docs_per_wave = 64;
+  if (B < 256 * 4 * 64) a.docs_per_wave = (int32_t)((B + 1023) / 1024 > 0 ? (B + 1023) / 1024 : 1);
+  if (a.docs_per_wave > 64) a.docs_per_wave = 64;
+  const int64_t mk = M * K;
+  if (mk * 4 * 4 <= 64 * 1024) return launch_lut_score<4>(a, st);
+  if (mk * 2 * 4 <= 64 * 1024) return launch_lut_score<2>(a, st);
+  return launch_lut_score<1>(a, st);
+}
+
+}  // namespace tms
+
+using namespace tms;
+
+static int pq_common_checks(const char* fn, int64_t nq, int64_t M, int64_t K, int64_t dsub, int64_t B, int64_t nd) {
+  if (nq < 0 || M < 0 || K < 0 || dsub < 0 || B < 0 || nd < 0)
+    return fail(TMS_ERR_INVALID, "%s: negative size", fn);
+  if (K > 256) return fail(TMS_ERR_UNSUPPORTED, "%s: K=%lld > 256 does not fit uint8 codes", fn, (long long)K);
+  return TMS_OK;
+}
+
+extern "C" {
+
+int tms_pq_build_lut(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
+                     float* lut, void* stream) {
+  const char* fn = "tms_pq_build_lut";
+  if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16) return fail(TMS_ERR_UNSUPPORTED, "%s: unsupported dtype %d", fn, dtype);
+  if (nq < 0 || M < 0 || K < 0 || dsub < 0) return fail(TMS_ERR_INVALID, "%s: negative size", fn);
+  if (nq * M * K == 0) return TMS_OK;
+  if (!Q || !codebook || !lut) return fail(TMS_ERR_INVALID, "%s: NULL pointer", fn);
+  if (nq * M * K > ((int64_t)1 << 40)) return fail(TMS_ERR_UNSUPPORTED, "%s: table too large", fn);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == TMS_DTYPE_F16) return build_lut<TMS_DTYPE_F16>(Q, nq, codebook, M, K, dsub, lut, st);
+  return build_lut<TMS_DTYPE_BF16>(Q, nq, codebook, M, K, dsub, lut, st);
+}
+
+int tms_pq_score_lut(const float* lut, int64_t nq, int64_t M, int64_t K, const uint8_t* codes, int64_t B, int64_t nd,
+                     float* out, void* stream) {
+  const char* fn = "tms_pq_score_lut";
+  int rc = pq_common_checks(fn, nq, M, K, 1, B, nd);
+  if (rc) return rc;
+  if (B == 0) return TMS_OK;
+  if (!out) return fail(TMS_ERR_INVALID, "%s: out is NULL", fn);
+  if (nd > 0 && M > 0 && !codes) return fail(TMS_ERR_INVALID, "%s: codes is NULL", fn);
+  if (nq > 0 && M > 0 && K > 0 && !lut) return fail(TMS_ERR_INVALID, "%s: lut is NULL", fn);
+  if (M * K > 16384) return fail(TMS_ERR_UNSUPPORTED, "%s: M*K=%lld > 16384 does not fit LDS", fn, (long long)(M * K));
+  if (M == 0 || K == 0) return fail(TMS_ERR_UNSUPPORTED, "%s: M and K must be positive", fn);
+  hipStream_t st = (hipStream_t)stream;
+  return score_lut(lut, nq, M, K, codes, B, nd, out, st);
+}
+
+int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
+                 const uint8_t* codes, int64_t B, int64_t nd, float* out, void* stream) {
+  const char* fn = "tms_pq_score";
+  if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16) return fail(TMS_ERR_UNSUPPORTED, "%s: unsupported dtype %d", fn, dtype);
+  int rc = pq_common_checks(fn, nq, M, K, dsub, B, nd);
+  if (rc) return rc;
+  if (B == 0) return TMS_OK;
+  if (!out) return fail(TMS_ERR_INVALID, "%s: out is NULL", fn);
+  if (nd > 0 && M > 0 && !codes) return fail(TMS_ERR_INVALID, "%s: codes is NULL", fn);
+  if (nq > 0 && (!Q || !codebook)) return fail(TMS_ERR_INVALID, "%s: Q or codebook is NULL", fn);
+  if (M == 0 || K == 0 || dsub == 0) return fail(TMS_ERR_UNSUPPORTED, "%s: M, K and dsub must be positive", fn);
+  hipStream_t st = (hipStream_t)stream;
+  // no query tokens: 0; no document tokens: -inf (the running max never moves)
+  if (nq == 0 || nd == 0) return fill_scores(out, B, nq == 0 ? 0.f : -__builtin_inff(), st);
+  if (mfma_supported(Q, codebook, codes, M, K, dsub)) {
+    PqArgs a;
+    memset(&a, 0, sizeof(a));
+    a.Q = (const uint8_t*)Q;
+    a.codebook = (const uint8_t*)codebook;
+    a.codes = codes;
+    a.out = out;
+    a.B = B;
+    a.nd = nd;
+    a.nq = (int32_t)nq;
+    a.nbq = (int32_t)((nq + 31) / 32);
+    a.K = (int32_t)K;
+    const int64_t d = M * dsub;
+    const int ks = (int)(d / 32);
+    // Two 8-wave workgroups per CU fit next to a 64 KiB codebook; each wave gets a long
+    // run of documents (about four rounds of the chip) so the per-workgroup codebook
+    // load is amortised and the last round stays short.
+    const int64_t waves_per_wg = kPqThreads / 64;
+    const int64_t target_waves = 256 * 2 * waves_per_wg * 4;
+    int64_t dpw = (B + target_waves - 1) / target_waves;
+    if (dpw < 1) dpw = 1;
+    a.docs_per_wave = (int32_t)dpw;
+    const int64_t waves = (B + dpw - 1) / dpw;
+    const int64_t grid = (waves + waves_per_wg - 1) / waves_per_wg;
+    const size_t lds = (size_t)d * K * 2;
+    for (int64_t blk0 = 0; blk0 < a.nbq; blk0 += 2) {
+      a.blk0 = (int32_t)blk0;
+      a.nblk = (int32_t)((a.nbq - blk0 < 2) ? a.nbq - blk0 : 2);
+      if (dtype == TMS_DTYPE_F16) rc = launch_mfma_dsub<TMS_DTYPE_F16>(a, (int)dsub, ks, grid, lds, st);
+      else rc = launch_mfma_dsub<TMS_DTYPE_BF16>(a, (int)dsub, ks, grid, lds, st);
+      if (rc) return rc;
+    }
+    return TMS_OK;
+  }
+  // Other shapes go through tms_pq_build_lut + tms_pq_score_lut: the table needs
+  // storage this allocation-free entry point cannot own, so the host wrapper
+  // allocates it and picks that path.
+  return fail(TMS_ERR_UNSUPPORTED,
+              "%s: shape M=%lld K=%lld dsub=%lld (or alignment) not supported by the MFMA kernel; "
+              "use tms_pq_build_lut + tms_pq_score_lut",
+              fn, (long long)M, (long long)K, (long long)dsub);
+}
+
+}  // extern "C"
+
+namespace tms {
+__global__ void pq_fill_kernel(float* out, int64_t n, float v) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = v;
+}
+static int fill_scores(float* out, int64_t n, float v, hipStream_t st) {
+  if (n <= 0) return TMS_OK;
+  hipLaunchKernelGGL(pq_fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, n, v);
+  return check_launch("pq_fill_kernel");
+}
+}  // namespace tms

@@ -1,0 +1,127 @@
+"""PQ / ADC MaxSim -- drop-in for ``TileMaxSimPQ`` of the reference module
+``src/flash_pqsim_kernel.py``.
+
+``build_distance_table`` runs ``tms_pq_build_lut``. ``score_batch`` runs the
+codebook-gather MFMA kernel (``tms_pq_score``) whenever the shape allows it and the
+reference's table-gather algorithm (``tms_pq_build_lut`` + ``tms_pq_score_lut``)
+otherwise; ``method=`` forces either one. Codes are read as uint8 in place (the
+reference makes an int32 copy of them first).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _check, _lib
+
+
+def _mfma_shape_ok(M: int, K: int, dsub: int) -> bool:
+    d = M * dsub
+    return (dsub in (2, 4, 8, 16, 32) and d % 32 == 0 and 0 < d <= 128 and M % 4 == 0
+            and 1 <= K <= 256 and d * K * 2 <= 64 * 1024)
+
+
+class TileMaxSimPQ:
+    """High-level PQ MaxSim scorer (``src/flash_pqsim_kernel.py:176-280``).
+
+    Args:
+        codebook: (M, K, dsub) PQ centroids, float16 or bfloat16, on the GPU.
+    """
+
+    def __init__(self, codebook: torch.Tensor):
+        _check.on_gpu("codebook", codebook)
+        if codebook.dim() != 3:
+            raise ValueError(f"codebook must be (M, K, dsub), got shape {tuple(codebook.shape)}")
+        _check.embedding_dtype("codebook", codebook)
+        self.codebook = codebook.contiguous()
+        self.M, self.K, self.dsub = codebook.shape
+        self.d = self.M * self.dsub
+        if self.K > 256:
+            raise NotImplementedError(f"K={self.K} > 256 centroids does not fit uint8 codes")
+
+    def _query(self, Q: torch.Tensor) -> torch.Tensor:
+        _check.on_gpu("Q", Q)
+        if Q.dim() != 2:
+            raise ValueError(f"Q must be (Nq, d), got shape {tuple(Q.shape)}")
+        assert Q.shape[1] == self.d, f"Q width {Q.shape[1]} != M*dsub = {self.d}"
+        _check.same_device(Q=Q, codebook=self.codebook)
+        return _check.query_like(Q, self.codebook.dtype)
+
+    def _codes(self, codes: torch.Tensor, validate: bool) -> torch.Tensor:
+        _check.on_gpu("codes", codes)
+        _check.same_device(codes=codes, codebook=self.codebook)
+        if codes.dtype.is_floating_point or codes.dtype == torch.bool:
+            raise TypeError(f"codes must be an integer tensor, got {codes.dtype}")
+        if validate and codes.numel() > 0 and (codes.dtype != torch.uint8 or self.K < 256):
+            lo, hi = int(codes.min()), int(codes.max())
+            if lo < 0 or hi >= self.K:
+                raise ValueError(f"codes must lie in [0, K={self.K}), found [{lo}, {hi}]")
+        if codes.dtype != torch.uint8:
+            codes = codes.to(torch.uint8)
+        return codes.contiguous()
+
+    def build_distance_table(self, Q: torch.Tensor) -> torch.Tensor:
+        """Query-centroid table ``T[q, m, k] = Q[q, m*dsub:(m+1)*dsub] . C[m, k]`` in fp32
+        (``src/flash_pqsim_kernel.py:190-211``). Returns (Nq, M, K) float32."""
+        Q = self._query(Q)
+        Nq = Q.shape[0]
+        table = torch.empty(Nq, self.M, self.K, dtype=torch.float32, device=Q.device)
+        if table.numel() == 0:
+            return table
+        lib = _lib.load()
+        with torch.cuda.device(Q.device):
+            _lib.check(lib.tms_pq_build_lut(Q.data_ptr(), Nq, self.codebook.data_ptr(), self.M, self.K, self.dsub,
+                                            _lib.dtype_code(self.codebook.dtype), table.data_ptr(),
+                                            _lib.stream_of(Q)))
+        return table
+
+    def score_batch(self, Q: torch.Tensor, codes: torch.Tensor, method: str = "auto",
+                    validate: bool = True) -> torch.Tensor:
+        """Score a batch of PQ-compressed documents against a query
+        (``src/flash_pqsim_kernel.py:213-252``).
+
+        Args:
+            Q: (Nq, d) query embeddings.
+            codes: (B, Nd, M) PQ codes (uint8, or any integer dtype with values < K).
+            method: "auto" (MFMA kernel when the shape allows it), "mfma" or "lut".
+            validate: check that codes lie in [0, K) (one device-to-host copy; skipped
+                for uint8 codes when K == 256, where every byte is valid).
+
+        Returns:
+            (B,) float32 MaxSim scores; a document with Nd == 0 scores -inf.
+        """
+        if codes.dim() != 3:
+            raise ValueError(f"codes must be (B, Nd, M), got shape {tuple(codes.shape)}")
+        B, Nd, M = codes.shape
+        assert M == self.M, f"codes have M={M} subspaces, codebook has {self.M}"
+        Q = self._query(Q)
+        codes = self._codes(codes, validate)
+        Nq = Q.shape[0]
+        scores = torch.empty(B, dtype=torch.float32, device=Q.device)
+        if B == 0:
+            return scores
+        if method not in ("auto", "mfma", "lut"):
+            raise ValueError(f"method must be 'auto', 'mfma' or 'lut', got {method!r}")
+        aligned = all(t.data_ptr() % 16 == 0 for t in (Q, self.codebook, codes))
+        use_mfma = method == "mfma" or (method == "auto" and _mfma_shape_ok(self.M, self.K, self.dsub) and aligned)
+        lib = _lib.load()
+        with torch.cuda.device(Q.device):
+            stream = _lib.stream_of(Q)
+            if use_mfma:
+                _lib.check(lib.tms_pq_score(Q.data_ptr(), Nq, self.codebook.data_ptr(), self.M, self.K, self.dsub,
+                                            _lib.dtype_code(self.codebook.dtype), codes.data_ptr(), B, Nd,
+                                            scores.data_ptr(), stream))
+            else:
+                table = self.build_distance_table(Q)
+                _lib.check(lib.tms_pq_score_lut(table.data_ptr(), Nq, self.M, self.K, codes.data_ptr(), B, Nd,
+                                                scores.data_ptr(), stream))
+        return scores
+
+    def score_single(self, Q: torch.Tensor, codes: torch.Tensor, method: str = "auto") -> torch.Tensor:
+        """Score one PQ-compressed document (``src/flash_pqsim_kernel.py:254-280``).
+
+        Args:
+            Q: (Nq, d); codes: (Nd, M). Returns a 0-d float32 tensor.
+        """
+        if codes.dim() != 2:
+            raise ValueError(f"codes must be (Nd, M), got shape {tuple(codes.shape)}")
+        return self.score_batch(Q, codes.unsqueeze(0), method=method).reshape(())
