@@ -1,0 +1,63 @@
+"""Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
+
+CPU: the oracle still reproduces every fixture (and the C restatement agrees).
+GPU: every HIP entry point reproduces the fixture scores to the BASELINE tolerance.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import c_oracle
+from oracle import maxsim_oracle as orc
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _load(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+def test_fixtures_reproduce_on_cpu():
+    f = _load("dense_d128.npz")
+    np.testing.assert_allclose(orc.maxsim_f64(f["Q"], f["D"]), f["scores"], rtol=1e-12)
+    np.testing.assert_allclose(c_oracle.maxsim_dense(f["Q"], f["D"]), f["scores"], rtol=1e-12)
+    f = _load("dense_d256.npz")
+    np.testing.assert_allclose(orc.maxsim_f64(f["Q"], f["D"]), f["scores"], rtol=1e-12)
+    f = _load("varlen_d64.npz")
+    got = orc.maxsim_varlen(f["Q"], f["D_flat"], f["offsets"], f64=True)
+    np.testing.assert_allclose(got, f["scores"], rtol=1e-12)
+    np.testing.assert_allclose(c_oracle.maxsim_varlen(f["Q"], f["D_flat"], f["offsets"]), f["scores"], rtol=1e-12)
+    f = _load("masked_d128.npz")
+    np.testing.assert_allclose(orc.maxsim_masked(f["Q"], f["D"], f["mask"], f64=True), f["scores"], rtol=1e-12)
+    f = _load("pq_m16_k256.npz")
+    np.testing.assert_allclose(orc.pq_decompress_score(f["Q"], f["codebook"], f["codes"], f64=True), f["scores"],
+                               rtol=1e-12)
+    np.testing.assert_allclose(orc.pq_build_lut(f["Q"], f["codebook"])[:2], f["lut_q01"], rtol=1e-5, atol=1e-6)
+
+
+def _close(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    inf = np.isinf(ref)
+    assert np.array_equal(np.isinf(got), inf)
+    np.testing.assert_allclose(got[~inf], ref[~inf], rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.gpu
+def test_fixtures_on_gpu(cuda):
+    import torch
+    import tilemaxsim_amd as tms
+    g = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    for name in ("dense_d128.npz", "dense_d256.npz"):
+        f = _load(name)
+        _close(tms.flash_maxsim_v2_multiquery(g(f["Q"]), g(f["D"])).cpu().numpy(), f["scores"])
+    f = _load("varlen_d64.npz")
+    _close(tms.flash_maxsim_multi_doc(g(f["Q"]), g(f["D_flat"]), g(f["offsets"])).cpu().numpy(), f["scores"])
+    f = _load("masked_d128.npz")
+    _close(tms.maxsim_score(g(f["Q"]), g(f["D"]), g(f["mask"])).cpu().numpy(), f["scores"])
+    f = _load("pq_m16_k256.npz")
+    pq = tms.TileMaxSimPQ(g(f["codebook"]))
+    for method in ("mfma", "lut"):
+        _close(pq.score_batch(g(f["Q"]), g(f["codes"]), method=method).cpu().numpy(), f["scores"])
+    lut = pq.build_distance_table(g(f["Q"])).cpu().numpy()
+    np.testing.assert_allclose(lut[:2], f["lut_q01"], rtol=1e-5, atol=1e-5)

@@ -1,0 +1,126 @@
+"""CPU tests of the host layer: the C ABI library loads and exports every declared
+symbol, argument errors surface before any HIP call (Python and C side), and the
+package has no CPU fallback."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "tilemaxsim.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tms_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from tilemaxsim_amd import _lib
+    lib = _lib.load()
+    declared = _declared_symbols()
+    assert "tms_maxsim_dense" in declared and "tms_pq_score" in declared
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, f"declared in include/tilemaxsim.h but not exported: {missing}"
+    bound = set(_lib.SIGNATURES) | {"tms_last_error"}
+    assert set(declared) == bound, "ctypes signatures out of sync with the header"
+    assert lib.tms_version() >= 100
+
+
+def test_library_is_built_for_gfx950():
+    from tilemaxsim_amd import _lib
+    blob = open(_lib.LIB_PATH, "rb").read()
+    assert b"gfx950" in blob
+
+
+def _c_call(name, *args):
+    from tilemaxsim_amd import _lib
+    lib = _lib.load()
+    rc = getattr(lib, name)(*args)
+    return rc, lib.tms_last_error().decode()
+
+
+def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
+    # negative sizes
+    rc, msg = _c_call("tms_maxsim_dense", None, -1, 128, None, 10, 5, 0, None, None)
+    assert rc == 1 and "negative" in msg
+    # unknown dtype
+    rc, msg = _c_call("tms_maxsim_dense", None, 32, 128, None, 10, 5, 7, None, None)
+    assert rc == 2 and "dtype" in msg
+    # NULL output with work to do
+    rc, msg = _c_call("tms_maxsim_dense", 16, 32, 128, 16, 10, 5, 0, None, None)
+    assert rc == 1 and "out" in msg
+    # empty batch: nothing to do, success, no HIP call
+    rc, _ = _c_call("tms_maxsim_dense", None, 32, 128, None, 0, 5, 0, None, None)
+    assert rc == 0
+    # d beyond the supported width
+    rc, msg = _c_call("tms_maxsim_dense", 16, 32, 4096, 16, 10, 5, 0, 16, None)
+    assert rc == 2 and "1024" in msg
+    # varlen without offsets
+    rc, msg = _c_call("tms_maxsim_varlen", 16, 32, 128, 16, 100, None, 10, 0, 16, None)
+    assert rc == 1 and "offsets" in msg
+    # masked without a mask
+    rc, msg = _c_call("tms_maxsim_masked", 16, 32, 128, 16, None, 10, 5, 0, 16, None)
+    assert rc == 1 and "mask" in msg
+    # PQ: K beyond uint8 codes, unsupported MFMA shape
+    rc, msg = _c_call("tms_pq_score", 16, 32, 16, 16, 300, 8, 0, 16, 10, 5, 16, None)
+    assert rc == 2 and "256" in msg
+    rc, msg = _c_call("tms_pq_score", 16, 32, 16, 16, 256, 3, 0, 16, 10, 5, 16, None)
+    assert rc == 2 and "tms_pq_score_lut" in msg
+    rc, msg = _c_call("tms_pq_score_lut", 16, 32, 1000, 256, 16, 10, 5, 16, None)
+    assert rc == 2 and "LDS" in msg
+
+
+def test_python_errors_before_device_checks():
+    from tilemaxsim_amd import (TileMaxSimPQ, flash_maxsim_multi_doc, flash_maxsim_single,
+                                flash_maxsim_v2_multiquery, maxsim_score)
+    Q = torch.zeros(32, 128, dtype=torch.float16)
+    D = torch.zeros(4, 10, 128, dtype=torch.float16)
+    with pytest.raises(TypeError):
+        flash_maxsim_v2_multiquery(np.zeros((32, 128)), D)
+    with pytest.raises(ValueError):
+        flash_maxsim_v2_multiquery(Q, D[0])
+    with pytest.raises(AssertionError):
+        flash_maxsim_v2_multiquery(Q[:, :64], D)
+    with pytest.raises(TypeError):
+        flash_maxsim_v2_multiquery(Q, D.float())
+    with pytest.raises(ValueError, match="contiguous"):
+        flash_maxsim_v2_multiquery(Q, D.transpose(0, 1))
+    with pytest.raises(ValueError, match="GPU"):
+        flash_maxsim_v2_multiquery(Q, D)  # CPU tensors: no CPU path
+    with pytest.raises(ValueError):
+        flash_maxsim_single(Q, D)
+    with pytest.raises(TypeError):
+        flash_maxsim_multi_doc(Q, D[0], torch.tensor([0.0, 10.0]))
+    with pytest.raises(ValueError):
+        flash_maxsim_multi_doc(Q, D[0], torch.zeros(2, 2, dtype=torch.int64))
+    with pytest.raises(ValueError):
+        maxsim_score(Q, D, torch.ones(4, 9, dtype=torch.bool))
+    with pytest.raises(ValueError):
+        TileMaxSimPQ(torch.zeros(16, 256, dtype=torch.float16))
+    with pytest.raises(TypeError):
+        TileMaxSimPQ(torch.zeros(16, 256, 8))
+    with pytest.raises(ValueError, match="GPU"):
+        TileMaxSimPQ(torch.zeros(16, 256, 8, dtype=torch.float16))
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from tilemaxsim_amd import _lib
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
+    with pytest.raises(ImportError, match="no CPU fallback"):
+        _lib.load()
+
+
+def test_product_never_imports_the_oracle():
+    pkg = os.path.join(REPO, "tilemaxsim_amd")
+    for root, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith(".py"):
+                text = open(os.path.join(root, f)).read()
+                assert not re.search(r"^\s*(import|from)\s+oracle\b", text, flags=re.M), f
+                assert "maxsim_oracle" not in text and "c_oracle" not in text, f
