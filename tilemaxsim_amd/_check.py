@@ -1,16 +1,20 @@
 """Argument checks shared by the host entry points.
 
-Every check runs before any HIP call, so shape / dtype / device / layout errors are
-raised the same way on a machine without a GPU.
+Every check runs before any HIP call. Shape, dtype and layout checks come before the
+device check, so each error is raised the same way on a machine without a GPU.
 """
 from __future__ import annotations
 
 import torch
 
 
-def on_gpu(name: str, t: torch.Tensor) -> None:
+def tensor(name: str, t) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+
+
+def on_gpu(name: str, t: torch.Tensor) -> None:
+    tensor(name, t)
     if t.device.type != "cuda":
         raise ValueError(f"{name} must be on a ROCm GPU device (got {t.device}); tilemaxsim_amd has no CPU path")
 

@@ -25,7 +25,7 @@ def flash_maxsim_single(Q: torch.Tensor, D: torch.Tensor) -> torch.Tensor:
     Returns:
         0-d float32 tensor (the reference returns ``out.sum()``).
     """
-    _check.on_gpu("D", D)
+    _check.tensor("D", D)
     if D.dim() != 2:
         raise ValueError(f"flash_maxsim_single: D must be (Nd, d), got shape {tuple(D.shape)}")
     assert Q.shape[1] == D.shape[1], f"flash_maxsim_single: Q width {Q.shape[1]} != D width {D.shape[1]}"
@@ -66,8 +66,9 @@ def flash_maxsim_multi_doc(Q: torch.Tensor, D_flat: torch.Tensor, doc_offsets: t
     Returns:
         (num_docs,) float32 scores; an empty document scores -inf.
     """
-    _check.on_gpu("Q", Q)
-    _check.on_gpu("D_flat", D_flat)
+    _check.tensor("Q", Q)
+    _check.tensor("D_flat", D_flat)
+    _check.tensor("doc_offsets", doc_offsets)
     if D_flat.dim() != 2:
         raise ValueError(f"flash_maxsim_multi_doc: D_flat must be (total_tokens, d), got {tuple(D_flat.shape)}")
     if doc_offsets.dim() != 1 or doc_offsets.shape[0] < 1:
@@ -77,9 +78,11 @@ def flash_maxsim_multi_doc(Q: torch.Tensor, D_flat: torch.Tensor, doc_offsets: t
     T, d = D_flat.shape
     Nq = Q.shape[0]
     assert Q.dim() == 2 and Q.shape[1] == d, f"flash_maxsim_multi_doc: Q width {Q.shape[1]} != D width {d}"
-    _check.same_device(Q=Q, D_flat=D_flat)
     _check.embedding_dtype("D_flat", D_flat)
     _check.contiguous("D_flat", D_flat)
+    _check.on_gpu("Q", Q)
+    _check.on_gpu("D_flat", D_flat)
+    _check.same_device(Q=Q, D_flat=D_flat)
     Q = _check.query_like(Q, D_flat.dtype)
     offsets = doc_offsets.to(device=Q.device, dtype=torch.int64).contiguous()
     num_docs = offsets.shape[0] - 1
@@ -111,18 +114,21 @@ def maxsim_score(Q: torch.Tensor, D: torch.Tensor, D_mask: torch.Tensor | None =
     """
     if D_mask is None:
         return _dense(Q, D, "maxsim_score")
-    _check.on_gpu("Q", Q)
-    _check.on_gpu("D", D)
-    _check.on_gpu("D_mask", D_mask)
+    _check.tensor("Q", Q)
+    _check.tensor("D", D)
+    _check.tensor("D_mask", D_mask)
     if D.dim() != 3 or Q.dim() != 2:
         raise ValueError("maxsim_score: Q must be (Nq, d) and D (B, Nd, d)")
     B, Nd, d = D.shape
     if tuple(D_mask.shape) != (B, Nd):
         raise ValueError(f"maxsim_score: D_mask must be (B, Nd) = {(B, Nd)}, got {tuple(D_mask.shape)}")
     assert Q.shape[1] == d, f"maxsim_score: Q width {Q.shape[1]} != D width {d}"
-    _check.same_device(Q=Q, D=D, D_mask=D_mask)
     _check.embedding_dtype("D", D)
     _check.contiguous("D", D)
+    _check.on_gpu("Q", Q)
+    _check.on_gpu("D", D)
+    _check.on_gpu("D_mask", D_mask)
+    _check.same_device(Q=Q, D=D, D_mask=D_mask)
     Q = _check.query_like(Q, D.dtype)
     mask = D_mask
     if mask.dtype != torch.uint8:

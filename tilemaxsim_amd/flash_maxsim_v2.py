@@ -13,8 +13,8 @@ from . import _check, _lib
 
 
 def _dense(Q: torch.Tensor, D: torch.Tensor, fn: str) -> torch.Tensor:
-    _check.on_gpu("Q", Q)
-    _check.on_gpu("D", D)
+    _check.tensor("Q", Q)
+    _check.tensor("D", D)
     if D.dim() != 3:
         raise ValueError(f"{fn}: D must be (B, Nd, d), got shape {tuple(D.shape)}")
     if Q.dim() != 2:
@@ -22,9 +22,11 @@ def _dense(Q: torch.Tensor, D: torch.Tensor, fn: str) -> torch.Tensor:
     B, Nd, d = D.shape
     Nq = Q.shape[0]
     assert Q.shape[1] == d, f"{fn}: Q width {Q.shape[1]} != D width {d}"
-    _check.same_device(Q=Q, D=D)
     _check.embedding_dtype("D", D)
     _check.contiguous("D", D)
+    _check.on_gpu("Q", Q)
+    _check.on_gpu("D", D)
+    _check.same_device(Q=Q, D=D)
     Q = _check.query_like(Q, D.dtype)
     scores = torch.empty(B, dtype=torch.float32, device=Q.device)
     if B == 0:
@@ -70,16 +72,18 @@ def flash_maxsim_batched_queries(Qs: torch.Tensor, D: torch.Tensor) -> torch.Ten
     Equivalent to stacking ``flash_maxsim_v2_multiquery(Qs[i], D)`` over i, but two
     blocks of 32 query tokens share each pass over D. No reference counterpart.
     """
-    _check.on_gpu("Qs", Qs)
-    _check.on_gpu("D", D)
+    _check.tensor("Qs", Qs)
+    _check.tensor("D", D)
     if D.dim() != 3 or Qs.dim() != 3:
         raise ValueError("flash_maxsim_batched_queries: Qs must be (nQ, Nq, d) and D (B, Nd, d)")
     B, Nd, d = D.shape
     nQ, Nq, dq = Qs.shape
     assert dq == d, f"flash_maxsim_batched_queries: Q width {dq} != D width {d}"
-    _check.same_device(Qs=Qs, D=D)
     _check.embedding_dtype("D", D)
     _check.contiguous("D", D)
+    _check.on_gpu("Qs", Qs)
+    _check.on_gpu("D", D)
+    _check.same_device(Qs=Qs, D=D)
     Qs = _check.query_like(Qs, D.dtype)
     out = torch.empty(nQ, B, dtype=torch.float32, device=Qs.device)
     if B == 0 or nQ == 0:

@@ -28,10 +28,11 @@ class TileMaxSimPQ:
     """
 
     def __init__(self, codebook: torch.Tensor):
-        _check.on_gpu("codebook", codebook)
+        _check.tensor("codebook", codebook)
         if codebook.dim() != 3:
             raise ValueError(f"codebook must be (M, K, dsub), got shape {tuple(codebook.shape)}")
         _check.embedding_dtype("codebook", codebook)
+        _check.on_gpu("codebook", codebook)
         self.codebook = codebook.contiguous()
         self.M, self.K, self.dsub = codebook.shape
         self.d = self.M * self.dsub
@@ -39,18 +40,19 @@ class TileMaxSimPQ:
             raise NotImplementedError(f"K={self.K} > 256 centroids does not fit uint8 codes")
 
     def _query(self, Q: torch.Tensor) -> torch.Tensor:
-        _check.on_gpu("Q", Q)
+        _check.tensor("Q", Q)
         if Q.dim() != 2:
             raise ValueError(f"Q must be (Nq, d), got shape {tuple(Q.shape)}")
         assert Q.shape[1] == self.d, f"Q width {Q.shape[1]} != M*dsub = {self.d}"
+        _check.on_gpu("Q", Q)
         _check.same_device(Q=Q, codebook=self.codebook)
         return _check.query_like(Q, self.codebook.dtype)
 
     def _codes(self, codes: torch.Tensor, validate: bool) -> torch.Tensor:
-        _check.on_gpu("codes", codes)
-        _check.same_device(codes=codes, codebook=self.codebook)
         if codes.dtype.is_floating_point or codes.dtype == torch.bool:
             raise TypeError(f"codes must be an integer tensor, got {codes.dtype}")
+        _check.on_gpu("codes", codes)
+        _check.same_device(codes=codes, codebook=self.codebook)
         if validate and codes.numel() > 0 and (codes.dtype != torch.uint8 or self.K < 256):
             lo, hi = int(codes.min()), int(codes.max())
             if lo < 0 or hi >= self.K:
@@ -89,6 +91,7 @@ class TileMaxSimPQ:
         Returns:
             (B,) float32 MaxSim scores; a document with Nd == 0 scores -inf.
         """
+        _check.tensor("codes", codes)
         if codes.dim() != 3:
             raise ValueError(f"codes must be (B, Nd, M), got shape {tuple(codes.shape)}")
         B, Nd, M = codes.shape
