@@ -1,0 +1,344 @@
+"""Benchmark of the fused MaxSim scoring path on one MI355X.
+
+Default workload (the one the headline metric is quoted on):
+64 queries x 1,000,000 documents, Nq = 32, Nd = 180, d = 128, fp16 L2-normalised
+Gaussian embeddings (~46 GB resident in HBM). One step scores every query against
+every document with ``flash_maxsim_v2_multiquery`` (one HBM pass over the corpus per
+query, as the reference's V2-MQ kernel) and takes the top-100 per query.
+
+Other workloads (``--config``): c1 (CPU-sized plumbing check), c3 (2M
+variable-length documents), c4 (d-tiled, ``--d 256|512|768``), c5 (PQ/ADC, 5M
+documents of uint8 codes).
+
+Prints ONE JSON line on stdout. ``value`` is (query, document) pairs scored per second
+over the whole step; ``roofline`` is the dominant kernel's algorithmic bandwidth from
+HIP events around each of its launches; ``cpu_baseline`` times the numpy restatement
+of the reference PyTorch path on this host's cores over a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "docs scored/sec + achieved HBM GB/s (% of peak), N_q=32 d=128 fp16"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=5)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy"])
+    p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+# ----------------------------------------------------------------------------- data
+def normalized_fp16(torch, shape, gen, chunk_rows=1 << 21):
+    """Gaussian -> L2-normalise each token in fp32 -> fp16, generated in chunks on the GPU."""
+    out = torch.empty(shape, dtype=torch.float16, device="cuda")
+    flat = out.view(-1, shape[-1])
+    for s in range(0, flat.shape[0], chunk_rows):
+        e = min(flat.shape[0], s + chunk_rows)
+        x = torch.randn(e - s, shape[-1], device="cuda", generator=gen)
+        flat[s:e] = torch.nn.functional.normalize(x, dim=-1).half()
+    return out
+
+
+class KernelTimer:
+    """HIP events around each launch of the dominant kernel, on the stream it runs on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+        self.enabled = False
+
+    def __call__(self, fn):
+        if not self.enabled:
+            return fn()
+        s = self.torch.cuda.Event(enable_timing=True)
+        e = self.torch.cuda.Event(enable_timing=True)
+        s.record()
+        r = fn()
+        e.record()
+        self.pairs.append((s, e))
+        return r
+
+    def avg_ms(self):
+        ts = [s.elapsed_time(e) for s, e in self.pairs]
+        return float(np.mean(ts)), float(np.median(ts)), len(ts)
+
+
+# ----------------------------------------------------------------------------- workloads
+class Dense:
+    kernel = "dense_maxsim_kernel"
+
+    def __init__(self, torch, n_queries, B, Nd, d, Nq=32, name="c2", topk=100):
+        self.torch, self.nQ, self.B, self.Nd, self.d, self.Nq, self.k = torch, n_queries, B, Nd, d, Nq, topk
+        self.name = name
+        gen = torch.Generator(device="cuda").manual_seed(1234)
+        log(f"[bench] generating {B} docs x {Nd} x {d} fp16 ({B * Nd * d * 2 / 1e9:.2f} GB)")
+        self.D = normalized_fp16(torch, (B, Nd, d), gen)
+        self.Q = normalized_fp16(torch, (n_queries, Nq, d), gen)
+        self.scores = torch.empty(n_queries, B, dtype=torch.float32, device="cuda")
+
+    def step(self, timer):
+        from tilemaxsim_amd import flash_maxsim_v2_multiquery
+        for i in range(self.nQ):
+            s = timer(lambda: flash_maxsim_v2_multiquery(self.Q[i], self.D))
+            self.scores[i].copy_(s)
+        return self.torch.topk(self.scores, min(self.k, self.B), dim=1)
+
+    def bytes_per_launch(self):
+        return self.Nq * self.d * 2 + self.B * self.Nd * self.d * 2 + self.B * 4
+
+    def pairs_per_step(self):
+        return self.nQ * self.B
+
+    def config(self):
+        return {"workload": f"{self.name}: {self.nQ} queries x {self.B:,} docs, Nq={self.Nq}, Nd={self.Nd}, d={self.d}, "
+                            f"fp16 L2-normalised Gaussian, top-{self.k} per query",
+                "queries": self.nQ, "docs": self.B, "Nq": self.Nq, "Nd": self.Nd, "d": self.d, "top_k": self.k,
+                "kernel": "flash_maxsim_v2_multiquery (one HBM pass per query)"}
+
+    def cpu_baseline(self, seconds, threads):
+        from oracle import maxsim_oracle as orc
+        n = min(self.B, 4000)
+        Q = self.Q[0].cpu().numpy()
+        D = self.D[:n].cpu().numpy()
+        return _time_cpu(lambda: orc.maxsim_naive(Q, D, chunk=500), n, seconds, threads,
+                         f"{n} docs of this corpus x query 0, numpy fp32 materialise-then-reduce "
+                         "(restates pytorch_maxsim_naive), repeated")
+
+
+class Varlen(Dense):
+    def __init__(self, torch, n_queries, B, lo, hi, d, Nq=32, topk=100):
+        self.torch, self.nQ, self.B, self.d, self.Nq, self.k = torch, n_queries, B, d, Nq, topk
+        self.name = "c3"
+        rng = np.random.default_rng(77)
+        lens = rng.integers(lo, hi + 1, size=B)
+        offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        self.T = int(offs[-1])
+        self.lo, self.hi = lo, hi
+        gen = torch.Generator(device="cuda").manual_seed(4321)
+        log(f"[bench] generating {B} varlen docs, {self.T} tokens x {d} fp16 ({self.T * d * 2 / 1e9:.2f} GB)")
+        self.D = normalized_fp16(torch, (self.T, d), gen)
+        self.offsets = torch.from_numpy(offs).cuda()
+        self.Q = normalized_fp16(torch, (n_queries, Nq, d), gen)
+        self.scores = torch.empty(n_queries, B, dtype=torch.float32, device="cuda")
+        from tilemaxsim_amd import flash_maxsim_multi_doc
+        flash_maxsim_multi_doc(self.Q[0], self.D, self.offsets, validate=True)  # offsets checked once, at load
+
+    def step(self, timer):
+        from tilemaxsim_amd import flash_maxsim_multi_doc
+        for i in range(self.nQ):
+            s = timer(lambda: flash_maxsim_multi_doc(self.Q[i], self.D, self.offsets, validate=False))
+            self.scores[i].copy_(s)
+        return self.torch.topk(self.scores, self.k, dim=1)
+
+    def bytes_per_launch(self):
+        return self.Nq * self.d * 2 + self.T * self.d * 2 + (self.B + 1) * 8 + self.B * 4
+
+    def config(self):
+        return {"workload": f"c3: {self.nQ} queries x {self.B:,} variable-length docs (Nd~U[{self.lo},{self.hi}], "
+                            f"{self.T:,} tokens), Nq={self.Nq}, d={self.d}, fp16, top-{self.k} per query",
+                "queries": self.nQ, "docs": self.B, "tokens": self.T, "Nq": self.Nq, "d": self.d, "top_k": self.k,
+                "kernel": "flash_maxsim_multi_doc (offsets, no padding)"}
+
+    def cpu_baseline(self, seconds, threads):
+        from oracle import maxsim_oracle as orc
+        n = 4000
+        offs = self.offsets[: n + 1].cpu().numpy()
+        Q = self.Q[0].cpu().numpy()
+        Dflat = self.D[: int(offs[-1])].cpu().numpy()
+        return _time_cpu(lambda: orc.maxsim_varlen(Q, Dflat, offs), n, seconds, threads,
+                         f"first {n} docs x query 0, numpy fp32 per-token sims + segmented max, repeated")
+
+
+class PQ:
+    kernel = "pq_mfma_score_kernel"
+
+    def __init__(self, torch, n_queries, B, Nd, M=16, K=256, dsub=8, Nq=32, topk=100):
+        self.torch, self.nQ, self.B, self.Nd, self.M, self.K, self.dsub, self.Nq, self.k = (
+            torch, n_queries, B, Nd, M, K, dsub, Nq, topk)
+        gen = torch.Generator(device="cuda").manual_seed(99)
+        log(f"[bench] generating {B} docs x {Nd} x {M} uint8 codes ({B * Nd * M / 1e9:.2f} GB)")
+        self.codes = torch.randint(0, K, (B, Nd, M), dtype=torch.uint8, device="cuda", generator=gen)
+        self.codebook = torch.randn(M, K, dsub, device="cuda", generator=gen).half()
+        self.Q = normalized_fp16(torch, (n_queries, Nq, M * dsub), gen)
+        self.scores = torch.empty(n_queries, B, dtype=torch.float32, device="cuda")
+        from tilemaxsim_amd import TileMaxSimPQ
+        self.pq = TileMaxSimPQ(self.codebook)
+
+    def step(self, timer):
+        for i in range(self.nQ):
+            s = timer(lambda: self.pq.score_batch(self.Q[i], self.codes, validate=False))
+            self.scores[i].copy_(s)
+        return self.torch.topk(self.scores, self.k, dim=1)
+
+    def bytes_per_launch(self):
+        return self.B * self.Nd * self.M  # code bytes: the north-star roofline for PQ
+
+    def pairs_per_step(self):
+        return self.nQ * self.B
+
+    def config(self):
+        return {"workload": f"c5: PQ/ADC, {self.nQ} queries x {self.B:,} docs x Nd={self.Nd}, M={self.M}, K={self.K}, "
+                            f"dsub={self.dsub}, uint8 codes, fp16 codebook, top-{self.k} per query",
+                "queries": self.nQ, "docs": self.B, "Nq": self.Nq, "Nd": self.Nd, "M": self.M, "K": self.K,
+                "dsub": self.dsub, "top_k": self.k,
+                "kernel": "TileMaxSimPQ.score_batch (codebook gather in LDS + MFMA)",
+                "roofline_bytes": "code bytes B*Nd*M per launch"}
+
+    def cpu_baseline(self, seconds, threads):
+        from oracle import maxsim_oracle as orc
+        n = 2000
+        Q = self.Q[0].cpu().numpy()
+        C = self.codebook.cpu().numpy()
+        codes = self.codes[:n].cpu().numpy()
+        return _time_cpu(lambda: orc.pq_decompress_score(Q, C, codes, chunk=500), n, seconds, threads,
+                         f"{n} docs x query 0, numpy decompress-then-score (restates pytorch_pqsim_baseline), repeated")
+
+
+class Copy:
+    """Plain device-to-device copy of a known size (torch's copy kernel): the reference
+    point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes."""
+    kernel = "copy"
+
+    def __init__(self, torch, nbytes=4 << 30):
+        self.torch, self.n = torch, nbytes
+        self.src = torch.ones(nbytes // 2, dtype=torch.float16, device="cuda")
+        self.dst = torch.empty_like(self.src)
+
+    def step(self, timer):
+        timer(lambda: self.dst.copy_(self.src))
+
+    def bytes_per_launch(self):
+        return 2 * self.n  # read + write
+
+    def pairs_per_step(self):
+        return 0
+
+    def config(self):
+        return {"workload": f"copy: {self.n} bytes device to device (rocprof counter calibration)"}
+
+    def cpu_baseline(self, seconds, threads):
+        return None
+
+
+def _time_cpu(fn, docs_per_call, seconds, threads, sample):
+    from threadpoolctl import threadpool_limits
+    with threadpool_limits(limits=threads):
+        fn()  # warm-up
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+    return {"value": docs_per_call * n / el, "unit": "docs/s (1 query)", "cores": threads, "kind": "port",
+            "sample": f"{sample} {n}x in {el:.1f} s; host {platform.processor() or platform.machine()}, "
+                      f"os.cpu_count()={os.cpu_count()}"}
+
+
+def _traffic(kernel, config):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(HERE, "profiles", f"{kernel}_{config}_traffic.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        t = json.load(f)
+    return t.get("bytes_per_launch"), os.path.relpath(path, HERE)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); documents shard across GPUs "
+              "with no communication besides a top-k merge, which is not part of this build", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    import tilemaxsim_amd  # noqa: F401  (fails loudly if libtilemaxsim.so is missing)
+
+    if args.config == "c1":
+        wl = Dense(torch, 1, 1000, 128, 128, name="c1")
+    elif args.config == "c2":
+        wl = Dense(torch, 64, 1_000_000, 180, 128, name="c2")
+    elif args.config == "c3":
+        wl = Varlen(torch, 32, 2_000_000, 32, 300, 128)
+    elif args.config == "c4":
+        wl = Dense(torch, 16, 200_000, 128, args.d, name=f"c4_d{args.d}")
+    elif args.config == "c5":
+        wl = PQ(torch, 32, 5_000_000, 128)
+    else:
+        wl = Copy(torch)
+    torch.cuda.synchronize()
+
+    timer = KernelTimer(torch)
+    log(f"[bench] warmup {args.warmup} step(s)")
+    for _ in range(args.warmup):
+        wl.step(timer)
+    torch.cuda.synchronize()
+    timer.enabled = True
+    log(f"[bench] timing {args.steps} step(s)")
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        wl.step(timer)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed * 1e3 / args.steps
+    k_mean, k_p50, k_n = timer.avg_ms()
+    log(f"[bench] {ms_step:.2f} ms/step, kernel mean {k_mean:.4f} ms over {k_n} launches")
+
+    nbytes = wl.bytes_per_launch()
+    achieved = nbytes / (k_mean * 1e-3) / 1e9
+    traffic, traffic_src = _traffic(wl.kernel, args.config if args.config != "c4" else f"c4_d{args.d}")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": wl.kernel, "bytes_per_launch": nbytes, "launch_ms_mean": round(k_mean, 5),
+                "launch_ms_p50": round(k_p50, 5), "launches": k_n}
+    if traffic_src:
+        roofline["traffic_source"] = traffic_src
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        log(f"[bench] CPU baseline on {threads} threads, ~{args.cpu_seconds:.0f} s")
+        cpu = wl.cpu_baseline(args.cpu_seconds, threads)
+
+    pairs = wl.pairs_per_step()
+    out = {
+        "metric": METRIC, "value": round(pairs / (ms_step * 1e-3), 1), "unit": "docs/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded; no dataset)", "config": wl.config(),
+        "hbm_gbs": round(achieved, 1), "hbm_pct_of_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
