@@ -26,6 +26,8 @@ HIPCC_FLAGS = [
     "-fPIC",
     # Packed-FP32 VALU forms stay disabled for all device code on this part.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Embeddings are finite: max/min need no NaN canonicalisation (halves the VALU max work).
+    "-fno-honor-nans",
     "-I", os.path.join(REPO_DIR, "include"),
     "-I", CSRC,
 ]

@@ -379,7 +379,13 @@ static int fill(float* out, int64_t n, float v, hipStream_t st) {
 // ------------------------------------------------------------------------------
 // host dispatch
 // ------------------------------------------------------------------------------
-constexpr int kNSub = 2;
+#ifndef TMS_DENSE_NSUB
+#define TMS_DENSE_NSUB 2  // 16-token MFMA row blocks per tile (tile = 16 * NSUB tokens)
+#endif
+#ifndef TMS_DENSE_TOKENS_PER_WAVE
+#define TMS_DENSE_TOKENS_PER_WAVE 192  // document tokens one wave streams (rounded to whole documents)
+#endif
+constexpr int kNSub = TMS_DENSE_NSUB;
 constexpr int kMaxQldsBytes = 64 * 1024;
 
 template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED>
@@ -407,13 +413,15 @@ static int launch_nqb(const DenseArgs& a, bool aligned, int64_t grid, hipStream_
   return launch_one<DT, MODE, NQB, 0, false, false>(a, grid, lds, st);
 }
 
-// Documents per wave: enough waves to fill the chip several times over, so the
-// hardware dispatcher balances ragged documents, but long enough streams that the
-// per-wave query-fragment load is amortised.
+// Documents per wave: short waves (about TMS_DENSE_TOKENS_PER_WAVE tokens, i.e. one
+// document at typical ColBERT lengths) keep every CU's load pipeline full until the
+// end of the launch and let the dispatcher balance ragged documents; the grid still
+// spans at least two rounds of the chip's resident waves, and a wave never carries
+// fewer tokens than it spends loading its query fragments.
 static int pick_docs_per_wave(int64_t B, int64_t tokens_per_doc_hint) {
-  const int64_t target_waves = 256 * 16 * 8;
-  int64_t dpw = B / target_waves;
-  if (tokens_per_doc_hint > 0 && dpw * tokens_per_doc_hint > 16384) dpw = 16384 / tokens_per_doc_hint;
+  int64_t dpw = tokens_per_doc_hint > 0 ? TMS_DENSE_TOKENS_PER_WAVE / tokens_per_doc_hint : 1;
+  const int64_t min_waves = (int64_t)256 * 16 * 2;
+  if (dpw > 1 && B / dpw < min_waves) dpw = B / min_waves;
   if (dpw < 1) dpw = 1;
   if (dpw > 64) dpw = 64;
   return (int)dpw;

@@ -21,6 +21,16 @@
 
 #include "tms_common.h"
 
+#ifndef TMS_PQ_UT
+#define TMS_PQ_UT 4  // 16-token subtiles per pipelined unit of the MFMA PQ kernel
+#endif
+#ifndef TMS_PQ_PIPE
+#define TMS_PQ_PIPE 2  // 1: gathers one subtile ahead; 2: two ahead, split accumulators
+#endif
+#ifndef TMS_PQ_WAVE_ROUNDS
+#define TMS_PQ_WAVE_ROUNDS 4  // grid covers the chip's resident waves about this many times
+#endif
+
 namespace tms {
 
 template <int DT>
@@ -282,25 +292,71 @@ __global__ void __launch_bounds__(kPqThreads) pq_mfma_score_kernel(PqArgs a) {
     }
   };
 
-  auto compute = [&](const Codes& c, int64_t t0) {
+  // Subtiles past the end of a document hold clamped duplicates of its last token,
+  // which cannot change a max, so every unit runs all UT subtiles without a branch.
+  // The LDS gathers of subtile u+1 are issued before the MFMAs of subtile u.
+  auto gather_sub = [&](u32x4 (&fr)[KS], const Codes& c, int u) {
+#pragma unroll
+    for (int s = 0; s < KS; s++) fr[s] = gather(c, u, s);
+  };
+  auto mfma_sub = [&](const u32x4 (&fr)[KS]) {
+#pragma unroll
+    for (int j = 0; j < NQB; j++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; s++) acc = mfma16x16x32<DT>(fr[s], qf[j][s][h], acc);
+#pragma unroll
+        for (int i = 0; i < 4; i++) rmax[j][h][i] = fmaxf(rmax[j][h][i], acc[i]);
+      }
+  };
+#if TMS_PQ_PIPE == 1
+  auto compute = [&](const Codes& c, int64_t) {
+    u32x4 fa[KS], fb[KS];
+    gather_sub(fa, c, 0);
+#pragma unroll
+    for (int u = 0; u < UT; u += 2) {
+      if (u + 1 < UT) gather_sub(fb, c, u + 1);
+      mfma_sub(fa);
+      if (u + 2 < UT) gather_sub(fa, c, u + 2);
+      if (u + 1 < UT) mfma_sub(fb);
+    }
+  };
+#else
+  // Gathers run two subtiles ahead (three fragment buffers) and the running max of
+  // subtile u-1 is taken after the MFMAs of subtile u are issued (two accumulator
+  // sets), so LDS latency and MFMA latency overlap with independent work.
+  auto compute = [&](const Codes& c, int64_t) {
+    u32x4 fr[3][KS];
+    f32x4 acc[2][NQB][2];
+    gather_sub(fr[0], c, 0);
+    if (UT > 1) gather_sub(fr[1], c, 1);
+    auto take_max = [&](int p) {
+#pragma unroll
+      for (int j = 0; j < NQB; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) rmax[j][h][i] = fmaxf(rmax[j][h][i], acc[p][j][h][i]);
+    };
 #pragma unroll
     for (int u = 0; u < UT; u++) {
-      if (t0 + 16 * u >= nd) break;  // whole subtile past the document (uniform)
-      u32x4 fr[KS];
-#pragma unroll
-      for (int s = 0; s < KS; s++) fr[s] = gather(c, u, s);
 #pragma unroll
       for (int j = 0; j < NQB; j++)
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          f32x4 a4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int s = 0; s < KS; s++) acc = mfma16x16x32<DT>(fr[s], qf[j][s][h], acc);
-#pragma unroll
-          for (int i = 0; i < 4; i++) rmax[j][h][i] = fmaxf(rmax[j][h][i], acc[i]);
+          for (int s = 0; s < KS; s++) a4 = mfma16x16x32<DT>(fr[u % 3][s], qf[j][s][h], a4);
+          acc[u & 1][j][h] = a4;
         }
+      if (u + 2 < UT) gather_sub(fr[(u + 2) % 3], c, u + 2);
+      if (u > 0) take_max((u - 1) & 1);
     }
+    take_max((UT - 1) & 1);
   };
+#endif
 
   if (nd == 0) {
     for (int64_t b = b_begin; b < b_end; b++) write_doc(b, NEG_INF);
@@ -363,7 +419,7 @@ static int launch_lut_score(const LutArgs& a, hipStream_t st) {
   return check_launch("pq_lut_score_kernel");
 }
 
-constexpr int kPqUT = 4;
+constexpr int kPqUT = TMS_PQ_UT;
 
 template <int DT, int DSUB, int KS, int NQB>
 static int launch_mfma_one(const PqArgs& a, int64_t grid, size_t lds, hipStream_t st) {
@@ -505,7 +561,7 @@ int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int
     // run of documents (about four rounds of the chip) so the per-workgroup codebook
     // load is amortised and the last round stays short.
     const int64_t waves_per_wg = kPqThreads / 64;
-    const int64_t target_waves = 256 * 2 * waves_per_wg * 4;
+    const int64_t target_waves = (int64_t)256 * 2 * waves_per_wg * TMS_PQ_WAVE_ROUNDS;
     int64_t dpw = (B + target_waves - 1) / target_waves;
     if (dpw < 1) dpw = 1;
     a.docs_per_wave = (int32_t)dpw;
