@@ -42,7 +42,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "copy"])
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c4", "c5", "copy"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -125,6 +125,32 @@ class Dense:
         return _time_cpu(lambda: orc.maxsim_naive(Q, D, chunk=500), n, seconds, threads,
                          f"{n} docs of this corpus x query 0, numpy fp32 materialise-then-reduce "
                          "(restates pytorch_maxsim_naive), repeated")
+
+
+class DenseBatched(Dense):
+    """C2 data, all queries scored by the batched-query entry point: each workgroup's
+    four waves hold 16 query blocks and share one HBM pass over the documents, which
+    moves the path from the HBM roof to the MFMA roof."""
+    kernel = "dense_maxsim_kernel"
+    MFMA_PEAK_TFLOPS = 2500.0
+
+    def step(self, timer):
+        from tilemaxsim_amd import flash_maxsim_batched_queries
+        s = timer(lambda: flash_maxsim_batched_queries(self.Q, self.D))
+        self.scores.copy_(s)
+        return self.torch.topk(self.scores, min(self.k, self.B), dim=1)
+
+    def flops_per_launch(self):
+        return 2 * self.nQ * self.Nq * self.B * self.Nd * self.d
+
+    def bytes_per_launch(self):  # every query against one read of the corpus
+        return self.nQ * self.Nq * self.d * 2 + self.B * self.Nd * self.d * 2 + self.nQ * self.B * 4
+
+    def config(self):
+        c = super().config()
+        c["workload"] += " (batched-query kernel)"
+        c["kernel"] = "flash_maxsim_batched_queries (16 query blocks per HBM pass)"
+        return c
 
 
 class Varlen(Dense):
@@ -286,6 +312,8 @@ def main():
         wl = Dense(torch, 1, 1000, 128, 128, name="c1")
     elif args.config == "c2":
         wl = Dense(torch, 64, 1_000_000, 180, 128, name="c2")
+    elif args.config == "c2b":
+        wl = DenseBatched(torch, 64, 1_000_000, 180, 128, name="c2b")
     elif args.config == "c3":
         wl = Varlen(torch, 32, 2_000_000, 32, 300, 128)
     elif args.config == "c4":
@@ -321,6 +349,11 @@ def main():
                 "launch_ms_p50": round(k_p50, 5), "launches": k_n}
     if traffic_src:
         roofline["traffic_source"] = traffic_src
+    if hasattr(wl, "flops_per_launch"):  # MFMA-bound path: price the call against dense fp16 MFMA
+        tf = wl.flops_per_launch() / (k_mean * 1e-3) / 1e12
+        roofline.update({"bound": "mfma", "achieved": round(tf, 1), "peak": wl.MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / wl.MFMA_PEAK_TFLOPS, 4), "flops_per_launch": wl.flops_per_launch(),
+                         "launch": "one flash_maxsim_batched_queries call (one kernel per 16 query blocks)"})
 
     cpu = None
     if not args.no_cpu_baseline:

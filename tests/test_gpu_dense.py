@@ -249,7 +249,10 @@ def test_batched_queries(cuda):
     import torch
     from tilemaxsim_amd import flash_maxsim_batched_queries, flash_maxsim_v2_multiquery
     rng = _rng(31)
-    for nQ, Nq in [(5, 32), (3, 20), (4, 70)]:
+    # (5, 32): 5 blocks, query-split kernel; (3, 20): 3 blocks, per-pass kernel;
+    # (4, 70): 3 blocks per query, split with 3 blocks per wave; (37, 32): three split
+    # launches, the last one partial; (6, 128): 4 blocks per query
+    for nQ, Nq in [(5, 32), (3, 20), (4, 70), (37, 32), (6, 128)]:
         Qs = _to_gpu(_randn(rng, (nQ, Nq, 128), normalize=True))
         D = _to_gpu(_randn(rng, (400, 60, 128), normalize=True))
         got = flash_maxsim_batched_queries(Qs, D).cpu().numpy()

@@ -27,6 +27,10 @@
 
 #include "tms_common.h"
 
+#ifndef TMS_SPLIT_INTERLEAVE
+#define TMS_SPLIT_INTERLEAVE 1  // query-split kernel: interleave the MFMA chains of all its blocks
+#endif
+
 namespace tms {
 
 static thread_local char g_err[512];
@@ -64,6 +68,7 @@ struct DenseArgs {
   int32_t nq;              // tokens per query
   int32_t nbq;             // 32-token blocks per query = ceil(nq / 32)
   int32_t blk0;            // first global query block of this launch
+  int32_t blk_end;         // query-split launches: one past the last block of the launch
   int32_t nblk;            // blocks in this launch (<= NQB template)
   int32_t d, nchunk, nstep, nkg;
   int32_t docs_per_wave;
@@ -101,24 +106,38 @@ struct Cursor {
 
 // KS_REG > 0: Q fragments in VGPRs, d == 32 * KS_REG (single k-group).
 // KS_REG == 0: Q fragments in LDS, k-groups of 4 steps (128 dims), any d.
-template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, int NSUB>
-__global__ void __launch_bounds__(256) dense_maxsim_kernel(DenseArgs a) {
+// QSPLIT (Q in VGPRs only): the four waves of a workgroup stream the same documents
+// and each owns its own a.nblk query blocks (the launch covers 4 * a.nblk blocks,
+// whole queries per wave), so one HBM pass over D serves many queries; the
+// repeated document reads of the other waves are served by L1/L2.
+template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, int NSUB, bool QSPLIT, int PFD>
+__global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(DenseArgs a) {
   constexpr bool QREG = KS_REG > 0;
   constexpr int KS = QREG ? KS_REG : 4;
   constexpr int TT = 16 * NSUB;
+  static_assert(!QSPLIT || QREG, "query splitting needs the query fragments in VGPRs");
   extern __shared__ u32x4 qlds[];
 
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g = lane >> 4;
+  const int wid = threadIdx.x >> 6;
+
+  // Query blocks of this wave: [my_blk0, my_blk0 + my_nblk).
+  int my_blk0 = a.blk0, my_nblk = a.nblk;
+  if constexpr (QSPLIT) {
+    my_blk0 = a.blk0 + wid * a.nblk;
+    const int left = a.blk_end - my_blk0;
+    my_nblk = left < 0 ? 0 : (left < a.nblk ? left : a.nblk);
+  }
 
   // ---- query fragments -------------------------------------------------------
   // Fragment (block j, step S, half h) for this lane: query row of block j, token
   // 16h + r, elements of chunk 4S + g.
   auto q_row = [&](int j, int h, int rr, bool& valid) -> int64_t {
-    int jb = a.blk0 + j;
+    int jb = my_blk0 + j;
     int qi = jb / a.nbq;
     int tok = (jb - qi * a.nbq) * 32 + 16 * h + rr;
-    valid = (j < a.nblk) && (tok < a.nq);
+    valid = (j < my_nblk) && (tok < a.nq);
     return (int64_t)qi * a.nq + tok;
   };
 
@@ -148,29 +167,29 @@ __global__ void __launch_bounds__(256) dense_maxsim_kernel(DenseArgs a) {
     __syncthreads();
   }
 
-  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t wave = QSPLIT ? (int64_t)blockIdx.x : (int64_t)blockIdx.x * (blockDim.x >> 6) + wid;
   const int64_t b_begin = wave * a.docs_per_wave;
-  if (b_begin >= a.B) return;
+  if (b_begin >= a.B || my_nblk <= 0) return;
   const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
 
   const float NEG_INF = -__builtin_inff();
 
   // ---- per-query output ------------------------------------------------------
-  // Block sums are added per query; a query whose first block precedes this launch
-  // accumulates onto the previous launch's partial score.
+  // Block sums are added per query; a query whose first block precedes this wave's
+  // blocks accumulates onto the previous launch's partial score.
   auto write_doc = [&](int64_t b, const float (&blk)[NQB]) {
     if (lane == 0) {
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < NQB; j++) {
-        if (j >= a.nblk) break;
-        int jb = a.blk0 + j;
+        if (j >= my_nblk) break;
+        int jb = my_blk0 + j;
         int qi = jb / a.nbq;
         s += blk[j];
-        bool last_of_query = (j == a.nblk - 1) || ((jb + 1) / a.nbq != qi);
+        bool last_of_query = (j == my_nblk - 1) || ((jb + 1) / a.nbq != qi);
         if (last_of_query) {
           float* o = a.out + (int64_t)qi * a.B + b;
-          bool cont = (qi * a.nbq) < a.blk0;  // query began in an earlier launch
+          bool cont = (qi * a.nbq) < my_blk0;  // query began in an earlier launch
           *o = cont ? (*o + s) : s;
           s = 0.f;
         }
@@ -271,16 +290,26 @@ __global__ void __launch_bounds__(256) dense_maxsim_kernel(DenseArgs a) {
     }
   };
 
-  f32x4 acc[NSUB][NQB][2];
-  f32x4 rmax[NQB][2];
+  // Accumulators that persist across k-groups (LDS-query path only).
+  f32x4 acc[QREG ? 1 : NSUB][QREG ? 1 : NQB][2];
+  // Running max of this lane's column (query token 16h + r of block j) over every row
+  // it has seen; the four rows of each MFMA result fold in with a tree of maxes.
+  float rmax[NQB][2];
 #pragma unroll
-  for (int j = 0; j < NQB; j++)
+  for (int j = 0; j < NQB; j++) rmax[j][0] = rmax[j][1] = NEG_INF;
+  auto fold = [&](float& m, f32x4 v, uint32_t valid_bits) {
+    if constexpr (MODE == MODE_MASKED) {
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      rmax[j][h] = f32x4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
-#pragma unroll
-      for (int sub = 0; sub < NSUB; sub++) acc[sub][j][h] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < 4; i++) v[i] = ((valid_bits >> i) & 1u) ? v[i] : NEG_INF;
     }
+    m = fmaxf(m, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+  };
+  if constexpr (!QREG) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+      for (int j = 0; j < NQB; j++) acc[sub][j][0] = acc[sub][j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   auto finish_doc = [&](int64_t b) {
     float blk[NQB];
@@ -289,7 +318,7 @@ __global__ void __launch_bounds__(256) dense_maxsim_kernel(DenseArgs a) {
       float s = 0.f;
 #pragma unroll
       for (int h = 0; h < 2; h++) {
-        float m = fmaxf(fmaxf(rmax[j][h][0], rmax[j][h][1]), fmaxf(rmax[j][h][2], rmax[j][h][3]));
+        float m = rmax[j][h];
         m = fmaxf(m, __shfl_xor(m, 16));
         m = fmaxf(m, __shfl_xor(m, 32));
         bool valid;
@@ -301,13 +330,58 @@ __global__ void __launch_bounds__(256) dense_maxsim_kernel(DenseArgs a) {
       s += __shfl_xor(s, 2);
       s += __shfl_xor(s, 1);
       blk[j] = s;
-      rmax[j][0] = f32x4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
-      rmax[j][1] = f32x4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
+      rmax[j][0] = rmax[j][1] = NEG_INF;
     }
     write_doc(b, blk);
   };
 
   auto compute_tile = [&](const Buf& buf, const Cursor& c) {
+    if constexpr (QREG && QSPLIT && NSUB == 1 && TMS_SPLIT_INTERLEAVE) {
+      // All of this wave's query blocks at once: 2 * NQB independent accumulator chains
+      // keep the MFMA pipe busy (the query-split kernel is MFMA-bound).
+      f32x4 accb[NQB][2];
+#pragma unroll
+      for (int j = 0; j < NQB; j++) accb[j][0] = accb[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int j = 0; j < NQB; j++) {
+          if (j >= my_nblk) break;
+#pragma unroll
+          for (int h = 0; h < 2; h++) accb[j][h] = mfma16x16x32<DT>(buf.f[0][s], qf[j][s][h], accb[j][h]);
+        }
+#pragma unroll
+      for (int j = 0; j < NQB; j++) {
+        if (j >= my_nblk) break;
+        fold(rmax[j][0], accb[j][0], 0u);
+        fold(rmax[j][1], accb[j][1], 0u);
+      }
+      if (c.t0 + TT >= c.len) finish_doc(c.b);
+      return;
+    } else if constexpr (QREG) {
+      // One k-group: each query block is finished before the next, so only one
+      // block's accumulators are live (what lets a wave hold several blocks).
+#pragma unroll
+      for (int j = 0; j < NQB; j++) {
+        if (j >= my_nblk) break;
+        f32x4 acc1[NSUB][2];
+#pragma unroll
+        for (int sub = 0; sub < NSUB; sub++) acc1[sub][0] = acc1[sub][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+#pragma unroll
+          for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int sub = 0; sub < NSUB; sub++)
+              acc1[sub][h] = mfma16x16x32<DT>(buf.f[sub][s], qf[j][s][h], acc1[sub][h]);
+#pragma unroll
+        for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+          for (int h = 0; h < 2; h++) fold(rmax[j][h], acc1[sub][h], MODE == MODE_MASKED ? buf.m[sub] : 0u);
+      }
+      if (c.t0 + TT >= c.len) finish_doc(c.b);
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < KS; s++) {
       const int S = c.kg * KS + s;
@@ -330,12 +404,7 @@ __global__ void __launch_bounds__(256) dense_maxsim_kernel(DenseArgs a) {
         for (int j = 0; j < NQB; j++)
 #pragma unroll
           for (int h = 0; h < 2; h++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              float v = acc[sub][j][h][i];
-              if constexpr (MODE == MODE_MASKED) v = ((buf.m[sub] >> i) & 1u) ? v : NEG_INF;
-              rmax[j][h][i] = fmaxf(rmax[j][h][i], v);
-            }
+            fold(rmax[j][h], acc[sub][j][h], MODE == MODE_MASKED ? buf.m[sub] : 0u);
             acc[sub][j][h] = f32x4{0.f, 0.f, 0.f, 0.f};
           }
       if (c.t0 + TT >= c.len) finish_doc(c.b);
@@ -343,23 +412,34 @@ __global__ void __launch_bounds__(256) dense_maxsim_kernel(DenseArgs a) {
   };
 
   // ---- pipelined main loop -----------------------------------------------------
-  Cursor cur;
-  seek(cur, b_begin);
-  if (cur.b >= b_end) return;
-  Buf b0, b1;
-  load_tile(b0, cur);
+  // A ring of PFD + 1 tile buffers: the loads of the next PFD tiles are in flight
+  // while a tile is scored. The ring is unrolled so every buffer index is static.
+  Cursor next;
+  seek(next, b_begin);
+  if (next.b >= b_end) return;
+  Buf ring[PFD + 1];
+  Cursor at[PFD + 1];
+#pragma unroll
+  for (int k = 0; k < PFD; k++) {
+    at[k] = next;
+    if (next.b < b_end) {
+      load_tile(ring[k], next);
+      advance(next);
+    }
+  }
   while (true) {
-    Cursor nxt = cur;
-    advance(nxt);
-    if (nxt.b < b_end) load_tile(b1, nxt);
-    compute_tile(b0, cur);
-    if (nxt.b >= b_end) break;
-    cur = nxt;
-    advance(nxt);
-    if (nxt.b < b_end) load_tile(b0, nxt);
-    compute_tile(b1, cur);
-    if (nxt.b >= b_end) break;
-    cur = nxt;
+#pragma unroll
+    for (int k = 0; k <= PFD; k++) {
+      constexpr int kPf = PFD;
+      const int slot_in = (k + kPf) % (kPf + 1);
+      at[slot_in] = next;
+      if (next.b < b_end) {
+        load_tile(ring[slot_in], next);
+        advance(next);
+      }
+      if (at[k].b >= b_end) return;
+      compute_tile(ring[k], at[k]);
+    }
   }
 }
 
@@ -387,12 +467,55 @@ static int fill(float* out, int64_t n, float v, hipStream_t st) {
 #endif
 constexpr int kNSub = TMS_DENSE_NSUB;
 constexpr int kMaxQldsBytes = 64 * 1024;
+#ifndef TMS_SPLIT_NSUB
+#define TMS_SPLIT_NSUB 1  // tile rows of the query-split kernel (its query fragments take 128 VGPRs)
+#endif
+#ifndef TMS_DENSE_PFD
+#define TMS_DENSE_PFD 1  // tiles in flight ahead of the one being scored
+#endif
+#ifndef TMS_SPLIT_PFD
+#define TMS_SPLIT_PFD 2  // ... in the query-split kernel, whose tiles are short (16 tokens)
+#endif
+constexpr int kSplitNSub = TMS_SPLIT_NSUB;
 
-template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED>
+template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, bool QSPLIT = false, int NS = kNSub>
 static int launch_one(const DenseArgs& a, int64_t grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((dense_maxsim_kernel<DT, MODE, NQB, KS_REG, FULL, ALIGNED, kNSub>), dim3((unsigned)grid), dim3(256),
-                     lds, st, a);
+  constexpr int kPfd = QSPLIT ? TMS_SPLIT_PFD : TMS_DENSE_PFD;
+  hipLaunchKernelGGL((dense_maxsim_kernel<DT, MODE, NQB, KS_REG, FULL, ALIGNED, NS, QSPLIT, kPfd>),
+                     dim3((unsigned)grid), dim3(256), lds, st, a);
   return check_launch("dense_maxsim_kernel");
+}
+
+// Batched queries with the query fragments in VGPRs: each wave holds up to four
+// 32-token blocks (whole queries), the four waves of a workgroup split up to 16
+// blocks and stream the same documents, so every HBM pass over D scores up to 16
+// blocks. Launches step through the blocks in groups of 4 * per-wave blocks; a
+// query never straddles two waves or two launches.
+template <int DT>
+static int run_split(DenseArgs a, int64_t nQ, hipStream_t st) {
+  const int per_wave = (4 / a.nbq) * a.nbq;
+  const int64_t nblocks_total = nQ * (int64_t)a.nbq;
+  int64_t dpw = a.nd > 0 ? 4096 / a.nd : 64;  // long streams: each wave loads up to 32 KB of queries
+  if (dpw < 1) dpw = 1;
+  if (dpw > 64) dpw = 64;
+  const int64_t min_wgs = (int64_t)256 * 4 * 2;
+  if (dpw > 1 && a.B / dpw < min_wgs) dpw = a.B / min_wgs > 0 ? a.B / min_wgs : 1;
+  a.docs_per_wave = (int32_t)dpw;
+  a.nblk = per_wave;
+  const int64_t grid = (a.B + dpw - 1) / dpw;
+  for (int64_t blk0 = 0; blk0 < nblocks_total; blk0 += 4 * per_wave) {
+    a.blk0 = (int32_t)blk0;
+    a.blk_end = (int32_t)((nblocks_total - blk0 < 4 * per_wave) ? nblocks_total : blk0 + 4 * per_wave);
+    int rc;
+    switch (a.d / 32) {
+      case 1: rc = launch_one<DT, MODE_FIXED, 4, 1, true, true, true, kSplitNSub>(a, grid, 0, st); break;
+      case 2: rc = launch_one<DT, MODE_FIXED, 4, 2, true, true, true, kSplitNSub>(a, grid, 0, st); break;
+      case 3: rc = launch_one<DT, MODE_FIXED, 4, 3, true, true, true, kSplitNSub>(a, grid, 0, st); break;
+      default: rc = launch_one<DT, MODE_FIXED, 4, 4, true, true, true, kSplitNSub>(a, grid, 0, st); break;
+    }
+    if (rc != TMS_OK) return rc;
+  }
+  return TMS_OK;
 }
 
 template <int DT, int MODE, int NQB>
@@ -493,6 +616,11 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   int64_t hint = (mode == MODE_VARLEN) ? (B > 0 ? total_tokens / B : 0) : nd;
   a.docs_per_wave = pick_docs_per_wave(B, hint);
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
+  const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
+  if (mode == MODE_FIXED && qreg && a.nbq <= 4 && nQ * a.nbq >= 4) {
+    if (dtype == TMS_DTYPE_F16) return run_split<TMS_DTYPE_F16>(a, nQ, st);
+    return run_split<TMS_DTYPE_BF16>(a, nQ, st);
+  }
   if (dtype == TMS_DTYPE_F16) return run_dense<TMS_DTYPE_F16>(a, nQ, mode, aligned, st);
   return run_dense<TMS_DTYPE_BF16>(a, nQ, mode, aligned, st);
 }
