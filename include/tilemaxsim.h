@@ -67,6 +67,17 @@ int tms_maxsim_varlen(const void* Q, int64_t nq, int64_t d, const void* D_flat, 
                       const int64_t* offsets, int64_t B, int dtype, float* out, void* stream);
 
 /*
+ * Variable-length MaxSim with the zero-padding semantics of the reference's PLAID
+ * drop-in: each document is scored as if zero-padded to pad_len tokens, so a document
+ * shorter than pad_len also sees dot products of 0 (its per-query-token max is at
+ * least 0, and an empty one scores 0). Nothing is padded in memory.
+ * Replaces flashmaxsim_score_packed (src/plaid_integration_benchmark.py:154-183), which
+ * builds the padded (B, max_len, d) tensor, zeroes its padding and runs the dense kernel.
+ */
+int tms_maxsim_varlen_padded(const void* Q, int64_t nq, int64_t d, const void* D_flat, int64_t total_tokens,
+                             const int64_t* offsets, int64_t B, int64_t pad_len, int dtype, float* out, void* stream);
+
+/*
  * Batched-query dense MaxSim: nQ queries of nq tokens each (Qs is (nQ, nq, d)) scored
  * against the same documents in one pass over D; out is (nQ, B), row-major.
  * Replaces nQ calls of flash_maxsim_v2_multiquery (src/flash_maxsim_v2.py:227-289).

@@ -19,6 +19,8 @@ Reference files followed (paths relative to the reference checkout):
   with -inf of padded doc tokens) -> :func:`maxsim_masked`.
 * ``src/flash_maxsim_kernel.py:248-273`` ``flash_maxsim_multi_doc`` (each document is
   scored over exactly ``D_flat[offsets[i]:offsets[i+1]]``) -> :func:`maxsim_varlen`.
+* ``src/plaid_integration_benchmark.py:154-183`` ``flashmaxsim_score_packed`` (pad the
+  packed documents, zero the padding, dense MaxSim) -> :func:`maxsim_packed_zero_padded`.
 * ``src/flash_pqsim_kernel.py:31-67`` distance table ``T[q,m,k] = sum_j
   Q[q,m*dsub+j] * C[m,k,j]`` in fp32 -> :func:`pq_build_lut`.
 * ``src/flash_pqsim_kernel.py:127-173`` + ``:250`` table gather, fp32 sum over ``m`` in
@@ -159,6 +161,23 @@ def maxsim_varlen(Q: np.ndarray, D_flat: np.ndarray, offsets: np.ndarray, f64: b
     # because the empty docs between them contribute no tokens.
     out[nonempty] = mx.sum(axis=1, dtype=dt)
     return out
+
+
+def maxsim_packed_zero_padded(Q: np.ndarray, D_packed: np.ndarray, lengths: np.ndarray) -> np.ndarray:
+    """The reference's PLAID drop-in (``src/plaid_integration_benchmark.py:160-183``):
+    pad the packed documents to (B, max_len, d), multiply the padding by zero
+    (``D_padded * D_mask``), then the plain MaxSim of ``flash_maxsim_v2_multiquery``.
+    Computed literally (a materialised padded tensor), float64."""
+    lengths = np.asarray(lengths, dtype=np.int64)
+    B = lengths.shape[0]
+    d = D_packed.shape[1]
+    max_len = int(lengths.max()) if B else 0
+    padded = np.zeros((B, max_len, d), dtype=np.float64)
+    start = 0
+    for b in range(B):
+        padded[b, : lengths[b]] = np.asarray(D_packed[start: start + lengths[b]], dtype=np.float64)
+        start += lengths[b]
+    return maxsim_f64(Q, padded)
 
 
 def pq_build_lut(Q: np.ndarray, codebook: np.ndarray) -> np.ndarray:

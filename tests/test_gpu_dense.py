@@ -245,6 +245,31 @@ def test_masked(cuda):
     _assert_scores(got, orc.maxsim_masked(Q, D, mask, f64=True), "masked")
 
 
+@pytest.mark.parametrize("padding", ["zeros", "mask"])
+def test_plaid_packed_dropin(cuda, padding):
+    """flashmaxsim_score_packed (src/plaid_integration_benchmark.py:154-183): zero
+    padding to the longest document, as the reference computes it, or ColBERT's mask."""
+    import torch
+    from tilemaxsim_amd import flashmaxsim_score_packed
+    rng = _rng(41 if padding == "zeros" else 42)
+    lens = rng.integers(0, 90, size=700)
+    lens[5] = 0
+    lens[9] = lens.max()
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    Q = _randn(rng, (1, 32, 128), normalize=True)
+    # anti-aligned documents (negative similarities) make zero padding visible
+    flat = -_randn(rng, (int(offsets[-1]), 128), normalize=True)
+    flat[: int(offsets[-1]) // 2] *= -1
+    got = flashmaxsim_score_packed(torch.from_numpy(Q).cuda(), _to_gpu(flat), torch.from_numpy(lens),
+                                   config=None, padding=padding).cpu().numpy()
+    if padding == "zeros":
+        ref = orc.maxsim_packed_zero_padded(Q[0], flat, lens)
+        assert got[5] == 0.0
+    else:
+        ref = orc.maxsim_varlen(Q[0], flat, offsets, f64=True)
+    _assert_scores(got, ref, f"packed {padding}")
+
+
 def test_batched_queries(cuda):
     import torch
     from tilemaxsim_amd import flash_maxsim_batched_queries, flash_maxsim_v2_multiquery

@@ -271,3 +271,22 @@ def test_planted_pq_transposed_codebook_is_caught():
     codes = rng.integers(0, K, size=(3, 5, M)).astype(np.uint8)
     wrong = orc.pq_decompress_score(Q, np.ascontiguousarray(C.transpose(1, 0, 2)), codes, f64=True)
     assert not np.allclose(wrong, brute_pq(Q, C, codes), rtol=1e-3)
+
+
+def test_packed_zero_padding_pins():
+    """The PLAID drop-in's zero padding: a shorter document's per-token max is at least
+    0; a document at the batch's max length is unaffected; an empty one scores 0."""
+    rng = _rng(14)
+    Q = _h(rng, (6, 16))
+    lens = np.array([3, 7, 0, 7, 1])
+    offsets = np.concatenate([[0], np.cumsum(lens)])
+    flat = _h(rng, (int(offsets[-1]), 16))
+    got = orc.maxsim_packed_zero_padded(Q, flat, lens)
+    for b in range(5):
+        rows = flat[offsets[b]:offsets[b + 1]].astype(np.float64)
+        per_q = [max([float(np.dot(q.astype(np.float64), r)) for r in rows] + ([0.0] if lens[b] < 7 else []))
+                 for q in Q]
+        assert got[b] == pytest.approx(sum(per_q), rel=1e-12, abs=1e-12)
+    full = orc.maxsim_varlen(Q, flat, offsets, f64=True)
+    assert got[1] == pytest.approx(full[1], rel=1e-13) and got[3] == pytest.approx(full[3], rel=1e-13)
+    assert got[2] == 0.0

@@ -15,3 +15,6 @@ __all__ = [
 from .flash_pqsim_kernel import TileMaxSimPQ
 
 __all__.append("TileMaxSimPQ")
+from .plaid import flashmaxsim_score_packed
+
+__all__.append("flashmaxsim_score_packed")

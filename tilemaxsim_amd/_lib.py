@@ -31,6 +31,8 @@ SIGNATURES = {
     "tms_maxsim_dense": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _int, _c_void_p, _c_void_p],
     "tms_maxsim_masked": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _i64, _int, _c_void_p, _c_void_p],
     "tms_maxsim_varlen": [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p, _i64, _int, _c_void_p, _c_void_p],
+    "tms_maxsim_varlen_padded": [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _int, _c_void_p,
+                                 _c_void_p],
     "tms_maxsim_dense_batched": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _int, _c_void_p, _c_void_p],
     "tms_pq_build_lut": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _c_void_p],
     "tms_pq_score_lut": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],

@@ -72,6 +72,7 @@ struct DenseArgs {
   int32_t nblk;            // blocks in this launch (<= NQB template)
   int32_t d, nchunk, nstep, nkg;
   int32_t docs_per_wave;
+  int64_t pad_len;         // varlen: score as if zero-padded to this many tokens (0 = off)
 };
 
 // 16-byte fragment of row `row`, chunk c (elements 8c .. 8c+7), zero outside [0, d).
@@ -239,7 +240,8 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
         c.kg = 0;
         return;
       }
-      write_empty(b, bad ? __builtin_nanf("") : NEG_INF);
+      // an empty document zero-padded to pad_len > 0 tokens has every max equal to 0
+      write_empty(b, bad ? __builtin_nanf("") : (a.pad_len > 0 ? 0.f : NEG_INF));
     }
     c.b = b_end;
   };
@@ -311,7 +313,9 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
       for (int j = 0; j < NQB; j++) acc[sub][j][0] = acc[sub][j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  auto finish_doc = [&](int64_t b) {
+  auto finish_doc = [&](int64_t b, int64_t len) {
+    // zero padding up to pad_len adds dot products equal to 0 to a shorter document
+    const bool padded = (MODE == MODE_VARLEN) && len < a.pad_len;
     float blk[NQB];
 #pragma unroll
     for (int j = 0; j < NQB; j++) {
@@ -321,6 +325,7 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
         float m = rmax[j][h];
         m = fmaxf(m, __shfl_xor(m, 16));
         m = fmaxf(m, __shfl_xor(m, 32));
+        if (padded) m = fmaxf(m, 0.f);
         bool valid;
         (void)q_row(j, h, r, valid);
         s += valid ? m : 0.f;
@@ -356,7 +361,7 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
         fold(rmax[j][0], accb[j][0], 0u);
         fold(rmax[j][1], accb[j][1], 0u);
       }
-      if (c.t0 + TT >= c.len) finish_doc(c.b);
+      if (c.t0 + TT >= c.len) finish_doc(c.b, c.len);
       return;
     } else if constexpr (QREG) {
       // One k-group: each query block is finished before the next, so only one
@@ -379,7 +384,7 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
 #pragma unroll
           for (int h = 0; h < 2; h++) fold(rmax[j][h], acc1[sub][h], MODE == MODE_MASKED ? buf.m[sub] : 0u);
       }
-      if (c.t0 + TT >= c.len) finish_doc(c.b);
+      if (c.t0 + TT >= c.len) finish_doc(c.b, c.len);
       return;
     }
 #pragma unroll
@@ -407,7 +412,7 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
             fold(rmax[j][h], acc[sub][j][h], MODE == MODE_MASKED ? buf.m[sub] : 0u);
             acc[sub][j][h] = f32x4{0.f, 0.f, 0.f, 0.f};
           }
-      if (c.t0 + TT >= c.len) finish_doc(c.b);
+      if (c.t0 + TT >= c.len) finish_doc(c.b, c.len);
     }
   };
 
@@ -578,8 +583,9 @@ static int run_dense(DenseArgs a, int64_t nQ, int mode, bool aligned, hipStream_
 
 static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B,
                        int64_t nd, int64_t total_tokens, const int64_t* offsets, const uint8_t* mask, int mode,
-                       int dtype, float* out, void* stream) {
+                       int dtype, float* out, void* stream, int64_t pad_len = 0) {
   if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16) return fail(TMS_ERR_UNSUPPORTED, "%s: unsupported dtype %d", fn, dtype);
+  if (pad_len < 0) return fail(TMS_ERR_INVALID, "%s: negative pad_len %lld", fn, (long long)pad_len);
   if (nQ < 0 || nq < 0 || d < 0 || B < 0 || nd < 0 || total_tokens < 0)
     return fail(TMS_ERR_INVALID, "%s: negative size (nQ=%lld nq=%lld d=%lld B=%lld nd=%lld T=%lld)", fn, (long long)nQ,
                 (long long)nq, (long long)d, (long long)B, (long long)nd, (long long)total_tokens);
@@ -615,6 +621,7 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   if (a.nkg < 1) a.nkg = 1;
   int64_t hint = (mode == MODE_VARLEN) ? (B > 0 ? total_tokens / B : 0) : nd;
   a.docs_per_wave = pick_docs_per_wave(B, hint);
+  a.pad_len = pad_len;
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
   const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
   if (mode == MODE_FIXED && qreg && a.nbq <= 4 && nQ * a.nbq >= 4) {
@@ -649,6 +656,12 @@ int tms_maxsim_varlen(const void* Q, int64_t nq, int64_t d, const void* D_flat, 
                       const int64_t* offsets, int64_t B, int dtype, float* out, void* stream) {
   return tms::dense_entry("tms_maxsim_varlen", Q, 1, nq, d, D_flat, B, 0, total_tokens, offsets, nullptr,
                           tms::MODE_VARLEN, dtype, out, stream);
+}
+
+int tms_maxsim_varlen_padded(const void* Q, int64_t nq, int64_t d, const void* D_flat, int64_t total_tokens,
+                             const int64_t* offsets, int64_t B, int64_t pad_len, int dtype, float* out, void* stream) {
+  return tms::dense_entry("tms_maxsim_varlen_padded", Q, 1, nq, d, D_flat, B, 0, total_tokens, offsets, nullptr,
+                          tms::MODE_VARLEN, dtype, out, stream, pad_len);
 }
 
 int tms_maxsim_dense_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd,

@@ -1,0 +1,79 @@
+"""PLAID / ColBERT packed-document scoring -- drop-in for the reference's
+``flashmaxsim_score_packed`` (``src/plaid_integration_benchmark.py:154-183``), the
+function the reference monkey-patches over ColBERT's ``colbert_score_packed``.
+
+ColBERT hands the scorer a packed token buffer ``D_packed`` (T, d) plus per-document
+lengths. The reference pads it to (B, max_len, d), multiplies the padding by zero and
+runs its dense kernel, so a document shorter than ``max_len`` also sees zero vectors
+(each query token's max is at least 0). Here the packed buffer is scored in place by
+the variable-length kernel; ``padding="zeros"`` (default) reproduces the reference's
+numbers exactly, and ``padding="mask"`` gives ColBERT's own masked semantics, where
+padding never wins a max.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _check, _lib
+from .flash_maxsim_kernel import flash_maxsim_multi_doc
+
+
+def lengths_to_offsets(D_lengths: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """(B,) integer lengths -> (B + 1,) int64 offsets on ``device`` (computed on device)."""
+    lengths = D_lengths.to(device=device, dtype=torch.int64)
+    offsets = torch.zeros(lengths.numel() + 1, dtype=torch.int64, device=device)
+    torch.cumsum(lengths, 0, out=offsets[1:])
+    return offsets
+
+
+def flashmaxsim_score_packed(Q: torch.Tensor, D_packed: torch.Tensor, D_lengths: torch.Tensor, config=None,
+                             padding: str = "zeros") -> torch.Tensor:
+    """Score one query against packed variable-length documents.
+
+    Args:
+        Q: (1, Nq, d) or (Nq, d) query embeddings (cast to half like the reference).
+        D_packed: (T, d) all document tokens back to back.
+        D_lengths: (B,) tokens per document; they must sum to at most T.
+        config: accepted for signature compatibility with the reference (ColBERT's
+            run config); unused, the tensors' device decides where scoring runs.
+        padding: "zeros" -- score as the reference does after zero-padding every
+            document to the longest one; "mask" -- padding is -inf (ColBERT semantics).
+
+    Returns:
+        (B,) float32 scores on the GPU.
+    """
+    del config
+    if padding not in ("zeros", "mask"):
+        raise ValueError(f"padding must be 'zeros' or 'mask', got {padding!r}")
+    _check.tensor("Q", Q)
+    _check.tensor("D_packed", D_packed)
+    _check.tensor("D_lengths", D_lengths)
+    Q2 = Q.squeeze(0) if Q.dim() == 3 else Q
+    if Q2.dim() != 2 or D_packed.dim() != 2 or D_lengths.dim() != 1:
+        raise ValueError("flashmaxsim_score_packed: Q (1, Nq, d), D_packed (T, d), D_lengths (B,)")
+    if D_lengths.dtype.is_floating_point or D_lengths.dtype == torch.bool:
+        raise TypeError(f"D_lengths must be integer, got {D_lengths.dtype}")
+    if D_packed.dtype != torch.float16:
+        D_packed = D_packed.half()  # the reference scores .half() copies
+    D_packed = D_packed.contiguous()
+    _check.on_gpu("D_packed", D_packed)
+    dev = D_packed.device
+    Q2 = Q2.to(dev).half().contiguous()
+    offsets = lengths_to_offsets(D_lengths, dev)
+    if padding == "mask":
+        return flash_maxsim_multi_doc(Q2, D_packed, offsets)
+    B = offsets.numel() - 1
+    T, d = D_packed.shape
+    assert Q2.shape[1] == d, f"flashmaxsim_score_packed: Q width {Q2.shape[1]} != D width {d}"
+    if B > 0 and (bool((offsets[1:] < offsets[:-1]).any()) or int(offsets[-1]) > T):
+        raise ValueError("flashmaxsim_score_packed: D_lengths must be >= 0 and sum to at most D_packed.shape[0]")
+    pad_len = int(D_lengths.max()) if B > 0 else 0
+    scores = torch.empty(B, dtype=torch.float32, device=dev)
+    if B == 0:
+        return scores
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        _lib.check(lib.tms_maxsim_varlen_padded(Q2.data_ptr(), Q2.shape[0], d, D_packed.data_ptr(), T,
+                                                offsets.data_ptr(), B, pad_len, _lib.TMS_DTYPE_F16,
+                                                scores.data_ptr(), _lib.stream_of(Q2)))
+    return scores
