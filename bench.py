@@ -61,6 +61,12 @@ def normalized_fp16(torch, shape, gen, chunk_rows=1 << 21):
     return out
 
 
+def topk_rows(scores, k):
+    """Per-query top-k of the (queries, docs) score matrix with the HIP top-k kernel."""
+    from tilemaxsim_amd import topk
+    return topk(scores, k)
+
+
 class KernelTimer:
     """HIP events around each launch of the dominant kernel, on the stream it runs on."""
 
@@ -103,7 +109,7 @@ class Dense:
         for i in range(self.nQ):
             s = timer(lambda: flash_maxsim_v2_multiquery(self.Q[i], self.D))
             self.scores[i].copy_(s)
-        return self.torch.topk(self.scores, min(self.k, self.B), dim=1)
+        return topk_rows(self.scores, min(self.k, self.B))
 
     def bytes_per_launch(self):
         return self.Nq * self.d * 2 + self.B * self.Nd * self.d * 2 + self.B * 4
@@ -138,7 +144,7 @@ class DenseBatched(Dense):
         from tilemaxsim_amd import flash_maxsim_batched_queries
         s = timer(lambda: flash_maxsim_batched_queries(self.Q, self.D))
         self.scores.copy_(s)
-        return self.torch.topk(self.scores, min(self.k, self.B), dim=1)
+        return topk_rows(self.scores, min(self.k, self.B))
 
     def flops_per_launch(self):
         return 2 * self.nQ * self.Nq * self.B * self.Nd * self.d
@@ -176,7 +182,7 @@ class Varlen(Dense):
         for i in range(self.nQ):
             s = timer(lambda: flash_maxsim_multi_doc(self.Q[i], self.D, self.offsets, validate=False))
             self.scores[i].copy_(s)
-        return self.torch.topk(self.scores, self.k, dim=1)
+        return topk_rows(self.scores, self.k)
 
     def bytes_per_launch(self):
         return self.Nq * self.d * 2 + self.T * self.d * 2 + (self.B + 1) * 8 + self.B * 4
@@ -216,7 +222,7 @@ class PQ:
         for i in range(self.nQ):
             s = timer(lambda: self.pq.score_batch(self.Q[i], self.codes, validate=False))
             self.scores[i].copy_(s)
-        return self.torch.topk(self.scores, self.k, dim=1)
+        return topk_rows(self.scores, self.k)
 
     def bytes_per_launch(self):
         return self.B * self.Nd * self.M  # code bytes: the north-star roofline for PQ

@@ -110,6 +110,20 @@ int tms_pq_score_lut(const float* lut, int64_t nq, int64_t M, int64_t K, const u
 int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
                  const uint8_t* codes, int64_t B, int64_t nd, float* out, void* stream);
 
+/*
+ * Row-wise top-k of an fp32 score matrix (nrows, n): values (nrows, k) descending with
+ * int64 indices; equal values come out in ascending index order and NaN ranks above
+ * +inf. Needs tms_topk_workspace_size(nrows, n, k) bytes of device workspace (0 when a
+ * row fits one 4096-element chunk). k <= 1024, n < 2^32, nrows <= 65535 per call.
+ * Replaces torch.topk(scores, k) in the reference's retrieval step
+ * (src/cycle3_experiments.py:215).
+ */
+int tms_topk(const float* scores, int64_t nrows, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+             float* out_values, int64_t* out_indices, void* stream);
+
+/* Device workspace in bytes that tms_topk needs for these sizes (0 if none or invalid). */
+int64_t tms_topk_workspace_size(int64_t nrows, int64_t n, int64_t k);
+
 #ifdef __cplusplus
 }
 #endif

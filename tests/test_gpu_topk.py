@@ -1,0 +1,84 @@
+"""GPU top-k (tms_topk) against the oracle's top-k (value descending, ties by lower
+index): bit-exact values and indices, which is the bar for index work."""
+import numpy as np
+import pytest
+
+from oracle import maxsim_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_row(vals, idx, row, k):
+    ev, ei = orc.topk(row, k)
+    assert np.array_equal(idx, ei), (idx[:10], ei[:10])
+    assert np.array_equal(vals.view(np.uint32), ev.astype(np.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (100, 100), (4096, 100), (4097, 100), (50_000, 100), (1_000_000, 100),
+                                 (1_000_000, 1024), (300_000, 7), (16_777_217, 100)])
+def test_topk_matches_oracle(cuda, n, k):
+    import torch
+    from tilemaxsim_amd import topk
+    rng = np.random.default_rng(n + k)
+    x = rng.standard_normal(n).astype(np.float32)
+    v, i = topk(torch.from_numpy(x).cuda(), k)
+    assert v.shape == (k,) and i.dtype == torch.int64
+    _check_row(v.cpu().numpy(), i.cpu().numpy(), x, k)
+
+
+def test_topk_rows_ties_nan_inf(cuda):
+    import torch
+    from tilemaxsim_amd import topk
+    rng = np.random.default_rng(7)
+    rows = np.round(rng.standard_normal((5, 20000)) * 4).astype(np.float32)  # many exact ties
+    rows[1, 17] = np.inf
+    rows[1, 9000] = -np.inf
+    rows[2, :] = -np.inf
+    rows[3, 123] = np.nan
+    rows[4, :] = 0.0
+    v, i = topk(torch.from_numpy(rows).cuda(), 100)
+    v, i = v.cpu().numpy(), i.cpu().numpy()
+    for r in range(5):
+        if r == 3:  # NaN ranks first, then the rest in order
+            assert i[r, 0] == 123 and np.isnan(v[r, 0])
+            rest = rows[r].copy()
+            rest[123] = -np.inf
+            ev, ei = orc.topk(rest, 99)
+            assert np.array_equal(i[r, 1:], ei)
+            continue
+        _check_row(v[r], i[r], rows[r], 100)
+
+
+def test_maxsim_topk_end_to_end(cuda):
+    import torch
+    from tilemaxsim_amd import maxsim_topk
+    rng = np.random.default_rng(3)
+    Qs = rng.standard_normal((4, 32, 128)).astype(np.float32)
+    Qs /= np.linalg.norm(Qs, axis=-1, keepdims=True)
+    D = rng.standard_normal((3000, 40, 128)).astype(np.float32)
+    D /= np.linalg.norm(D, axis=-1, keepdims=True)
+    Qs, D = Qs.astype(np.float16), D.astype(np.float16)
+    v, i = maxsim_topk(torch.from_numpy(Qs).cuda(), torch.from_numpy(D).cuda(), 100)
+    v1, i1 = maxsim_topk(torch.from_numpy(Qs[2]).cuda(), torch.from_numpy(D).cuda(), 100)
+    assert v.shape == (4, 100) and v1.shape == (100,)
+    for q in range(4):
+        ref = orc.maxsim_f64(Qs[q], D)
+        kth = np.sort(ref)[::-1][99]
+        diff = set(i[q].cpu().numpy().tolist()) ^ set(orc.topk(ref, 100)[1].tolist())
+        for d in diff:  # only swaps among scores within tolerance of the 100th
+            assert abs(ref[d] - kth) <= 1e-3 * abs(kth) + 1e-3
+    assert np.array_equal(i1.cpu().numpy(), i[2].cpu().numpy())
+
+
+def test_topk_errors(cuda):
+    import torch
+    from tilemaxsim_amd import topk
+    x = torch.zeros(10, device="cuda")
+    with pytest.raises(ValueError):
+        topk(x, 11)
+    with pytest.raises(TypeError):
+        topk(x.double(), 3)
+    with pytest.raises(NotImplementedError):
+        topk(torch.zeros(5000, device="cuda"), 2000)
+    v, i = topk(x, 0)
+    assert v.shape == (0,)

@@ -75,6 +75,20 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert rc == 2 and "LDS" in msg
 
 
+def test_topk_workspace_sizes():
+    from tilemaxsim_amd import _lib
+    lib = _lib.load()
+    assert lib.tms_topk_workspace_size(1, 4096, 100) == 0          # one chunk: no workspace
+    assert lib.tms_topk_workspace_size(1, 4097, 100) == 2 * 100 * 8  # 2 chunks x k keys
+    # 1M: 245 chunks -> 24500 keys -> 6 chunks -> 600 keys; ping-pong buffers, 3 rows
+    assert lib.tms_topk_workspace_size(3, 1_000_000, 100) == (24500 + 600) * 3 * 8
+    assert lib.tms_topk_workspace_size(1, 10, 11) == 0 and lib.tms_topk_workspace_size(1, 10**6, 2000) == 0
+    rc, msg = _c_call("tms_topk", 16, 1, 10, 11, None, 0, 16, 16, None)
+    assert rc == 1 and "exceeds" in msg
+    rc, msg = _c_call("tms_topk", 16, 1, 10**6, 100, None, 0, 16, 16, None)
+    assert rc == 1 and "workspace" in msg
+
+
 def test_python_errors_before_device_checks():
     from tilemaxsim_amd import (TileMaxSimPQ, flash_maxsim_multi_doc, flash_maxsim_single,
                                 flash_maxsim_v2_multiquery, maxsim_score)

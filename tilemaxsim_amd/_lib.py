@@ -37,7 +37,10 @@ SIGNATURES = {
     "tms_pq_build_lut": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _c_void_p],
     "tms_pq_score_lut": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tms_pq_score": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
+    "tms_topk": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p],
+    "tms_topk_workspace_size": [_i64, _i64, _i64],
 }
+RESTYPES = {"tms_topk_workspace_size": ctypes.c_int64}
 
 _lib = None
 _lock = threading.Lock()
@@ -65,7 +68,7 @@ def load() -> ctypes.CDLL:
             if fn is None:
                 continue  # calling it raises AttributeError
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         lib.tms_last_error.argtypes = []
         lib.tms_last_error.restype = ctypes.c_char_p
         _lib = lib
