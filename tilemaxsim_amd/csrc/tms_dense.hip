@@ -30,8 +30,14 @@
 #ifndef TMS_SPLIT_INTERLEAVE
 #define TMS_SPLIT_INTERLEAVE 1  // query-split kernel: interleave the MFMA chains of all its blocks
 #endif
+#ifndef TMS_USE_STREAM
+#define TMS_USE_STREAM 1  // fixed-length d <= 128: use stream_maxsim_kernel (tms_stream.hip)
+#endif
 
 namespace tms {
+
+int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype,
+               float* out, hipStream_t st);
 
 static thread_local char g_err[512];
 
@@ -176,17 +182,30 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
   const float NEG_INF = -__builtin_inff();
 
   // ---- per-query output ------------------------------------------------------
+  // Scores are staged in registers, lane i holding document b_begin + i (a wave owns at
+  // most 64 documents), and stored once after the loop with coalesced writes. Keeping
+  // stores out of the loop keeps the memory-counter waits exact, so the tile loads in
+  // flight are not drained at every document boundary.
+  float pend[NQB];
+#pragma unroll
+  for (int j = 0; j < NQB; j++) pend[j] = 0.f;
+  auto stage = [&](int64_t b, const float (&blk)[NQB]) {
+    const bool mine = lane == (int)(b - b_begin);
+#pragma unroll
+    for (int j = 0; j < NQB; j++) pend[j] = mine ? blk[j] : pend[j];
+  };
   // Block sums are added per query; a query whose first block precedes this wave's
   // blocks accumulates onto the previous launch's partial score.
-  auto write_doc = [&](int64_t b, const float (&blk)[NQB]) {
-    if (lane == 0) {
+  auto flush = [&]() {
+    if (lane < b_end - b_begin) {
+      const int64_t b = b_begin + lane;
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < NQB; j++) {
         if (j >= my_nblk) break;
         int jb = my_blk0 + j;
         int qi = jb / a.nbq;
-        s += blk[j];
+        s += pend[j];
         bool last_of_query = (j == my_nblk - 1) || ((jb + 1) / a.nbq != qi);
         if (last_of_query) {
           float* o = a.out + (int64_t)qi * a.B + b;
@@ -201,11 +220,8 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
   auto write_empty = [&](int64_t b, float v) {
     float blk[NQB];
 #pragma unroll
-    for (int j = 0; j < NQB; j++) {
-      // -inf for every block that holds a real token (all blocks in range do)
-      blk[j] = v;
-    }
-    write_doc(b, blk);
+    for (int j = 0; j < NQB; j++) blk[j] = v;  // every block in range holds a real token
+    stage(b, blk);
   };
 
   // ---- document cursor -------------------------------------------------------
@@ -337,27 +353,26 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
       blk[j] = s;
       rmax[j][0] = rmax[j][1] = NEG_INF;
     }
-    write_doc(b, blk);
+    stage(b, blk);
   };
 
   auto compute_tile = [&](const Buf& buf, const Cursor& c) {
     if constexpr (QREG && QSPLIT && NSUB == 1 && TMS_SPLIT_INTERLEAVE) {
       // All of this wave's query blocks at once: 2 * NQB independent accumulator chains
-      // keep the MFMA pipe busy (the query-split kernel is MFMA-bound).
+      // keep the MFMA pipe busy (the query-split kernel is MFMA-bound). Straight-line
+      // code: blocks past my_nblk (only in a launch's last, partial wave) have zero query
+      // fragments and are never written out, so they need no branch.
       f32x4 accb[NQB][2];
 #pragma unroll
       for (int j = 0; j < NQB; j++) accb[j][0] = accb[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; s++)
 #pragma unroll
-        for (int j = 0; j < NQB; j++) {
-          if (j >= my_nblk) break;
+        for (int j = 0; j < NQB; j++)
 #pragma unroll
           for (int h = 0; h < 2; h++) accb[j][h] = mfma16x16x32<DT>(buf.f[0][s], qf[j][s][h], accb[j][h]);
-        }
 #pragma unroll
       for (int j = 0; j < NQB; j++) {
-        if (j >= my_nblk) break;
         fold(rmax[j][0], accb[j][0], 0u);
         fold(rmax[j][1], accb[j][1], 0u);
       }
@@ -419,33 +434,40 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
   // ---- pipelined main loop -----------------------------------------------------
   // A ring of PFD + 1 tile buffers: the loads of the next PFD tiles are in flight
   // while a tile is scored. The ring is unrolled so every buffer index is static.
+  // Loads are issued unconditionally: past the end of the wave's documents they re-read
+  // the first tile (results unused), so every iteration issues the same number of loads
+  // and the compiler's memory-counter waits stay exact.
   Cursor next;
   seek(next, b_begin);
-  if (next.b >= b_end) return;
+  if (next.b >= b_end) {
+    flush();
+    return;
+  }
+  const Cursor first = next;
   Buf ring[PFD + 1];
   Cursor at[PFD + 1];
+  auto issue = [&](int slot) {
+    at[slot] = next;
+    const bool live = next.b < b_end;
+    load_tile(ring[slot], live ? next : first);
+    if (live) advance(next);
+  };
 #pragma unroll
-  for (int k = 0; k < PFD; k++) {
-    at[k] = next;
-    if (next.b < b_end) {
-      load_tile(ring[k], next);
-      advance(next);
-    }
-  }
-  while (true) {
+  for (int k = 0; k < PFD; k++) issue(k);
+  bool done = false;
+  while (!done) {
 #pragma unroll
     for (int k = 0; k <= PFD; k++) {
       constexpr int kPf = PFD;
-      const int slot_in = (k + kPf) % (kPf + 1);
-      at[slot_in] = next;
-      if (next.b < b_end) {
-        load_tile(ring[slot_in], next);
-        advance(next);
+      issue((k + kPf) % (kPf + 1));
+      if (at[k].b >= b_end) {
+        done = true;
+        break;
       }
-      if (at[k].b >= b_end) return;
       compute_tile(ring[k], at[k]);
     }
   }
+  flush();
 }
 
 // Writes v into out[0..n).
@@ -624,6 +646,7 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   a.pad_len = pad_len;
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
   const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
+  if (TMS_USE_STREAM && mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, dtype, out, st);
   if (mode == MODE_FIXED && qreg && a.nbq <= 4 && nQ * a.nbq >= 4) {
     if (dtype == TMS_DTYPE_F16) return run_split<TMS_DTYPE_F16>(a, nQ, st);
     return run_split<TMS_DTYPE_BF16>(a, nQ, st);

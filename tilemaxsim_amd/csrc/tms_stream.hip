@@ -1,0 +1,286 @@
+// Fixed-length dense MaxSim, d <= 128, query fragments in VGPRs: the streaming kernel
+// with a control-flow shape the compiler's memory-counter tracking follows exactly.
+//
+// The general kernel (tms_dense.hip) walks documents with a cursor whose branches make
+// the compiler drain every outstanding load before each tile. Here:
+//  * documents are fixed length, so a wave's tiles are a flat sequence; each document
+//    is padded to a multiple of R = PFD + 1 tiles with clamped duplicates of its last
+//    token (a duplicate cannot change a max), so every document starts at ring slot 0;
+//  * the inner loop body is straight-line and unrolled R times: it issues the loads of
+//    tile g + PFD (index clamped to the last tile, so the count never varies) and scores
+//    tile g from the ring; the per-document reduction sits between inner loops;
+//  * scores are staged in registers (lane i holds document i of the wave's run) and
+//    stored once, coalesced, after the loop.
+// Two work splits:
+//  * SPLIT = false: every wave streams its own documents with the same query blocks.
+//  * SPLIT = true: the four waves of a workgroup stream the same documents and each owns
+//    a.nblk query blocks (whole queries), so one HBM pass serves up to 16 blocks.
+//
+// Semantics as tms_dense.hip: fp32 accumulation, query rows past nq contribute 0, an
+// empty document scores -inf.
+#include "tms_common.h"
+
+namespace tms {
+
+struct StreamArgs {
+  const uint8_t* Q;  // (nQ * nq, d)
+  const uint8_t* D;  // (B, nd, d)
+  float* out;        // (nQ, B)
+  int64_t B, nd;
+  int32_t nq, nbq;   // tokens per query, 32-token blocks per query
+  int32_t blk0;      // first global query block of this launch
+  int32_t blk_end;   // one past the last block of this launch
+  int32_t nblk;      // blocks per wave
+  int32_t d;         // 32 * KS
+  int32_t docs_per_wave;  // documents per wave (per workgroup when SPLIT); <= 64
+};
+
+template <int DT, int KS, int NB, int PFD, bool SPLIT, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES, SPLIT ? 2 : 1) stream_maxsim_kernel(StreamArgs a) {
+  constexpr int R = PFD + 1;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int wid = threadIdx.x >> 6;
+  const float NEG_INF = -__builtin_inff();
+
+  const int my_blk0 = SPLIT ? a.blk0 + wid * a.nblk : a.blk0;
+  int my_nblk = a.blk_end - my_blk0;
+  if (my_nblk > a.nblk) my_nblk = a.nblk;
+  if (my_nblk <= 0) return;
+
+  const int64_t unit = SPLIT ? (int64_t)blockIdx.x : (int64_t)blockIdx.x * WAVES + wid;
+  const int64_t b_begin = unit * a.docs_per_wave;
+  if (b_begin >= a.B) return;
+  const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
+  const int64_t ndocs = b_end - b_begin;
+
+  // query fragments: block j, half h, step s -> token 16h + r of the block, chunk 4s + g
+  auto q_valid = [&](int j, int h, int64_t& row) -> bool {
+    const int jb = my_blk0 + j;
+    const int qi = jb / a.nbq;
+    const int tok = (jb - qi * a.nbq) * 32 + 16 * h + r;
+    row = (int64_t)qi * a.nq + tok;
+    return j < my_nblk && tok < a.nq;
+  };
+  u32x4 qf[NB][KS][2];
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      int64_t row;
+      const bool v = q_valid(j, h, row);
+#pragma unroll
+      for (int s = 0; s < KS; s++)
+        qf[j][s][h] = v ? *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2) : u32x4{0u, 0u, 0u, 0u};
+    }
+
+  float pend[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) pend[j] = NEG_INF;
+
+  if (a.nd > 0) {
+    const int64_t tiles = (a.nd + 15) / 16;
+    const int64_t tpd = (tiles + R - 1) / R * R;  // tiles per document, padded to a multiple of R
+    const int64_t total = ndocs * tpd;
+    const int64_t row_bytes = (int64_t)a.d * 2;
+    const uint8_t* base = a.D + b_begin * a.nd * row_bytes + (int64_t)(8 * g) * 2;
+
+    // Address of this lane's token row for tile (doc offset dd, tile t).
+    auto tile_ptr = [&](int64_t dd, int64_t t) -> const uint8_t* {
+      int64_t tok = t * 16 + r;
+      if (tok > a.nd - 1) tok = a.nd - 1;
+      return base + (dd * a.nd + tok) * row_bytes;
+    };
+    // Prefetch cursor: tile index pf = pd * tpd + pt, saturating at the last tile.
+    int64_t pd = 0, pt = 0, pf = 0;
+    auto pf_next = [&]() {
+      const bool more = pf < total - 1;
+      pf += more ? 1 : 0;
+      pt += more ? 1 : 0;
+      const bool wrap = pt == tpd;
+      pt = wrap ? 0 : pt;
+      pd += wrap ? 1 : 0;
+    };
+
+    u32x4 ring[R][KS];
+    auto load = [&](u32x4 (&buf)[KS]) {
+      const uint8_t* p = tile_ptr(pd, pt);
+#pragma unroll
+      for (int s = 0; s < KS; s++) buf[s] = *(const u32x4*)(p + 64 * s);
+    };
+#pragma unroll
+    for (int k = 0; k < PFD; k++) {
+      load(ring[k]);
+      pf_next();
+    }
+
+    float rmax[NB][2];
+    auto score = [&](const u32x4 (&buf)[KS]) {
+      f32x4 acc[NB][2];
+#pragma unroll
+      for (int j = 0; j < NB; j++) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+          for (int h = 0; h < 2; h++) acc[j][h] = mfma16x16x32<DT>(buf[s], qf[j][s][h], acc[j][h]);
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+          rmax[j][h] = fmaxf(rmax[j][h], fmaxf(fmaxf(acc[j][h][0], acc[j][h][1]), fmaxf(acc[j][h][2], acc[j][h][3])));
+    };
+
+    for (int64_t dd = 0; dd < ndocs; dd++) {
+#pragma unroll
+      for (int j = 0; j < NB; j++) rmax[j][0] = rmax[j][1] = NEG_INF;
+      for (int64_t t = 0; t < tpd; t += R) {
+#pragma unroll
+        for (int k = 0; k < R; k++) {
+          load(ring[(k + PFD) % R]);
+          pf_next();
+          score(ring[k]);
+        }
+      }
+      // document done: max over the 64 rows of each column, sum over query tokens
+      float blk[NB];
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        float s = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          float m = rmax[j][h];
+          m = fmaxf(m, __shfl_xor(m, 16));
+          m = fmaxf(m, __shfl_xor(m, 32));
+          int64_t row;
+          s += q_valid(j, h, row) ? m : 0.f;
+        }
+        s += __shfl_xor(s, 8);
+        s += __shfl_xor(s, 4);
+        s += __shfl_xor(s, 2);
+        s += __shfl_xor(s, 1);
+        blk[j] = s;
+      }
+      const bool mine = lane == (int)dd;
+#pragma unroll
+      for (int j = 0; j < NB; j++) pend[j] = mine ? blk[j] : pend[j];
+    }
+  }
+
+  // coalesced store: lane i writes document b_begin + i, per query (blocks of one query
+  // summed in order; a query that began in an earlier launch accumulates)
+  if (lane < ndocs) {
+    const int64_t b = b_begin + lane;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      if (j >= my_nblk) break;
+      const int jb = my_blk0 + j;
+      const int qi = jb / a.nbq;
+      s += pend[j];
+      if (j == my_nblk - 1 || (jb + 1) / a.nbq != qi) {
+        float* o = a.out + (int64_t)qi * a.B + b;
+        *o = (qi * a.nbq < my_blk0) ? *o + s : s;
+        s = 0.f;
+      }
+    }
+  }
+}
+
+#ifndef TMS_STREAM_PFD
+#define TMS_STREAM_PFD 2  // tiles in flight ahead of the one being scored (single-query path)
+#endif
+#ifndef TMS_STREAM_SPLIT_PFD
+#define TMS_STREAM_SPLIT_PFD 2  // ... batched-query path
+#endif
+#ifndef TMS_SPLIT_WAVES
+#define TMS_SPLIT_WAVES 4  // waves per workgroup sharing documents in the batched-query path
+#endif
+#ifndef TMS_SPLIT_BLOCKS
+#define TMS_SPLIT_BLOCKS 4  // query blocks held in VGPRs per wave in the batched-query path
+#endif
+#ifndef TMS_STREAM_TOKENS_PER_WAVE
+#define TMS_STREAM_TOKENS_PER_WAVE 192
+#endif
+
+template <int DT, int KS, int NB, bool SPLIT>
+static int stream_launch(const StreamArgs& a, int64_t grid, hipStream_t st) {
+  constexpr int kPfd = SPLIT ? TMS_STREAM_SPLIT_PFD : TMS_STREAM_PFD;
+  constexpr int kWaves = SPLIT ? TMS_SPLIT_WAVES : 4;
+  hipLaunchKernelGGL((stream_maxsim_kernel<DT, KS, NB, kPfd, SPLIT, kWaves>), dim3((unsigned)grid), dim3(64 * kWaves), 0,
+                     st, a);
+  return check_launch("stream_maxsim_kernel");
+}
+
+template <int DT, int NB, bool SPLIT>
+static int stream_ks(const StreamArgs& a, int64_t grid, hipStream_t st) {
+  switch (a.d / 32) {
+    case 1: return stream_launch<DT, 1, NB, SPLIT>(a, grid, st);
+    case 2: return stream_launch<DT, 2, NB, SPLIT>(a, grid, st);
+    case 3: return stream_launch<DT, 3, NB, SPLIT>(a, grid, st);
+    default: return stream_launch<DT, 4, NB, SPLIT>(a, grid, st);
+  }
+}
+
+// Entry used by tms_dense.hip for fixed-length documents with d in {32, 64, 96, 128},
+// 16-byte aligned Q and D. nQ queries of nq tokens; out is (nQ, B).
+int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype,
+               float* out, hipStream_t st) {
+  StreamArgs a;
+  a.Q = (const uint8_t*)Q;
+  a.D = (const uint8_t*)D;
+  a.out = out;
+  a.B = B;
+  a.nd = nd;
+  a.nq = (int32_t)nq;
+  a.nbq = (int32_t)((nq + 31) / 32);
+  a.d = (int32_t)d;
+  const int64_t nblocks = nQ * (int64_t)a.nbq;
+  const bool split = a.nbq <= TMS_SPLIT_BLOCKS && nblocks >= 4;
+  if (split) {
+    const int per_wave = (TMS_SPLIT_BLOCKS / a.nbq) * a.nbq;
+    int64_t dpw = nd > 0 ? 4096 / nd : 64;  // long streams: each wave loads up to 32 KB of queries
+    if (dpw < 1) dpw = 1;
+    if (dpw > 64) dpw = 64;
+    const int64_t min_wgs = (int64_t)256 * 4 * 2;
+    if (dpw > 1 && B / dpw < min_wgs) dpw = B / min_wgs > 0 ? B / min_wgs : 1;
+    a.docs_per_wave = (int32_t)dpw;
+    a.nblk = per_wave;
+    const int64_t grid = (B + dpw - 1) / dpw;
+    const int64_t per_launch = (int64_t)TMS_SPLIT_WAVES * per_wave;
+    for (int64_t b0 = 0; b0 < nblocks; b0 += per_launch) {
+      a.blk0 = (int32_t)b0;
+      a.blk_end = (int32_t)(nblocks - b0 < per_launch ? nblocks : b0 + per_launch);
+      const int rc = dtype == TMS_DTYPE_F16 ? stream_ks<TMS_DTYPE_F16, TMS_SPLIT_BLOCKS, true>(a, grid, st)
+                                            : stream_ks<TMS_DTYPE_BF16, TMS_SPLIT_BLOCKS, true>(a, grid, st);
+      if (rc) return rc;
+    }
+    return TMS_OK;
+  }
+  int64_t dpw = nd > 0 ? TMS_STREAM_TOKENS_PER_WAVE / nd : 1;
+  const int64_t min_waves = (int64_t)256 * 16 * 2;
+  if (dpw > 1 && B / dpw < min_waves) dpw = B / min_waves;
+  if (dpw < 1) dpw = 1;
+  if (dpw > 64) dpw = 64;
+  a.docs_per_wave = (int32_t)dpw;
+  const int64_t waves = (B + dpw - 1) / dpw;
+  const int64_t grid = (waves + 3) / 4;
+  for (int64_t b0 = 0; b0 < nblocks; b0 += 2) {  // two query blocks per pass over D
+    a.blk0 = (int32_t)b0;
+    a.blk_end = (int32_t)(nblocks - b0 < 2 ? nblocks : b0 + 2);
+    a.nblk = a.blk_end - a.blk0;
+    int rc;
+    if (a.nblk == 2) {
+      rc = dtype == TMS_DTYPE_F16 ? stream_ks<TMS_DTYPE_F16, 2, false>(a, grid, st)
+                                  : stream_ks<TMS_DTYPE_BF16, 2, false>(a, grid, st);
+    } else {
+      rc = dtype == TMS_DTYPE_F16 ? stream_ks<TMS_DTYPE_F16, 1, false>(a, grid, st)
+                                  : stream_ks<TMS_DTYPE_BF16, 1, false>(a, grid, st);
+    }
+    if (rc) return rc;
+  }
+  return TMS_OK;
+}
+
+}  // namespace tms
