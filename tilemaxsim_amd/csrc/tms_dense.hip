@@ -182,30 +182,19 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
   const float NEG_INF = -__builtin_inff();
 
   // ---- per-query output ------------------------------------------------------
-  // Scores are staged in registers, lane i holding document b_begin + i (a wave owns at
-  // most 64 documents), and stored once after the loop with coalesced writes. Keeping
-  // stores out of the loop keeps the memory-counter waits exact, so the tile loads in
-  // flight are not drained at every document boundary.
-  float pend[NQB];
-#pragma unroll
-  for (int j = 0; j < NQB; j++) pend[j] = 0.f;
-  auto stage = [&](int64_t b, const float (&blk)[NQB]) {
-    const bool mine = lane == (int)(b - b_begin);
-#pragma unroll
-    for (int j = 0; j < NQB; j++) pend[j] = mine ? blk[j] : pend[j];
-  };
   // Block sums are added per query; a query whose first block precedes this wave's
-  // blocks accumulates onto the previous launch's partial score.
-  auto flush = [&]() {
-    if (lane < b_end - b_begin) {
-      const int64_t b = b_begin + lane;
+  // blocks accumulates onto the previous launch's partial score. (The fixed-length
+  // d <= 128 path, stream_maxsim_kernel, stages scores and stores them coalesced; this
+  // general path writes each document's score when it finishes.)
+  auto stage = [&](int64_t b, const float (&blk)[NQB]) {
+    if (lane == 0) {
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < NQB; j++) {
         if (j >= my_nblk) break;
         int jb = my_blk0 + j;
         int qi = jb / a.nbq;
-        s += pend[j];
+        s += blk[j];
         bool last_of_query = (j == my_nblk - 1) || ((jb + 1) / a.nbq != qi);
         if (last_of_query) {
           float* o = a.out + (int64_t)qi * a.B + b;
@@ -434,40 +423,33 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
   // ---- pipelined main loop -----------------------------------------------------
   // A ring of PFD + 1 tile buffers: the loads of the next PFD tiles are in flight
   // while a tile is scored. The ring is unrolled so every buffer index is static.
-  // Loads are issued unconditionally: past the end of the wave's documents they re-read
-  // the first tile (results unused), so every iteration issues the same number of loads
-  // and the compiler's memory-counter waits stay exact.
   Cursor next;
   seek(next, b_begin);
-  if (next.b >= b_end) {
-    flush();
-    return;
-  }
-  const Cursor first = next;
+  if (next.b >= b_end) return;
   Buf ring[PFD + 1];
   Cursor at[PFD + 1];
-  auto issue = [&](int slot) {
-    at[slot] = next;
-    const bool live = next.b < b_end;
-    load_tile(ring[slot], live ? next : first);
-    if (live) advance(next);
-  };
 #pragma unroll
-  for (int k = 0; k < PFD; k++) issue(k);
-  bool done = false;
-  while (!done) {
+  for (int k = 0; k < PFD; k++) {
+    at[k] = next;
+    if (next.b < b_end) {
+      load_tile(ring[k], next);
+      advance(next);
+    }
+  }
+  while (true) {
 #pragma unroll
     for (int k = 0; k <= PFD; k++) {
       constexpr int kPf = PFD;
-      issue((k + kPf) % (kPf + 1));
-      if (at[k].b >= b_end) {
-        done = true;
-        break;
+      const int slot_in = (k + kPf) % (kPf + 1);
+      at[slot_in] = next;
+      if (next.b < b_end) {
+        load_tile(ring[slot_in], next);
+        advance(next);
       }
+      if (at[k].b >= b_end) return;
       compute_tile(ring[k], at[k]);
     }
   }
-  flush();
 }
 
 // Writes v into out[0..n).

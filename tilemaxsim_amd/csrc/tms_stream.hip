@@ -91,7 +91,8 @@ __global__ void __launch_bounds__(64 * WAVES, SPLIT ? 2 : 1) stream_maxsim_kerne
       if (tok > a.nd - 1) tok = a.nd - 1;
       return base + (dd * a.nd + tok) * row_bytes;
     };
-    // Prefetch cursor: tile index pf = pd * tpd + pt, saturating at the last tile.
+    // Prefetch cursor: tile index pf = pd * tpd + pt, saturating at the last tile (the
+    // prefetches past the end re-read it, L1-resident, so each iteration issues KS loads).
     int64_t pd = 0, pt = 0, pf = 0;
     auto pf_next = [&]() {
       const bool more = pf < total - 1;
