@@ -98,6 +98,8 @@ class Dense:
     def __init__(self, torch, n_queries, B, Nd, d, Nq=32, name="c2", topk=100):
         self.torch, self.nQ, self.B, self.Nd, self.d, self.Nq, self.k = torch, n_queries, B, Nd, d, Nq, topk
         self.name = name
+        # fixed-length documents with d in {32, 64, 96, 128} run the streaming kernel
+        self.kernel = "stream_maxsim_kernel" if d <= 128 and d % 32 == 0 else "dense_maxsim_kernel"
         gen = torch.Generator(device="cuda").manual_seed(1234)
         log(f"[bench] generating {B} docs x {Nd} x {d} fp16 ({B * Nd * d * 2 / 1e9:.2f} GB)")
         self.D = normalized_fp16(torch, (B, Nd, d), gen)
@@ -137,7 +139,6 @@ class DenseBatched(Dense):
     """C2 data, all queries scored by the batched-query entry point: each workgroup's
     four waves hold 16 query blocks and share one HBM pass over the documents, which
     moves the path from the HBM roof to the MFMA roof."""
-    kernel = "dense_maxsim_kernel"
     MFMA_PEAK_TFLOPS = 2500.0
 
     def step(self, timer):

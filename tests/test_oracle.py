@@ -228,6 +228,34 @@ def test_topk_ties_break_by_index():
     assert i.tolist() == [1, 2, 3] and v.tolist() == [3.0, 3.0, 2.0]
 
 
+def _brute_topk(x, k):
+    order = sorted(range(len(x)), key=lambda j: (-float(x[j]), j))[:k]
+    return [float(x[j]) for j in order], order
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (7, 7), (50, 10), (300, 100)])
+def test_topk_matches_brute_force_and_sort(n, k):
+    rng = _rng(n + k)
+    x = np.round(rng.standard_normal(n) * 3).astype(np.float32)  # many exact ties
+    x[rng.integers(0, n)] = np.inf
+    x[rng.integers(0, n)] = -np.inf
+    v, i = orc.topk(x, k)
+    bv, bi = _brute_topk(x, k)
+    assert i.tolist() == bi and v.tolist() == bv
+    assert np.array_equal(v, np.sort(x)[::-1][:k])  # values: the library sort
+    rest = np.delete(x, i)
+    assert rest.size == 0 or rest.max() <= v.min()  # nothing left out beats what was kept
+
+
+def test_planted_topk_mistakes_are_caught():
+    x = np.array([2.0, 5.0, 5.0, 1.0, 5.0, 3.0], dtype=np.float32)
+    bv, bi = _brute_topk(x, 4)
+    ascending = np.argsort(x, kind="stable")[:4]
+    ties_high_first = np.argsort(x, kind="stable")[::-1][:4]  # ties by the higher index
+    assert ascending.tolist() != bi and ties_high_first.tolist() != bi
+    assert orc.topk(x, 4)[1].tolist() == bi == [1, 2, 4, 5]
+
+
 # ---------------------------------------------------------------- planted mistakes
 # Each mutant is a plausible oracle bug; the pins above must reject it.
 def _mut_sum_instead_of_max(Q, D):

@@ -27,15 +27,9 @@
 
 #include "tms_common.h"
 
-#ifndef TMS_SPLIT_INTERLEAVE
-#define TMS_SPLIT_INTERLEAVE 1  // query-split kernel: interleave the MFMA chains of all its blocks
-#endif
-#ifndef TMS_USE_STREAM
-#define TMS_USE_STREAM 1  // fixed-length d <= 128: use stream_maxsim_kernel (tms_stream.hip)
-#endif
-
 namespace tms {
 
+// Fixed-length documents with d in {32, 64, 96, 128} (tms_stream.hip).
 int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype,
                float* out, hipStream_t st);
 
@@ -74,7 +68,6 @@ struct DenseArgs {
   int32_t nq;              // tokens per query
   int32_t nbq;             // 32-token blocks per query = ceil(nq / 32)
   int32_t blk0;            // first global query block of this launch
-  int32_t blk_end;         // query-split launches: one past the last block of the launch
   int32_t nblk;            // blocks in this launch (<= NQB template)
   int32_t d, nchunk, nstep, nkg;
   int32_t docs_per_wave;
@@ -113,29 +106,19 @@ struct Cursor {
 
 // KS_REG > 0: Q fragments in VGPRs, d == 32 * KS_REG (single k-group).
 // KS_REG == 0: Q fragments in LDS, k-groups of 4 steps (128 dims), any d.
-// QSPLIT (Q in VGPRs only): the four waves of a workgroup stream the same documents
-// and each owns its own a.nblk query blocks (the launch covers 4 * a.nblk blocks,
-// whole queries per wave), so one HBM pass over D serves many queries; the
-// repeated document reads of the other waves are served by L1/L2.
-template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, int NSUB, bool QSPLIT, int PFD>
-__global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(DenseArgs a) {
+template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, int NSUB, int PFD>
+__global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
   constexpr bool QREG = KS_REG > 0;
   constexpr int KS = QREG ? KS_REG : 4;
   constexpr int TT = 16 * NSUB;
-  static_assert(!QSPLIT || QREG, "query splitting needs the query fragments in VGPRs");
   extern __shared__ u32x4 qlds[];
 
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g = lane >> 4;
   const int wid = threadIdx.x >> 6;
 
-  // Query blocks of this wave: [my_blk0, my_blk0 + my_nblk).
-  int my_blk0 = a.blk0, my_nblk = a.nblk;
-  if constexpr (QSPLIT) {
-    my_blk0 = a.blk0 + wid * a.nblk;
-    const int left = a.blk_end - my_blk0;
-    my_nblk = left < 0 ? 0 : (left < a.nblk ? left : a.nblk);
-  }
+  // Query blocks of this launch: [my_blk0, my_blk0 + my_nblk).
+  const int my_blk0 = a.blk0, my_nblk = a.nblk;
 
   // ---- query fragments -------------------------------------------------------
   // Fragment (block j, step S, half h) for this lane: query row of block j, token
@@ -174,7 +157,7 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
     __syncthreads();
   }
 
-  const int64_t wave = QSPLIT ? (int64_t)blockIdx.x : (int64_t)blockIdx.x * (blockDim.x >> 6) + wid;
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + wid;
   const int64_t b_begin = wave * a.docs_per_wave;
   if (b_begin >= a.B || my_nblk <= 0) return;
   const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
@@ -183,10 +166,9 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
 
   // ---- per-query output ------------------------------------------------------
   // Block sums are added per query; a query whose first block precedes this wave's
-  // blocks accumulates onto the previous launch's partial score. (The fixed-length
-  // d <= 128 path, stream_maxsim_kernel, stages scores and stores them coalesced; this
-  // general path writes each document's score when it finishes.)
-  auto stage = [&](int64_t b, const float (&blk)[NQB]) {
+  // blocks accumulates onto the previous launch's partial score. Lane 0 writes each
+  // document's score when the document finishes.
+  auto write_doc = [&](int64_t b, const float (&blk)[NQB]) {
     if (lane == 0) {
       float s = 0.f;
 #pragma unroll
@@ -210,7 +192,7 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
     float blk[NQB];
 #pragma unroll
     for (int j = 0; j < NQB; j++) blk[j] = v;  // every block in range holds a real token
-    stage(b, blk);
+    write_doc(b, blk);
   };
 
   // ---- document cursor -------------------------------------------------------
@@ -342,32 +324,11 @@ __global__ void __launch_bounds__(256, QSPLIT ? 2 : 1) dense_maxsim_kernel(Dense
       blk[j] = s;
       rmax[j][0] = rmax[j][1] = NEG_INF;
     }
-    stage(b, blk);
+    write_doc(b, blk);
   };
 
   auto compute_tile = [&](const Buf& buf, const Cursor& c) {
-    if constexpr (QREG && QSPLIT && NSUB == 1 && TMS_SPLIT_INTERLEAVE) {
-      // All of this wave's query blocks at once: 2 * NQB independent accumulator chains
-      // keep the MFMA pipe busy (the query-split kernel is MFMA-bound). Straight-line
-      // code: blocks past my_nblk (only in a launch's last, partial wave) have zero query
-      // fragments and are never written out, so they need no branch.
-      f32x4 accb[NQB][2];
-#pragma unroll
-      for (int j = 0; j < NQB; j++) accb[j][0] = accb[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; s++)
-#pragma unroll
-        for (int j = 0; j < NQB; j++)
-#pragma unroll
-          for (int h = 0; h < 2; h++) accb[j][h] = mfma16x16x32<DT>(buf.f[0][s], qf[j][s][h], accb[j][h]);
-#pragma unroll
-      for (int j = 0; j < NQB; j++) {
-        fold(rmax[j][0], accb[j][0], 0u);
-        fold(rmax[j][1], accb[j][1], 0u);
-      }
-      if (c.t0 + TT >= c.len) finish_doc(c.b, c.len);
-      return;
-    } else if constexpr (QREG) {
+    if constexpr (QREG) {
       // One k-group: each query block is finished before the next, so only one
       // block's accumulators are live (what lets a wave hold several blocks).
 #pragma unroll
@@ -476,55 +437,15 @@ static int fill(float* out, int64_t n, float v, hipStream_t st) {
 #endif
 constexpr int kNSub = TMS_DENSE_NSUB;
 constexpr int kMaxQldsBytes = 64 * 1024;
-#ifndef TMS_SPLIT_NSUB
-#define TMS_SPLIT_NSUB 1  // tile rows of the query-split kernel (its query fragments take 128 VGPRs)
-#endif
 #ifndef TMS_DENSE_PFD
 #define TMS_DENSE_PFD 1  // tiles in flight ahead of the one being scored
 #endif
-#ifndef TMS_SPLIT_PFD
-#define TMS_SPLIT_PFD 2  // ... in the query-split kernel, whose tiles are short (16 tokens)
-#endif
-constexpr int kSplitNSub = TMS_SPLIT_NSUB;
 
-template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, bool QSPLIT = false, int NS = kNSub>
+template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED>
 static int launch_one(const DenseArgs& a, int64_t grid, size_t lds, hipStream_t st) {
-  constexpr int kPfd = QSPLIT ? TMS_SPLIT_PFD : TMS_DENSE_PFD;
-  hipLaunchKernelGGL((dense_maxsim_kernel<DT, MODE, NQB, KS_REG, FULL, ALIGNED, NS, QSPLIT, kPfd>),
+  hipLaunchKernelGGL((dense_maxsim_kernel<DT, MODE, NQB, KS_REG, FULL, ALIGNED, kNSub, TMS_DENSE_PFD>),
                      dim3((unsigned)grid), dim3(256), lds, st, a);
   return check_launch("dense_maxsim_kernel");
-}
-
-// Batched queries with the query fragments in VGPRs: each wave holds up to four
-// 32-token blocks (whole queries), the four waves of a workgroup split up to 16
-// blocks and stream the same documents, so every HBM pass over D scores up to 16
-// blocks. Launches step through the blocks in groups of 4 * per-wave blocks; a
-// query never straddles two waves or two launches.
-template <int DT>
-static int run_split(DenseArgs a, int64_t nQ, hipStream_t st) {
-  const int per_wave = (4 / a.nbq) * a.nbq;
-  const int64_t nblocks_total = nQ * (int64_t)a.nbq;
-  int64_t dpw = a.nd > 0 ? 4096 / a.nd : 64;  // long streams: each wave loads up to 32 KB of queries
-  if (dpw < 1) dpw = 1;
-  if (dpw > 64) dpw = 64;
-  const int64_t min_wgs = (int64_t)256 * 4 * 2;
-  if (dpw > 1 && a.B / dpw < min_wgs) dpw = a.B / min_wgs > 0 ? a.B / min_wgs : 1;
-  a.docs_per_wave = (int32_t)dpw;
-  a.nblk = per_wave;
-  const int64_t grid = (a.B + dpw - 1) / dpw;
-  for (int64_t blk0 = 0; blk0 < nblocks_total; blk0 += 4 * per_wave) {
-    a.blk0 = (int32_t)blk0;
-    a.blk_end = (int32_t)((nblocks_total - blk0 < 4 * per_wave) ? nblocks_total : blk0 + 4 * per_wave);
-    int rc;
-    switch (a.d / 32) {
-      case 1: rc = launch_one<DT, MODE_FIXED, 4, 1, true, true, true, kSplitNSub>(a, grid, 0, st); break;
-      case 2: rc = launch_one<DT, MODE_FIXED, 4, 2, true, true, true, kSplitNSub>(a, grid, 0, st); break;
-      case 3: rc = launch_one<DT, MODE_FIXED, 4, 3, true, true, true, kSplitNSub>(a, grid, 0, st); break;
-      default: rc = launch_one<DT, MODE_FIXED, 4, 4, true, true, true, kSplitNSub>(a, grid, 0, st); break;
-    }
-    if (rc != TMS_OK) return rc;
-  }
-  return TMS_OK;
 }
 
 template <int DT, int MODE, int NQB>
@@ -628,11 +549,7 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   a.pad_len = pad_len;
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
   const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
-  if (TMS_USE_STREAM && mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, dtype, out, st);
-  if (mode == MODE_FIXED && qreg && a.nbq <= 4 && nQ * a.nbq >= 4) {
-    if (dtype == TMS_DTYPE_F16) return run_split<TMS_DTYPE_F16>(a, nQ, st);
-    return run_split<TMS_DTYPE_BF16>(a, nQ, st);
-  }
+  if (mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, dtype, out, st);
   if (dtype == TMS_DTYPE_F16) return run_dense<TMS_DTYPE_F16>(a, nQ, mode, aligned, st);
   return run_dense<TMS_DTYPE_BF16>(a, nQ, mode, aligned, st);
 }
