@@ -124,6 +124,45 @@ int tms_topk(const float* scores, int64_t nrows, int64_t n, int64_t k, void* wor
 /* Device workspace in bytes that tms_topk needs for these sizes (0 if none or invalid). */
 int64_t tms_topk_workspace_size(int64_t nrows, int64_t n, int64_t k);
 
+/*
+ * Residual-compressed documents: the ColBERTv2 codec (ResidualCodec in
+ * colbert/indexing/codecs/residual.py) of colbert-ai 0.2.22, the ColBERT release the
+ * reference's PLAID drop-in is written against (src/plaid_integration_benchmark.py:23).
+ * Token t of the index is a centroid id codes[t] (int32) and a residual row of
+ * d * nbits / 8 bytes at residuals + t * d * nbits / 8: for each dimension, bits
+ * 0 .. nbits-1 of its bucket index (least significant first), dimensions in order,
+ * packed from the most significant bit of each byte. It decodes to
+ *   v = fp16(centroids[code] + bucket_weights[bucket]),  x = fp16(v / fp16(|v|)).
+ * centroids (ncent, d) and bucket_weights (2^nbits) are fp16; nbits is 1, 2 or 4;
+ * d is 32, 64, 96 or 128. Centroid ids outside [0, ncent) are clamped.
+ */
+
+/*
+ * Decompress T tokens into out (T, d) fp16 (16-byte aligned).
+ * Replaces ResidualCodec.decompress (GPU path) of colbert-ai 0.2.22, which PLAID runs on
+ * candidate documents before the scorer the reference replaces
+ * (src/plaid_integration_benchmark.py:154-183).
+ */
+int tms_residual_decompress(const int32_t* codes, const uint8_t* residuals, int64_t T, const void* centroids,
+                            int64_t ncent, int64_t d, const void* bucket_weights, int nbits, void* out, void* stream);
+
+/*
+ * MaxSim of one fp16 query Q (nq, d) against residual-compressed documents, decoded in
+ * registers: no decompressed copy is written. Document p < ndocs is index rows
+ * [offsets[p], offsets[p+1]) of total_tokens; out[b] scores document pids[b] (or b when
+ * pids is NULL, then B <= ndocs). pad_len > 0 gives the zero-padding semantics of
+ * tms_maxsim_varlen_padded; 0 gives plain MaxSim (an empty document scores -inf). An
+ * invalid pid or offsets scores NaN. Each token's dot products are scaled by
+ * 1 / fp16(|v|) before the max, so scores equal MaxSim over the decompressed tokens up
+ * to their fp16 rounding.
+ * Replaces, in the reference's PLAID path, ColBERT's decompression of the candidates
+ * followed by flashmaxsim_score_packed (src/plaid_integration_benchmark.py:154-183).
+ */
+int tms_maxsim_residual(const void* Q, int64_t nq, int64_t d, const void* centroids, int64_t ncent,
+                        const void* bucket_weights, int nbits, const int32_t* codes, const uint8_t* residuals,
+                        int64_t total_tokens, const int64_t* offsets, int64_t ndocs, const int64_t* pids, int64_t B,
+                        int64_t pad_len, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,175 @@
+"""CPU oracle for residual-compressed (ColBERTv2) documents -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module; the product path never calls it.
+
+Where the format comes from. The reference does not store compressed documents itself.
+Its PLAID drop-in (``src/plaid_integration_benchmark.py:154-183``, patched into ColBERT
+at ``:328-333``) receives documents that ColBERT's search has already decompressed from
+its residual-compressed index. ColBERT is a third-party dependency absent from the
+reference checkout: the package ``colbert-ai``, pinned at **0.2.22**
+(``src/plaid_integration_benchmark.py:23``). Its codec is ``ResidualCodec`` in
+``colbert/indexing/codecs/residual.py`` of that package. This module restates the
+codec's published algorithm (Santhanam et al., "ColBERTv2", NAACL 2022, section 3;
+the package's compress / binarize / decompress):
+
+index build (:func:`compress`)
+  * ``code[t] = argmax_c <centroid[c], emb[t]>``;
+  * ``r = fp16(emb[t] - centroid[code[t]])``;
+  * ``bucket[j] = #{i : cutoffs[i] < r[j]}`` (``torch.bucketize``, ``right=False``),
+    with ``2**nbits - 1`` cutoffs;
+  * bits ``0 .. nbits-1`` of every dimension's bucket, least significant bit first,
+    dimensions in order, packed eight to a byte with the first bit in the most
+    significant position (``numpy.packbits``). A token's residual row is
+    ``d * nbits / 8`` bytes (:func:`pack_buckets`).
+
+decompression, GPU path of the codec (:func:`decompress`)
+  * ``v = fp16(centroid[code] + bucket_weights[bucket])`` (half arithmetic);
+  * ``n = fp16(sqrt(sum_j v_j**2))``, accumulated in fp32;
+  * ``out = fp16(v / n)``: ``torch.nn.functional.normalize`` applied to a half tensor.
+
+The codec's own decoder does not extract bits directly. It maps each residual byte
+through a bit-reversal table and then through the ``itertools.product`` table of bucket
+tuples. :func:`colbert_tables` and :func:`unpack_buckets_via_tables` restate that
+route, so the tests can check the direct bit extraction of :func:`unpack_buckets`
+against it.
+
+:func:`maxsim_residual` scores a query against documents of such tokens. Document
+``b`` is index rows ``[offsets[p], offsets[p+1])`` with ``p = pids[b]``. It follows the
+PLAID drop-in's semantics (``maxsim_oracle.maxsim_packed_zero_padded`` for
+``pad_len > 0``, plain varlen MaxSim otherwise).
+"""
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+
+from . import maxsim_oracle as _mo
+
+
+def pack_buckets(buckets: np.ndarray, nbits: int) -> np.ndarray:
+    """(T, d) bucket indices < 2**nbits -> (T, d*nbits/8) uint8 residual rows."""
+    b = np.asarray(buckets, dtype=np.uint8)
+    T, d = b.shape
+    assert (d * nbits) % 8 == 0, (d, nbits)
+    bits = (b[..., None] >> np.arange(nbits, dtype=np.uint8)) & 1  # (T, d, nbits), LSB first
+    return np.packbits(bits.reshape(T, d * nbits), axis=-1)
+
+
+def unpack_buckets(residuals: np.ndarray, nbits: int, d: int) -> np.ndarray:
+    """(T, d*nbits/8) uint8 -> (T, d) bucket indices (inverse of :func:`pack_buckets`)."""
+    r = np.asarray(residuals, dtype=np.uint8)
+    T = r.shape[0]
+    bits = np.unpackbits(r, axis=-1).reshape(T, d, nbits).astype(np.uint8)
+    return (bits << np.arange(nbits, dtype=np.uint8)).sum(axis=-1).astype(np.uint8)
+
+
+def colbert_tables(nbits: int):
+    """The codec's two decode tables, restated from their published construction:
+    ``reversed_bit_map[byte]`` reverses the bit order inside every ``nbits`` group of
+    the byte (groups stay in place); ``lookup[z]`` is the ``z``-th tuple of
+    ``itertools.product(range(2**nbits), repeat=8 // nbits)``."""
+    mask = (1 << nbits) - 1
+    rev = np.zeros(256, dtype=np.uint8)
+    for byte in range(256):
+        z = 0
+        for hi in range(8, 0, -nbits):  # groups from the most significant end
+            x = (byte >> (hi - nbits)) & mask
+            y = 0
+            for k in range(nbits):
+                y |= ((x >> k) & 1) << (nbits - 1 - k)
+            z = (z << nbits) | y
+        rev[byte] = z
+    lookup = np.array(list(itertools.product(range(1 << nbits), repeat=8 // nbits)), dtype=np.uint8)
+    return rev, lookup
+
+
+def unpack_buckets_via_tables(residuals: np.ndarray, nbits: int, d: int) -> np.ndarray:
+    """Bucket indices by the codec's table route: byte -> reversed_bit_map -> lookup."""
+    rev, lookup = colbert_tables(nbits)
+    r = np.asarray(residuals, dtype=np.uint8)
+    return lookup[rev[r].astype(np.int64)].reshape(r.shape[0], d)
+
+
+def compress(embs: np.ndarray, centroids: np.ndarray, bucket_cutoffs: np.ndarray, nbits: int):
+    """Index build: fp16 (T, d) embeddings -> (int32 codes (T,), uint8 residuals)."""
+    E = np.asarray(embs, dtype=np.float16)
+    C = np.asarray(centroids, dtype=np.float16)
+    codes = np.argmax(E.astype(np.float32) @ C.astype(np.float32).T, axis=1).astype(np.int32)
+    r = (E.astype(np.float32) - C[codes].astype(np.float32)).astype(np.float16)
+    cut = np.asarray(bucket_cutoffs, dtype=np.float32)
+    assert cut.shape == ((1 << nbits) - 1,), cut.shape
+    buckets = np.searchsorted(cut, r.astype(np.float32), side="left").astype(np.uint8)
+    return codes, pack_buckets(buckets, nbits)
+
+
+def decompress_unnormalised(codes, residuals, centroids, bucket_weights, nbits: int) -> np.ndarray:
+    """``fp16(centroid[code] + bucket_weights[bucket])`` per dimension, (T, d) fp16."""
+    C = np.asarray(centroids, dtype=np.float16)
+    d = C.shape[1]
+    w = np.asarray(bucket_weights, dtype=np.float16)
+    assert w.shape == (1 << nbits,), w.shape
+    b = unpack_buckets(residuals, nbits, d)
+    c = C[np.asarray(codes, dtype=np.int64)]
+    return (c.astype(np.float32) + w[b].astype(np.float32)).astype(np.float16)
+
+
+def decompress(codes, residuals, centroids, bucket_weights, nbits: int) -> np.ndarray:
+    """The codec's GPU decompression: (T, d) fp16 unit vectors."""
+    v = decompress_unnormalised(codes, residuals, centroids, bucket_weights, nbits).astype(np.float32)
+    n = np.sqrt((v * v).sum(axis=1, dtype=np.float32), dtype=np.float32).astype(np.float16).astype(np.float32)
+    n = np.maximum(n, np.float32(1e-12))
+    return (v / n[:, None]).astype(np.float16)
+
+
+def doc_rows(offsets: np.ndarray, pids) -> list:
+    """(start, end) index rows of every scored document, or None for an invalid one."""
+    offsets = np.asarray(offsets, dtype=np.int64)
+    ndocs = offsets.shape[0] - 1
+    ids = range(ndocs) if pids is None else np.asarray(pids, dtype=np.int64)
+    out = []
+    for p in ids:
+        p = int(p)
+        if p < 0 or p >= ndocs or offsets[p] < 0 or offsets[p + 1] < offsets[p]:
+            out.append(None)
+        else:
+            out.append((int(offsets[p]), int(offsets[p + 1])))
+    return out
+
+
+def maxsim_residual(Q, codes, residuals, centroids, bucket_weights, nbits: int, offsets, pids=None,
+                    pad_len: int = 0) -> np.ndarray:
+    """float64 MaxSim of Q (Nq, d) against the decompressed documents.
+
+    ``pad_len > 0``: a document shorter than ``pad_len`` also sees zero vectors (each
+    query token's max is at least 0; an empty document scores 0), as the PLAID drop-in
+    computes after padding. ``pad_len == 0``: varlen semantics (empty -> -inf).
+    Invalid documents (pid or offsets out of range) score NaN."""
+    D = decompress(codes, residuals, centroids, bucket_weights, nbits)
+    Qd = np.asarray(Q, dtype=np.float64)
+    rows = doc_rows(offsets, pids)
+    out = np.empty(len(rows), dtype=np.float64)
+    for i, se in enumerate(rows):
+        if se is None or se[1] > D.shape[0]:
+            out[i] = np.nan
+            continue
+        s, e = se
+        if e == s:
+            out[i] = 0.0 if (pad_len > 0 and Qd.shape[0] > 0) else (-np.inf if Qd.shape[0] > 0 else 0.0)
+            continue
+        m = (D[s:e].astype(np.float64) @ Qd.T).max(axis=0)
+        if pad_len > 0 and e - s < pad_len:
+            m = np.maximum(m, 0.0)
+        out[i] = m.sum()
+    return out
+
+
+def maxsim_residual_f32(Q, codes, residuals, centroids, bucket_weights, nbits: int, offsets, pids=None,
+                        pad_len: int = 0, chunk: int = 4096) -> np.ndarray:
+    """The reference pipeline's CPU cost model for the ``cpu_baseline``: decompress the
+    documents, then fp32 varlen MaxSim (``maxsim_oracle.maxsim_varlen``). ``pids`` must
+    be None (all documents) and ``pad_len`` 0."""
+    assert pids is None and pad_len == 0
+    D = decompress(codes, residuals, centroids, bucket_weights, nbits)
+    return _mo.maxsim_varlen(Q, D, offsets)

@@ -1,0 +1,178 @@
+"""GPU parity of the residual-compressed (ColBERTv2) path against oracle/residual_oracle.py.
+
+* tms_residual_decompress: fp16 outputs equal to the oracle's restatement of the codec
+  (same half add, fp32 norm, fp32 division) up to 1 fp16 ulp; only the fp32 summation
+  order of the norm differs, and it can move a rounding boundary;
+* tms_maxsim_residual: |score - oracle| <= 1e-3 relative + 1e-3 absolute, the BASELINE
+  bar; the oracle scores the decompressed fp16 tokens in float64.
+"""
+import numpy as np
+import pytest
+
+from oracle import maxsim_oracle as mo
+from oracle import residual_oracle as ro
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-3
+ATOL = 1e-3
+
+
+def _index(rng, T, d, nbits, ncent):
+    """A synthetic index: unit-norm fp16 centroids, random codes and residual buckets,
+    bucket weights at the quantiles of a small residual distribution (as the codec fits
+    them)."""
+    C = rng.standard_normal((ncent, d)).astype(np.float32)
+    C /= np.linalg.norm(C, axis=1, keepdims=True)
+    codes = rng.integers(0, ncent, T).astype(np.int32)
+    buckets = rng.integers(0, 1 << nbits, (T, d)).astype(np.uint8)
+    w = np.sort(rng.normal(0, 0.05, 1 << nbits)).astype(np.float16)
+    return C.astype(np.float16), codes, ro.pack_buckets(buckets, nbits), w
+
+
+def _gpu(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _assert_scores(got, ref, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), f"{what}: NaN pattern differs"
+    assert np.array_equal(np.isinf(got), np.isinf(ref)), f"{what}: inf pattern differs"
+    fin = np.isfinite(ref)
+    assert np.all(got[np.isinf(ref)] == ref[np.isinf(ref)]), what
+    np.testing.assert_allclose(got[fin], ref[fin], rtol=RTOL, atol=ATOL, err_msg=what)
+
+
+@pytest.mark.parametrize("nbits", [1, 2, 4])
+@pytest.mark.parametrize("d", [32, 64, 96, 128])
+def test_decompress_matches_codec(cuda, nbits, d):
+    from tilemaxsim_amd import decompress_residual
+    rng = np.random.default_rng(100 * nbits + d)
+    T = 3001
+    C, codes, res, w = _index(rng, T, d, nbits, 97)
+    got = decompress_residual(_gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits).cpu().numpy()
+    ref = ro.decompress(codes, res, C, w, nbits)
+    assert got.shape == (T, d) and got.dtype == np.float16
+    ulps = np.abs(got.view(np.int16).astype(np.int32) - ref.view(np.int16).astype(np.int32))
+    assert ulps.max() <= 1, f"max ulp difference {ulps.max()}"
+    assert (ulps == 0).mean() > 0.99
+    # int64 codes take the same path
+    got64 = decompress_residual(_gpu(codes.astype(np.int64)), _gpu(res), _gpu(C), _gpu(w), nbits).cpu().numpy()
+    assert np.array_equal(got64, got)
+
+
+@pytest.mark.parametrize("nbits,d,nq", [(2, 128, 32), (1, 128, 32), (4, 128, 32), (2, 64, 20), (2, 32, 1),
+                                        (2, 96, 33), (4, 128, 64), (2, 128, 100)])
+@pytest.mark.parametrize("padding", ["zeros", "mask"])
+def test_fused_maxsim_matches_oracle(cuda, nbits, d, nq, padding):
+    from tilemaxsim_amd import flashmaxsim_score_residual
+    rng = np.random.default_rng(nbits * 1000 + d + nq)
+    ndocs = 900
+    lens = rng.integers(0, 160, ndocs)
+    lens[::37] = 0
+    lens[5] = 300
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(offsets[-1])
+    C, codes, res, w = _index(rng, T, d, nbits, 517)
+    Q = rng.standard_normal((nq, d)).astype(np.float32)
+    Q /= np.linalg.norm(Q, axis=1, keepdims=True)
+    Q = Q.astype(np.float16)
+    got = flashmaxsim_score_residual(_gpu(Q), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(offsets),
+                                     padding=padding).cpu().numpy()
+    pad_len = int(lens.max()) if padding == "zeros" else 0
+    ref = ro.maxsim_residual(Q, codes, res, C, w, nbits, offsets, None, pad_len)
+    _assert_scores(got, ref, f"nbits={nbits} d={d} nq={nq} {padding}")
+
+
+def test_fused_candidates_match_packed_scoring(cuda):
+    """PLAID's flow: pick candidate pids, decompress their tokens, score them packed.
+    The fused kernel must give the same scores without the decompressed copy."""
+    import torch
+    from tilemaxsim_amd import decompress_residual, flashmaxsim_score_packed, flashmaxsim_score_residual
+    rng = np.random.default_rng(77)
+    d, nbits, ndocs = 128, 2, 4000
+    lens = rng.integers(20, 180, ndocs)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    C, codes, res, w = _index(rng, int(offsets[-1]), d, nbits, 1024)
+    Q = rng.standard_normal((32, d)).astype(np.float32)
+    Q = (Q / np.linalg.norm(Q, axis=1, keepdims=True)).astype(np.float16)
+    pids = rng.choice(ndocs, 700, replace=False).astype(np.int64)
+    pids[10] = pids[11]  # a duplicate candidate
+    fused = flashmaxsim_score_residual(_gpu(Q), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(offsets),
+                                       _gpu(pids)).cpu().numpy()
+    rows = np.concatenate([np.arange(offsets[p], offsets[p + 1]) for p in pids])
+    D = decompress_residual(_gpu(codes[rows]), _gpu(res[rows]), _gpu(C), _gpu(w), nbits)
+    packed = flashmaxsim_score_packed(_gpu(Q), D, torch.from_numpy(lens[pids])).cpu().numpy()
+    np.testing.assert_allclose(fused, packed, rtol=2e-4, atol=2e-4)
+    ref = ro.maxsim_residual(Q, codes, res, C, w, nbits, offsets, pids, int(lens[pids].max()))
+    _assert_scores(fused, ref, "candidates")
+    assert fused[10] == fused[11]
+    # top-100 identical except swaps within tolerance of the 100th score
+    kth = np.sort(ref)[::-1][99]
+    diff = set(np.argsort(-fused, kind="stable")[:100].tolist()) ^ set(mo.topk(ref, 100)[1].tolist())
+    for i in diff:
+        assert abs(ref[i] - kth) <= RTOL * abs(kth) + ATOL
+
+
+def test_invalid_documents_and_codes(cuda):
+    from tilemaxsim_amd import flashmaxsim_score_residual
+    rng = np.random.default_rng(5)
+    d, nbits = 64, 2
+    lens = np.array([5, 0, 7, 3])
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    C, codes, res, w = _index(rng, int(offsets[-1]), d, nbits, 11)
+    Q = rng.standard_normal((8, d)).astype(np.float16)
+    args = (_gpu(Q), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(offsets))
+    pids = np.array([3, -1, 4, 1, 0], dtype=np.int64)
+    with pytest.raises(ValueError):
+        flashmaxsim_score_residual(*args, _gpu(pids))
+    got = flashmaxsim_score_residual(*args, _gpu(pids), padding="mask", validate=False).cpu().numpy()
+    ref = ro.maxsim_residual(Q, codes, res, C, w, nbits, offsets, pids, 0)
+    assert np.isnan(got[1]) and np.isnan(got[2]) and got[3] == -np.inf
+    _assert_scores(got, ref, "invalid pids")
+    # centroid ids outside [0, C) are clamped to the table, never read out of bounds
+    bad = codes.copy()
+    bad[0], bad[3] = 11, -4
+    clamped = np.clip(bad, 0, 10).astype(np.int32)
+    got = flashmaxsim_score_residual(_gpu(Q), _gpu(bad), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(offsets),
+                                     padding="mask").cpu().numpy()
+    _assert_scores(got, ro.maxsim_residual(Q, clamped, res, C, w, nbits, offsets), "clamped codes")
+
+
+def test_edge_sizes(cuda):
+    import torch
+    from tilemaxsim_amd import decompress_residual, flashmaxsim_score_residual
+    rng = np.random.default_rng(9)
+    d, nbits = 128, 2
+    C, codes, res, w = _index(rng, 40, d, nbits, 3)
+    Q = rng.standard_normal((32, d)).astype(np.float16)
+    # one document of one token; every document empty; no query tokens; no documents
+    one = np.array([0, 1], dtype=np.int64)
+    got = flashmaxsim_score_residual(_gpu(Q), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(one))
+    _assert_scores(got.cpu().numpy(), ro.maxsim_residual(Q, codes, res, C, w, nbits, one, None, 1), "one token")
+    empty = np.zeros(6, dtype=np.int64)  # all empty: nothing to pad to, so -inf either way
+    for padding in ("zeros", "mask"):
+        got = flashmaxsim_score_residual(_gpu(Q), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(empty),
+                                         padding=padding)
+        assert np.all(got.cpu().numpy() == -np.inf)
+    some = np.array([0, 0, 0, 3, 3], dtype=np.int64)  # empties beside a 3-token document
+    got = flashmaxsim_score_residual(_gpu(Q), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(some))
+    assert got.cpu().numpy()[[0, 1, 3]].tolist() == [0.0, 0.0, 0.0]  # zero padding: each max is 0
+    _assert_scores(got.cpu().numpy(), ro.maxsim_residual(Q, codes, res, C, w, nbits, some, None, 3), "some")
+    got = flashmaxsim_score_residual(_gpu(Q[:0]), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits,
+                                     _gpu(np.array([0, 10, 40])))
+    assert np.all(got.cpu().numpy() == 0.0)
+    got = flashmaxsim_score_residual(_gpu(Q), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits,
+                                     _gpu(np.array([0, 40])), pids=_gpu(np.zeros(0, np.int64)))
+    assert got.shape == (0,)
+    assert decompress_residual(_gpu(codes[:0]), _gpu(res[:0]), _gpu(C), _gpu(w), nbits).shape == (0, d)
+    with pytest.raises(NotImplementedError):
+        decompress_residual(_gpu(codes), _gpu(res), _gpu(C), _gpu(w), 3)
+    with pytest.raises(ValueError):
+        decompress_residual(_gpu(codes), _gpu(res[:, :16]), _gpu(C), _gpu(w), nbits)
+    with pytest.raises(NotImplementedError):  # d not in {32, 64, 96, 128}
+        Cw = torch.zeros(3, 256, dtype=torch.float16, device="cuda")
+        decompress_residual(_gpu(codes), torch.zeros(40, 64, dtype=torch.uint8, device="cuda"), Cw, _gpu(w), nbits)

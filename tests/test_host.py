@@ -89,6 +89,32 @@ def test_topk_workspace_sizes():
     assert rc == 1 and "workspace" in msg
 
 
+def test_residual_c_abi_rejects_bad_arguments():
+    # tms_residual_decompress(codes, residuals, T, centroids, ncent, d, weights, nbits, out, stream)
+    rc, msg = _c_call("tms_residual_decompress", 16, 16, 10, 16, 4, 128, 16, 3, 16, None)
+    assert rc == 2 and "nbits" in msg
+    rc, msg = _c_call("tms_residual_decompress", 16, 16, 10, 16, 4, 256, 16, 2, 16, None)
+    assert rc == 2 and "d=256" in msg
+    rc, msg = _c_call("tms_residual_decompress", 16, 16, 10, 16, 0, 128, 16, 2, 16, None)
+    assert rc == 1 and "centroids" in msg
+    rc, msg = _c_call("tms_residual_decompress", 16, 16, 10, 16, 4, 128, None, 2, 16, None)
+    assert rc == 1 and "NULL" in msg
+    rc, msg = _c_call("tms_residual_decompress", 16, 16, 10, 24, 4, 128, 16, 2, 16, None)
+    assert rc == 1 and "aligned" in msg
+    rc, _ = _c_call("tms_residual_decompress", None, None, 0, 16, 4, 128, 16, 2, None, None)
+    assert rc == 0  # nothing to decompress, no HIP call
+    # tms_maxsim_residual(Q, nq, d, centroids, ncent, weights, nbits, codes, residuals, T,
+    #                     offsets, ndocs, pids, B, pad_len, out, stream)
+    rc, msg = _c_call("tms_maxsim_residual", 16, 32, 128, 16, 4, 16, 2, 16, 16, 10, 16, 3, None, 5, 0, 16, None)
+    assert rc == 1 and "ndocs" in msg
+    rc, msg = _c_call("tms_maxsim_residual", 16, 32, 128, 16, 4, 16, 2, 16, 16, 10, None, 3, None, 3, 0, 16, None)
+    assert rc == 1 and "offsets" in msg
+    rc, msg = _c_call("tms_maxsim_residual", 16, 32, 128, 16, 4, 16, 2, 16, 16, 10, 16, 3, None, 3, -1, 16, None)
+    assert rc == 1 and "negative" in msg
+    rc, _ = _c_call("tms_maxsim_residual", 16, 32, 128, 16, 4, 16, 2, 16, 16, 10, 16, 3, None, 0, 0, None, None)
+    assert rc == 0  # no documents to score
+
+
 def test_python_errors_before_device_checks():
     from tilemaxsim_amd import (TileMaxSimPQ, flash_maxsim_multi_doc, flash_maxsim_single,
                                 flash_maxsim_v2_multiquery, maxsim_score)

@@ -39,6 +39,10 @@ SIGNATURES = {
     "tms_pq_score": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tms_topk": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p],
     "tms_topk_workspace_size": [_i64, _i64, _i64],
+    "tms_residual_decompress": [_c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _int, _c_void_p,
+                                _c_void_p],
+    "tms_maxsim_residual": [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p, _int, _c_void_p, _c_void_p, _i64,
+                            _c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
 }
 RESTYPES = {"tms_topk_workspace_size": ctypes.c_int64}
 

@@ -1,0 +1,488 @@
+// Residual-compressed documents (the ColBERTv2 codec of colbert-ai 0.2.22, the ColBERT
+// release the reference's PLAID drop-in runs against, src/plaid_integration_benchmark.py:23):
+// decompression, and MaxSim decoded in registers.
+//
+// Format. Token t of the index is a centroid id codes[t] (int32) and a residual row of
+// rb = d * nbits / 8 bytes: for every dimension j, bits 0..nbits-1 of its bucket index
+// (least significant first) enter one bit stream, dimension after dimension, and the
+// stream fills each byte from its most significant bit. The codec decodes
+//   v = fp16(centroid[code] + weight[bucket])   (half arithmetic, per dimension)
+//   x = v / fp16(|v|)                            (|v| accumulated in fp32)
+// and PLAID scores the decoded documents with MaxSim.
+//
+// Decoding on gfx950:
+//  * a byte of residual covers 8 / nbits dimensions; a 256-entry table in LDS (built by
+//    each workgroup from the 2^nbits weights) maps a byte to the fp16 weights of its
+//    dimensions, so an 8-dimension chunk takes nbits table reads (16 bytes in all);
+//  * the centroid chunk is gathered straight into the MFMA A-operand registers of the
+//    lane that owns the chunk (lane (r, g) owns chunk 4s + g of token r at k-step s, as in
+//    the dense kernels); v = centroid + weight is one v_pk_add_f16 per 2 dimensions;
+//  * |v|^2 is v_dot2_f32_f16 over the lane's dimensions plus two cross-lane adds.
+//
+// tms_residual_decompress writes x exactly as the codec computes it (fp32 division of
+// fp16 values, rounded to fp16). The fused MaxSim kernel instead multiplies each token's
+// dot products <q, v> by 1 / fp16(|v|) before the max, which is the same score without
+// rounding x to fp16 first (differences ~1e-4 relative on unit-norm data).
+#include <string.h>
+
+#include "tms_common.h"
+
+namespace tms {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;  // every kernel here is launched with 256 threads
+
+// Reinterpret a dword as two halves and back. The argument is taken by value: with the
+// ROCm 7.2 clang, __builtin_bit_cast applied directly to a subscripted ext-vector element
+// (bit_cast(T, vec[i])) reads element 0 whatever i is, so element values must pass
+// through a scalar first.
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t x) { return __builtin_bit_cast(f16x2, x); }
+__device__ __forceinline__ uint32_t as_u32(f16x2 x) { return __builtin_bit_cast(uint32_t, x); }
+
+// A value the whole wave shares, moved to scalar registers (so control flow that depends
+// on it is uniform to the compiler).
+__device__ __forceinline__ int64_t wave_uniform(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+struct ResArgs {
+  const uint8_t* Q;          // (nq, d) fp16
+  const uint8_t* centroids;  // (ncent, d) fp16
+  const int32_t* codes;      // (T)
+  const uint8_t* residuals;  // (T, rb)
+  const int64_t* offsets;    // (ndocs + 1): document p is index rows [offsets[p], offsets[p+1])
+  const int64_t* pids;       // (B) documents to score, or null for 0 .. B-1
+  const uint16_t* weights;   // (2^nbits) fp16 bucket weights
+  float* out;                // (B) scores, or (T, d) fp16 for the decompression kernel
+  int64_t B, ndocs, T, ncent, pad_len;
+  int32_t nq, nbq, blk0, d, rb, docs_per_wave;
+};
+
+// Byte -> fp16 weights of its 8 / NBITS dimensions, in dimension order. The table is
+// written and read only through __builtin_memcpy (byte-typed accesses), so no access
+// to it depends on type-based alias rules.
+template <int NBITS>
+__device__ void build_lut(uint8_t* lut, const uint16_t* weights) {
+  constexpr int kPerByte = 8 / NBITS;
+  constexpr uint32_t kMask = (1u << NBITS) - 1u;
+  for (int byte = threadIdx.x; byte < 256; byte += kThreads) {
+    uint16_t e[kPerByte];
+#pragma unroll
+    for (int k = 0; k < kPerByte; k++) {
+      // dimension k's bits sit at byte bits 7 - (k*NBITS + j), j = 0 .. NBITS-1
+      uint32_t bucket = 0;
+#pragma unroll
+      for (int j = 0; j < NBITS; j++) bucket |= ((byte >> (7 - (k * NBITS + j))) & 1u) << j;
+      e[k] = weights[bucket & kMask];
+    }
+    __builtin_memcpy(lut + byte * 2 * kPerByte, e, sizeof(e));
+  }
+}
+
+// The NBITS residual bytes of one 8-dimension chunk (little-endian in a u32).
+template <int NBITS>
+__device__ __forceinline__ uint32_t load_res(const uint8_t* row, int chunk) {
+  if constexpr (NBITS == 1) return row[chunk];
+  else if constexpr (NBITS == 2) return *(const uint16_t*)(row + 2 * chunk);
+  else return *(const uint32_t*)(row + 4 * chunk);
+}
+
+// fp16 weights of the chunk's 8 dimensions from the LDS table.
+template <int NBITS>
+__device__ __forceinline__ u32x4 chunk_weights(const uint8_t* lut, uint32_t rw) {
+  uint32_t w[4];
+  if constexpr (NBITS == 1) {
+    __builtin_memcpy(w, lut + (rw & 0xffu) * 16, 16);
+  } else if constexpr (NBITS == 2) {
+    __builtin_memcpy(w, lut + (rw & 0xffu) * 8, 8);
+    __builtin_memcpy(w + 2, lut + ((rw >> 8) & 0xffu) * 8, 8);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) __builtin_memcpy(w + i, lut + ((rw >> (8 * i)) & 0xffu) * 4, 4);
+  }
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// v = fp16(c + w) for 8 dimensions; n2 += sum v^2 in fp32.
+__device__ __forceinline__ u32x4 add_chunk(u32x4 c, u32x4 w, float& n2) {
+  u32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t ci = c[i], wi = w[i];
+    const f16x2 s = as_f16x2(ci) + as_f16x2(wi);
+    n2 = __builtin_amdgcn_fdot2(s, s, n2, false);
+    v[i] = as_u32(s);
+  }
+  return v;
+}
+
+// Wave-uniform read of read-only data through the constant address space: a scalar load
+// (counted by lgkmcnt), so waiting for it never waits for the vector loads in flight.
+__device__ __forceinline__ int64_t load_uniform(const int64_t* p, int64_t i) {
+  typedef const __attribute__((address_space(4))) int64_t* const_ptr;
+  return ((const_ptr)p)[i];
+}
+
+// 1 / fp16(sqrt(n2)): the codec's half-precision norm (clamped at the smallest fp16 > 0).
+__device__ __forceinline__ float inv_norm(float n2) {
+  float n = (float)(_Float16)sqrtf(n2);
+  return 1.0f / fmaxf(n, 5.9604645e-8f);
+}
+
+// ---------------------------------------------------------------------------------
+// Fused MaxSim. One wave streams whole documents; a tile is 16 * NSUB tokens x d.
+// Centroid ids are read two tiles ahead and the centroid chunks and residual bytes one
+// tile ahead of the tile being decoded and scored.
+template <int KS, int NBITS, int NSUB>
+__global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
+  constexpr int TT = 16 * NSUB;
+  __shared__ __attribute__((aligned(16))) uint8_t lut[4096];
+  build_lut<NBITS>(lut, a.weights);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+  // wave-uniform, so the document walk below runs on the scalar unit
+  const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t b_begin = wave_uniform(wave * a.docs_per_wave);
+  if (b_begin >= a.B) return;
+  const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
+  const float NEG_INF = -__builtin_inff();
+
+  // query block a.blk0: query tokens 32 * blk0 + 16 h + r
+  u32x4 qf[KS][2];
+  bool qvalid[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int tok = a.blk0 * 32 + 16 * h + r;
+    qvalid[h] = tok < a.nq;
+    const int64_t row = qvalid[h] ? tok : a.nq - 1;  // loaded unconditionally, zeroed below
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+      const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2);
+      qf[s][h] = qvalid[h] ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  // ---- documents ---------------------------------------------------------------
+  struct Cur {
+    int64_t b;     // position in [b_begin, b_end)
+    int64_t base;  // first index row
+    int64_t len;   // tokens
+    int64_t t0;    // first token of the tile
+  };
+  // Bounds of document position b: len < 0 marks an invalid pid or offsets.
+  auto bounds = [&](int64_t b, int64_t& base) -> int64_t {
+    const int64_t p = a.pids ? load_uniform(a.pids, b) : b;
+    if (p < 0 || p >= a.ndocs) return -1;
+    const int64_t s = load_uniform(a.offsets, p), e = load_uniform(a.offsets, p + 1);
+    if (s < 0 || e < s || e > a.T) return -1;
+    base = s;
+    return e - s;
+  };
+  const bool first_blk = a.blk0 == 0;
+  auto write = [&](int64_t b, float v) {
+    if (lane == 0) {
+      float* o = a.out + b;
+      *o = first_blk ? v : *o + v;
+    }
+  };
+  // Move to the first document at or after b with a token; write_skipped: score the
+  // skipped ones (only the cursor that scores does this). Past the last document the
+  // cursor keeps its last tile's rows, so prefetches through it stay in bounds.
+  auto seek = [&](Cur& c, int64_t b, bool write_skipped) {
+    for (; b < b_end; b++) {
+      int64_t base = 0;
+      const int64_t len = bounds(b, base);
+      if (len > 0) {
+        c.b = b;
+        c.base = base;
+        c.len = len;
+        c.t0 = 0;
+        return;
+      }
+      if (write_skipped) write(b, len < 0 ? __builtin_bit_cast(float, 0x7fc00000u) : (a.pad_len > 0 ? 0.f : NEG_INF));
+    }
+    c.b = b_end;
+  };
+  auto advance = [&](Cur& c, bool write_skipped) {
+    c.t0 += TT;
+    if (c.t0 >= c.len) seek(c, c.b + 1, write_skipped);
+  };
+  auto row_of = [&](const Cur& c, int sub) -> int64_t {
+    int64_t t = c.t0 + 16 * sub + r;
+    if (t > c.len - 1) t = c.len - 1;
+    return c.base + t;
+  };
+
+  // ---- pipeline state ------------------------------------------------------------
+  struct Body {
+    u32x4 cen[NSUB][KS];     // centroid chunks
+    uint32_t res[NSUB][KS];  // residual bytes of the chunks
+  };
+  auto load_codes = [&](int32_t (&cd)[NSUB], const Cur& c) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; sub++) cd[sub] = a.codes[row_of(c, sub)];
+  };
+  auto load_body = [&](const int32_t (&cd)[NSUB], const Cur& c, Body& bd) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; sub++) {
+      int64_t code = cd[sub];
+      code = code < 0 ? 0 : (code >= a.ncent ? a.ncent - 1 : code);
+      const uint8_t* crow = a.centroids + code * a.d * 2;
+      const uint8_t* rrow = a.residuals + row_of(c, sub) * a.rb;
+#pragma unroll
+      for (int s = 0; s < KS; s++) {
+        bd.cen[sub][s] = *(const u32x4*)(crow + 16 * (4 * s + g));
+        bd.res[sub][s] = load_res<NBITS>(rrow, 4 * s + g);
+      }
+    }
+  };
+
+  float rmax[2] = {NEG_INF, NEG_INF};
+  auto finish = [&](int64_t b, int64_t len) {
+    const bool padded = len < a.pad_len;
+    float s = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      float m = rmax[h];
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      if (padded) m = fmaxf(m, 0.f);
+      s += qvalid[h] ? m : 0.f;
+      rmax[h] = NEG_INF;
+    }
+    s += __shfl_xor(s, 8);
+    s += __shfl_xor(s, 4);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 1);
+    write(b, s);
+  };
+
+  auto compute = [&](const Cur& c, const Body& bd) {
+#pragma unroll
+    for (int sub = 0; sub < NSUB; sub++) {
+      float n2 = 0.f;
+      f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int s = 0; s < KS; s++) {
+        const u32x4 v = add_chunk(bd.cen[sub][s], chunk_weights<NBITS>(lut, bd.res[sub][s]), n2);
+        acc[0] = mfma16x16x32<TMS_DTYPE_F16>(v, qf[s][0], acc[0]);
+        acc[1] = mfma16x16x32<TMS_DTYPE_F16>(v, qf[s][1], acc[1]);
+      }
+      n2 += __shfl_xor(n2, 16);
+      n2 += __shfl_xor(n2, 32);
+      const float inv = inv_norm(n2);  // of token r (every g holds it)
+      // accumulator rows are tokens 4 g + i
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float sc = __shfl(inv, 4 * g + i);
+        rmax[0] = fmaxf(rmax[0], acc[0][i] * sc);
+        rmax[1] = fmaxf(rmax[1], acc[1][i] * sc);
+      }
+    }
+    if (c.t0 + TT >= c.len) finish(c.b, c.len);
+  };
+
+  // Tile i is scored from `cur` while tile i+1's body lands in `nxt` and tile i+2's ids
+  // in `ids`; the loop body runs twice with the two bodies' roles swapped, so every
+  // register is fixed at compile time.
+  Cur c_cur, c_nxt;
+  int32_t ids[NSUB];
+  Body b0, b1;
+  seek(c_cur, b_begin, true);
+  if (c_cur.b >= b_end) return;
+  load_codes(ids, c_cur);
+  load_body(ids, c_cur, b0);
+  c_nxt = c_cur;
+  advance(c_nxt, false);
+  load_codes(ids, c_nxt);
+  auto step = [&](Body& cur, Body& nxt) -> bool {
+    load_body(ids, c_nxt, nxt);
+    Cur c_far = c_nxt;
+    if (c_far.b < b_end) advance(c_far, false);
+    load_codes(ids, c_far);
+    compute(c_cur, cur);
+    advance(c_cur, true);
+    c_nxt = c_far;
+    return c_cur.b >= b_end;
+  };
+  while (true) {
+    if (step(b0, b1)) return;
+    if (step(b1, b0)) return;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Decompression: 16 lanes per token (lane k owns dimensions 8k .. 8k+7), four tokens
+// per wave. Writes x = fp16(v / fp16(|v|)) with fp32 division, as the codec computes.
+template <int NBITS>
+__global__ void __launch_bounds__(256) residual_decompress_kernel(ResArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lut[4096];
+  build_lut<NBITS>(lut, a.weights);
+  __syncthreads();
+  const int k = threadIdx.x & 15;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
+  const bool live = t < a.T && 8 * k < a.d;
+  const int64_t tt = t < a.T ? t : a.T - 1;
+  int64_t code = a.codes[tt];
+  code = code < 0 ? 0 : (code >= a.ncent ? a.ncent - 1 : code);
+  const int kk = 8 * k < a.d ? k : 0;
+  const u32x4 c = *(const u32x4*)(a.centroids + (code * a.d + 8 * kk) * 2);
+  const uint32_t rw = load_res<NBITS>(a.residuals + tt * a.rb, kk);
+  float n2 = 0.f;
+  const u32x4 v = add_chunk(c, chunk_weights<NBITS>(lut, rw), n2);
+  if (!live) n2 = 0.f;
+  n2 += __shfl_xor(n2, 1);
+  n2 += __shfl_xor(n2, 2);
+  n2 += __shfl_xor(n2, 4);
+  n2 += __shfl_xor(n2, 8);
+  float n = (float)(_Float16)sqrtf(n2);
+  n = fmaxf(n, 5.9604645e-8f);
+  u32x4 x;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t vi = v[i];
+    const f16x2 p = as_f16x2(vi);
+    f16x2 q;
+    q.x = (_Float16)((float)p.x / n);
+    q.y = (_Float16)((float)p.y / n);
+    x[i] = as_u32(q);
+  }
+  if (live) *(u32x4*)((uint8_t*)a.out + (t * a.d + 8 * k) * 2) = x;
+}
+
+__global__ void residual_fill_kernel(float* out, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = v;
+}
+
+// ---------------------------------------------------------------------------------
+// host side
+static int check_format(const char* fn, int64_t d, int nbits, int64_t ncent, const void* centroids,
+                        const void* weights) {
+  if (nbits != 1 && nbits != 2 && nbits != 4)
+    return fail(TMS_ERR_UNSUPPORTED, "%s: nbits=%d (supported: 1, 2, 4)", fn, nbits);
+  if (d <= 0 || d > 128 || d % 32 != 0)
+    return fail(TMS_ERR_UNSUPPORTED, "%s: d=%lld (supported: 32, 64, 96, 128)", fn, (long long)d);
+  if (ncent <= 0) return fail(TMS_ERR_INVALID, "%s: no centroids", fn);
+  if (!centroids || !weights) return fail(TMS_ERR_INVALID, "%s: centroids / bucket_weights is NULL", fn);
+  if (((uintptr_t)centroids & 15) != 0) return fail(TMS_ERR_INVALID, "%s: centroids must be 16-byte aligned", fn);
+  return TMS_OK;
+}
+
+template <int KS>
+static int launch_fused_ks(const ResArgs& a, int nbits, int64_t grid, hipStream_t st) {
+  constexpr int kNSub = 1;
+  if (nbits == 1) hipLaunchKernelGGL((residual_maxsim_kernel<KS, 1, kNSub>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else if (nbits == 2) hipLaunchKernelGGL((residual_maxsim_kernel<KS, 2, kNSub>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((residual_maxsim_kernel<KS, 4, kNSub>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  return check_launch("residual_maxsim_kernel");
+}
+
+}  // namespace tms
+
+extern "C" {
+
+int tms_residual_decompress(const int32_t* codes, const uint8_t* residuals, int64_t T, const void* centroids,
+                            int64_t ncent, int64_t d, const void* bucket_weights, int nbits, void* out, void* stream) {
+  using namespace tms;
+  const char* fn = "tms_residual_decompress";
+  if (T < 0 || d < 0 || ncent < 0) return fail(TMS_ERR_INVALID, "%s: negative size", fn);
+  int rc = check_format(fn, d, nbits, ncent, centroids, bucket_weights);
+  if (rc) return rc;
+  if (T == 0) return TMS_OK;
+  if (!codes || !residuals || !out) return fail(TMS_ERR_INVALID, "%s: NULL pointer", fn);
+  if (((uintptr_t)out & 15) != 0) return fail(TMS_ERR_INVALID, "%s: out must be 16-byte aligned", fn);
+  if ((((uintptr_t)residuals) & (nbits - 1)) != 0)
+    return fail(TMS_ERR_INVALID, "%s: residuals must be %d-byte aligned", fn, nbits);
+  ResArgs a;
+  memset(&a, 0, sizeof(a));
+  a.centroids = (const uint8_t*)centroids;
+  a.codes = codes;
+  a.residuals = residuals;
+  a.weights = (const uint16_t*)bucket_weights;
+  a.out = (float*)out;
+  a.T = T;
+  a.ncent = ncent;
+  a.d = (int32_t)d;
+  a.rb = (int32_t)(d * nbits / 8);
+  const int64_t grid = (T + 15) / 16;
+  hipStream_t st = (hipStream_t)stream;
+  if (nbits == 1) hipLaunchKernelGGL(residual_decompress_kernel<1>, dim3((unsigned)grid), dim3(256), 0, st, a);
+  else if (nbits == 2) hipLaunchKernelGGL(residual_decompress_kernel<2>, dim3((unsigned)grid), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(residual_decompress_kernel<4>, dim3((unsigned)grid), dim3(256), 0, st, a);
+  return check_launch("residual_decompress_kernel");
+}
+
+int tms_maxsim_residual(const void* Q, int64_t nq, int64_t d, const void* centroids, int64_t ncent,
+                        const void* bucket_weights, int nbits, const int32_t* codes, const uint8_t* residuals,
+                        int64_t total_tokens, const int64_t* offsets, int64_t ndocs, const int64_t* pids, int64_t B,
+                        int64_t pad_len, float* out, void* stream) {
+  using namespace tms;
+  const char* fn = "tms_maxsim_residual";
+  if (nq < 0 || d < 0 || ncent < 0 || total_tokens < 0 || ndocs < 0 || B < 0 || pad_len < 0)
+    return fail(TMS_ERR_INVALID, "%s: negative size", fn);
+  int rc = check_format(fn, d, nbits, ncent, centroids, bucket_weights);
+  if (rc) return rc;
+  if (B == 0) return TMS_OK;
+  if (!out) return fail(TMS_ERR_INVALID, "%s: out is NULL", fn);
+  if (!pids && B > ndocs) return fail(TMS_ERR_INVALID, "%s: B=%lld > ndocs=%lld without pids", fn, (long long)B,
+                                      (long long)ndocs);
+  if (!offsets) return fail(TMS_ERR_INVALID, "%s: offsets is NULL", fn);
+  hipStream_t st = (hipStream_t)stream;
+  if (nq == 0) {
+    hipLaunchKernelGGL(residual_fill_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, st, out, B, 0.f);
+    return check_launch("residual_fill_kernel");
+  }
+  if (!Q) return fail(TMS_ERR_INVALID, "%s: Q is NULL", fn);
+  if (total_tokens > 0 && (!codes || !residuals)) return fail(TMS_ERR_INVALID, "%s: codes / residuals is NULL", fn);
+  if (((uintptr_t)Q & 15) != 0) return fail(TMS_ERR_INVALID, "%s: Q must be 16-byte aligned", fn);
+  if ((((uintptr_t)residuals) & (nbits - 1)) != 0)
+    return fail(TMS_ERR_INVALID, "%s: residuals must be %d-byte aligned", fn, nbits);
+  if (nq > ((int64_t)1 << 24)) return fail(TMS_ERR_UNSUPPORTED, "%s: too many query tokens", fn);
+  ResArgs a;
+  memset(&a, 0, sizeof(a));
+  a.Q = (const uint8_t*)Q;
+  a.centroids = (const uint8_t*)centroids;
+  a.codes = codes;
+  a.residuals = residuals;
+  a.offsets = offsets;
+  a.pids = pids;
+  a.weights = (const uint16_t*)bucket_weights;
+  a.out = out;
+  a.B = B;
+  a.ndocs = ndocs;
+  a.T = total_tokens;
+  a.ncent = ncent;
+  a.pad_len = pad_len;
+  a.nq = (int32_t)nq;
+  a.nbq = (int32_t)((nq + 31) / 32);
+  a.d = (int32_t)d;
+  a.rb = (int32_t)(d * nbits / 8);
+  // about 192 tokens per wave when documents are ColBERT-sized, at least two rounds of the
+  // chip's resident waves
+  const int64_t hint = ndocs > 0 ? total_tokens / ndocs : 1;
+  int64_t dpw = hint > 0 ? 192 / hint : 1;
+  if (dpw > 1 && B / dpw < (int64_t)256 * 16 * 2) dpw = B / ((int64_t)256 * 16 * 2);
+  if (dpw < 1) dpw = 1;
+  if (dpw > 64) dpw = 64;
+  a.docs_per_wave = (int32_t)dpw;
+  const int64_t grid = ((B + dpw - 1) / dpw + 3) / 4;
+  for (int blk = 0; blk < a.nbq; blk++) {
+    a.blk0 = blk;
+    switch (d / 32) {
+      case 1: rc = launch_fused_ks<1>(a, nbits, grid, st); break;
+      case 2: rc = launch_fused_ks<2>(a, nbits, grid, st); break;
+      case 3: rc = launch_fused_ks<3>(a, nbits, grid, st); break;
+      default: rc = launch_fused_ks<4>(a, nbits, grid, st); break;
+    }
+    if (rc) return rc;
+  }
+  return TMS_OK;
+}
+
+}  // extern "C"
