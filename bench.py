@@ -6,9 +6,11 @@ Gaussian embeddings (~46 GB resident in HBM). One step scores every query agains
 every document with ``flash_maxsim_v2_multiquery`` (one HBM pass over the corpus per
 query, as the reference's V2-MQ kernel) and takes the top-100 per query.
 
-Other workloads (``--config``): c1 (CPU-sized plumbing check), c3 (2M
-variable-length documents), c4 (d-tiled, ``--d 256|512|768``), c5 (PQ/ADC, 5M
-documents of uint8 codes).
+Other workloads (``--config``): c1 (CPU-sized plumbing check), c2b (C2 with all 64
+queries through the batched-query kernel), c3 (2M variable-length documents), c4
+(d-tiled, ``--d 256|512|768``), c5 (PQ/ADC, 5M documents of uint8 codes), c6 (C3's
+corpus as a ColBERTv2 residual-compressed index, fused decode + MaxSim), copy (counter
+calibration).
 
 Prints ONE JSON line on stdout. ``value`` is (query, document) pairs scored per second
 over the whole step; ``roofline`` is the dominant kernel's algorithmic bandwidth from
@@ -42,7 +44,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c4", "c5", "copy"])
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c4", "c5", "c6", "copy"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -204,6 +206,89 @@ class Varlen(Dense):
                          f"first {n} docs x query 0, numpy fp32 per-token sims + segmented max, repeated")
 
 
+class Residual(Varlen):
+    """C3's corpus shape stored as a ColBERTv2 residual-compressed index (colbert-ai 0.2.22
+    codec, nbits=2): int32 centroid ids + 32-byte residual rows per token, 2^18 fp16
+    centroids (ColBERT's choice, 2^floor(log2(16 sqrt(#tokens))), for ~332M tokens).
+    Each query is scored by the fused decode + MaxSim kernel (flashmaxsim_score_residual,
+    plain MaxSim semantics): the decompressed tokens never exist in memory."""
+    kernel = "residual_maxsim_kernel"
+
+    def __init__(self, torch, n_queries, B, lo, hi, d=128, nbits=2, ncent=1 << 18, Nq=32, topk=100):
+        self.torch, self.nQ, self.B, self.d, self.Nq, self.k = torch, n_queries, B, d, Nq, topk
+        self.nbits, self.ncent = nbits, ncent
+        self.name = "c6"
+        rng = np.random.default_rng(77)
+        lens = rng.integers(lo, hi + 1, size=B)
+        offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        self.T = int(offs[-1])
+        self.lo, self.hi = lo, hi
+        self.rb = d * nbits // 8
+        gen = torch.Generator(device="cuda").manual_seed(4321)
+        log(f"[bench] generating a residual index: {B} varlen docs, {self.T} tokens, {ncent} centroids, "
+            f"nbits={nbits} ({self.T * (4 + self.rb) / 1e9:.2f} GB)")
+        self.codes = torch.randint(0, ncent, (self.T,), dtype=torch.int32, device="cuda", generator=gen)
+        self.res = torch.randint(0, 256, (self.T, self.rb), dtype=torch.uint8, device="cuda", generator=gen)
+        self.centroids = normalized_fp16(torch, (ncent, d), gen)
+        # bucket weights at the quantiles of a small residual spread, as the codec fits them
+        self.weights = torch.tensor(np.sort(np.random.default_rng(5).normal(0, 0.04, 1 << nbits)),
+                                    dtype=torch.float16, device="cuda")
+        self.offsets = torch.from_numpy(offs).cuda()
+        self.Q = normalized_fp16(torch, (n_queries, Nq, d), gen)
+        self.scores = torch.empty(n_queries, B, dtype=torch.float32, device="cuda")
+        self._score(0, validate=True)  # offsets checked once, at load
+
+    def _score(self, i, validate=False):
+        from tilemaxsim_amd import flashmaxsim_score_residual
+        return flashmaxsim_score_residual(self.Q[i], self.codes, self.res, self.centroids, self.weights, self.nbits,
+                                          self.offsets, padding="mask", validate=validate)
+
+    def step(self, timer):
+        for i in range(self.nQ):
+            s = timer(lambda: self._score(i))
+            self.scores[i].copy_(s)
+        return topk_rows(self.scores, self.k)
+
+    def bytes_per_launch(self):  # the compressed index streamed once, plus the centroid table once
+        return (self.Nq * self.d * 2 + self.T * (4 + self.rb) + (self.B + 1) * 8 + self.B * 4
+                + self.ncent * self.d * 2)
+
+    def unfused_ms(self):
+        """The unfused flow for comparison (outside the timed steps): decompress the whole
+        index into fp16 tokens in HBM, then varlen MaxSim over them, for one query."""
+        from tilemaxsim_amd import decompress_residual, flash_maxsim_multi_doc
+        torch = self.torch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        D = decompress_residual(self.codes, self.res, self.centroids, self.weights, self.nbits)
+        flash_maxsim_multi_doc(self.Q[0], D, self.offsets, validate=False)
+        e1.record()
+        torch.cuda.synchronize()
+        del D
+        return e0.elapsed_time(e1)
+
+    def config(self):
+        return {"workload": f"c6: residual-compressed c3 corpus, {self.nQ} queries x {self.B:,} docs "
+                            f"(Nd~U[{self.lo},{self.hi}], {self.T:,} tokens), nbits={self.nbits}, "
+                            f"{self.ncent:,} centroids, Nq={self.Nq}, d={self.d}, top-{self.k} per query",
+                "queries": self.nQ, "docs": self.B, "tokens": self.T, "Nq": self.Nq, "d": self.d,
+                "nbits": self.nbits, "centroids": self.ncent, "top_k": self.k,
+                "kernel": "flashmaxsim_score_residual (decode in registers + MFMA)",
+                "roofline_bytes": "compressed index bytes (codes + residuals + offsets) + centroid table per launch"}
+
+    def cpu_baseline(self, seconds, threads):
+        from oracle import residual_oracle as ro
+        n = 2000
+        offs = self.offsets[: n + 1].cpu().numpy()
+        t = int(offs[-1])
+        Q = self.Q[0].cpu().numpy()
+        codes, res = self.codes[:t].cpu().numpy(), self.res[:t].cpu().numpy()
+        C, w = self.centroids.cpu().numpy(), self.weights.cpu().numpy()
+        return _time_cpu(lambda: ro.maxsim_residual_f32(Q, codes, res, C, w, self.nbits, offs), n, seconds, threads,
+                         f"first {n} docs x query 0, numpy decompress (restated codec) then fp32 varlen MaxSim, "
+                         "repeated")
+
+
 class PQ:
     kernel = "pq_mfma_score_kernel"
 
@@ -327,6 +412,8 @@ def main():
         wl = Dense(torch, 16, 200_000, 128, args.d, name=f"c4_d{args.d}")
     elif args.config == "c5":
         wl = PQ(torch, 32, 5_000_000, 128)
+    elif args.config == "c6":
+        wl = Residual(torch, 32, 2_000_000, 32, 300)
     else:
         wl = Copy(torch)
     torch.cuda.synchronize()
@@ -367,6 +454,8 @@ def main():
         threads = max(1, min(16, os.cpu_count() or 1))
         log(f"[bench] CPU baseline on {threads} threads, ~{args.cpu_seconds:.0f} s")
         cpu = wl.cpu_baseline(args.cpu_seconds, threads)
+    if hasattr(wl, "unfused_ms"):  # after the timed steps: needs a decompressed copy of the corpus
+        roofline["unfused_decompress_then_score_ms"] = round(wl.unfused_ms(), 3)
 
     pairs = wl.pairs_per_step()
     out = {

@@ -119,28 +119,39 @@ __device__ __forceinline__ u32x4 add_chunk(u32x4 c, u32x4 w, float& n2) {
   return v;
 }
 
-// Wave-uniform read of read-only data through the constant address space: a scalar load
-// (counted by lgkmcnt), so waiting for it never waits for the vector loads in flight.
-__device__ __forceinline__ int64_t load_uniform(const int64_t* p, int64_t i) {
-  typedef const __attribute__((address_space(4))) int64_t* const_ptr;
-  return ((const_ptr)p)[i];
-}
-
 // 1 / fp16(sqrt(n2)): the codec's half-precision norm (clamped at the smallest fp16 > 0).
 __device__ __forceinline__ float inv_norm(float n2) {
   float n = (float)(_Float16)sqrtf(n2);
   return 1.0f / fmaxf(n, 5.9604645e-8f);
 }
 
+template <int K>
+struct RingSlot {
+  static constexpr int value = K;
+};
+
 // ---------------------------------------------------------------------------------
 // Fused MaxSim. One wave streams whole documents; a tile is 16 * NSUB tokens x d.
-// Centroid ids are read two tiles ahead and the centroid chunks and residual bytes one
-// tile ahead of the tile being decoded and scored.
-template <int KS, int NBITS, int NSUB>
+// Centroid ids are read three tiles ahead and the centroid chunks and residual bytes
+// two tiles ahead of the tile being decoded and scored.
+// QLDS: the query fragments sit in LDS (shared by the workgroup's four waves) instead of
+// 8 * KS VGPRs per lane, which buys occupancy.
+template <int KS, int NBITS, int NSUB, bool QLDS>
 __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
   constexpr int TT = 16 * NSUB;
   __shared__ __attribute__((aligned(16))) uint8_t lut[4096];
+  __shared__ u32x4 qsh[QLDS ? KS * 2 * 64 : 1];
   build_lut<NBITS>(lut, a.weights);
+  if constexpr (QLDS) {
+    // fragment (s, h) of lane l: query token 32 blk0 + 16 h + l % 16, chunk 4 s + l / 16
+    for (int f = threadIdx.x; f < KS * 2 * 64; f += kThreads) {
+      const int l = f & 63, h = (f >> 6) & 1, s = f >> 7;
+      const int tok = a.blk0 * 32 + 16 * h + (l & 15);
+      const int64_t row = tok < a.nq ? tok : a.nq - 1;
+      const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + (l >> 4))) * 2);
+      qsh[f] = tok < a.nq ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
@@ -153,35 +164,62 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
   const float NEG_INF = -__builtin_inff();
 
   // query block a.blk0: query tokens 32 * blk0 + 16 h + r
-  u32x4 qf[KS][2];
+  u32x4 qf[QLDS ? 1 : KS][2];
   bool qvalid[2];
 #pragma unroll
   for (int h = 0; h < 2; h++) {
     const int tok = a.blk0 * 32 + 16 * h + r;
     qvalid[h] = tok < a.nq;
-    const int64_t row = qvalid[h] ? tok : a.nq - 1;  // loaded unconditionally, zeroed below
+    if constexpr (!QLDS) {
+      const int64_t row = qvalid[h] ? tok : a.nq - 1;  // loaded unconditionally, zeroed below
 #pragma unroll
-    for (int s = 0; s < KS; s++) {
-      const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2);
-      qf[s][h] = qvalid[h] ? v : u32x4{0u, 0u, 0u, 0u};
+      for (int s = 0; s < KS; s++) {
+        const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2);
+        qf[s][h] = qvalid[h] ? v : u32x4{0u, 0u, 0u, 0u};
+      }
     }
   }
+  auto qfrag = [&](int s, int h) -> u32x4 {
+    if constexpr (QLDS) {
+      // the empty asm hides the index from the optimiser, which would otherwise hoist
+      // these loop-invariant reads into registers and undo the point of QLDS
+      uint32_t idx = (uint32_t)((s * 2 + h) * 64 + lane);
+      asm volatile("" : "+v"(idx));
+      return qsh[idx];
+    } else {
+      return qf[s][h];
+    }
+  };
 
   // ---- documents ---------------------------------------------------------------
+  // A cursor is a tile position: document position b in [b_begin, b_end), its first
+  // index row, its length (< 2^31 tokens) and the tile's first token. All of it is
+  // wave-uniform and lives in scalar registers.
   struct Cur {
-    int64_t b;     // position in [b_begin, b_end)
-    int64_t base;  // first index row
-    int64_t len;   // tokens
-    int64_t t0;    // first token of the tile
+    int64_t b, base;
+    int32_t len, t0;
   };
-  // Bounds of document position b: len < 0 marks an invalid pid or offsets.
+  // The wave's documents (at most 64) are read once, lane j holding document
+  // b_begin + j: base row and length (-1 for an invalid pid or offsets). The walk
+  // below takes them with readlane, so crossing a document never waits for memory.
+  int64_t dbase = 0;
+  int32_t dlen = -1;
+  if (b_begin + lane < b_end) {
+    const int64_t p = a.pids ? a.pids[b_begin + lane] : b_begin + lane;
+    if (p >= 0 && p < a.ndocs) {
+      const int64_t s0 = a.offsets[p], e0 = a.offsets[p + 1];
+      if (s0 >= 0 && e0 >= s0 && e0 <= a.T && e0 - s0 <= 0x7fffffff) {
+        dbase = s0;
+        dlen = (int32_t)(e0 - s0);
+      }
+    }
+  }
   auto bounds = [&](int64_t b, int64_t& base) -> int64_t {
-    const int64_t p = a.pids ? load_uniform(a.pids, b) : b;
-    if (p < 0 || p >= a.ndocs) return -1;
-    const int64_t s = load_uniform(a.offsets, p), e = load_uniform(a.offsets, p + 1);
-    if (s < 0 || e < s || e > a.T) return -1;
-    base = s;
-    return e - s;
+    const int j = (int)(b - b_begin);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)dbase, j);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)dbase >> 32), j);
+    base = (int64_t)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_readlane(dlen, j);
   };
   const bool first_blk = a.blk0 == 0;
   auto write = [&](int64_t b, float v) {
@@ -190,30 +228,31 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
       *o = first_blk ? v : *o + v;
     }
   };
-  // Move to the first document at or after b with a token; write_skipped: score the
-  // skipped ones (only the cursor that scores does this). Past the last document the
-  // cursor keeps its last tile's rows, so prefetches through it stay in bounds.
-  auto seek = [&](Cur& c, int64_t b, bool write_skipped) {
+  // Move to the first document at or after b with a token, scoring the empty (or
+  // invalid) ones on the way. Past the last document the cursor keeps its last tile's
+  // rows, so prefetches through it stay in bounds.
+  auto seek = [&](Cur& c, int64_t b) {
     for (; b < b_end; b++) {
       int64_t base = 0;
       const int64_t len = bounds(b, base);
       if (len > 0) {
         c.b = b;
         c.base = base;
-        c.len = len;
+        c.len = (int32_t)len;
         c.t0 = 0;
         return;
       }
-      if (write_skipped) write(b, len < 0 ? __builtin_bit_cast(float, 0x7fc00000u) : (a.pad_len > 0 ? 0.f : NEG_INF));
+      write(b, len < 0 ? __builtin_bit_cast(float, 0x7fc00000u) : (a.pad_len > 0 ? 0.f : NEG_INF));
     }
     c.b = b_end;
   };
-  auto advance = [&](Cur& c, bool write_skipped) {
+  auto advance = [&](Cur& c) {
+    if (c.b >= b_end) return;
     c.t0 += TT;
-    if (c.t0 >= c.len) seek(c, c.b + 1, write_skipped);
+    if (c.t0 >= c.len) seek(c, c.b + 1);
   };
   auto row_of = [&](const Cur& c, int sub) -> int64_t {
-    int64_t t = c.t0 + 16 * sub + r;
+    int32_t t = c.t0 + 16 * sub + r;
     if (t > c.len - 1) t = c.len - 1;
     return c.base + t;
   };
@@ -243,7 +282,7 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
   };
 
   float rmax[2] = {NEG_INF, NEG_INF};
-  auto finish = [&](int64_t b, int64_t len) {
+  auto finish = [&](int64_t b, int32_t len) {
     const bool padded = len < a.pad_len;
     float s = 0.f;
 #pragma unroll
@@ -270,8 +309,8 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
 #pragma unroll
       for (int s = 0; s < KS; s++) {
         const u32x4 v = add_chunk(bd.cen[sub][s], chunk_weights<NBITS>(lut, bd.res[sub][s]), n2);
-        acc[0] = mfma16x16x32<TMS_DTYPE_F16>(v, qf[s][0], acc[0]);
-        acc[1] = mfma16x16x32<TMS_DTYPE_F16>(v, qf[s][1], acc[1]);
+        acc[0] = mfma16x16x32<TMS_DTYPE_F16>(v, qfrag(s, 0), acc[0]);
+        acc[1] = mfma16x16x32<TMS_DTYPE_F16>(v, qfrag(s, 1), acc[1]);
       }
       n2 += __shfl_xor(n2, 16);
       n2 += __shfl_xor(n2, 32);
@@ -287,32 +326,40 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
     if (c.t0 + TT >= c.len) finish(c.b, c.len);
   };
 
-  // Tile i is scored from `cur` while tile i+1's body lands in `nxt` and tile i+2's ids
-  // in `ids`; the loop body runs twice with the two bodies' roles swapped, so every
-  // register is fixed at compile time.
-  Cur c_cur, c_nxt;
-  int32_t ids[NSUB];
-  Body b0, b1;
-  seek(c_cur, b_begin, true);
-  if (c_cur.b >= b_end) return;
-  load_codes(ids, c_cur);
-  load_body(ids, c_cur, b0);
-  c_nxt = c_cur;
-  advance(c_nxt, false);
-  load_codes(ids, c_nxt);
-  auto step = [&](Body& cur, Body& nxt) -> bool {
-    load_body(ids, c_nxt, nxt);
-    Cur c_far = c_nxt;
-    if (c_far.b < b_end) advance(c_far, false);
-    load_codes(ids, c_far);
-    compute(c_cur, cur);
-    advance(c_cur, true);
-    c_nxt = c_far;
-    return c_cur.b >= b_end;
+  // A ring of three tiles. While tile i is scored, the bodies of tiles i+1 and i+2 and
+  // the ids of tile i+3 are in flight. Each step issues the ids of tile i+3 before the
+  // body of tile i+2, so waiting for the ids of tile i+2 (issued a step earlier, before
+  // the body of tile i+1) never waits for the later loads. One cursor walks ahead (and
+  // scores empty documents as it passes them); the ring keeps its positions. The step
+  // is unrolled three times, so every ring slot is a compile-time register.
+  Body bd[3];
+  int32_t ids[3][NSUB];
+  Cur cr[3];
+  Cur walk;
+  seek(walk, b_begin);
+  if (walk.b >= b_end) return;
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    cr[k] = walk;
+    load_codes(ids[k], walk);
+    advance(walk);
+  }
+  load_body(ids[0], cr[0], bd[0]);
+  load_body(ids[1], cr[1], bd[1]);
+  auto step = [&](auto slot) -> bool {
+    constexpr int k = decltype(slot)::value;  // tile i sits in ring slot k
+    const Cur c = cr[k];
+    cr[k] = walk;                                            // tile i+3
+    advance(walk);
+    load_codes(ids[k], cr[k]);
+    load_body(ids[(k + 2) % 3], cr[(k + 2) % 3], bd[(k + 2) % 3]);  // tile i+2
+    compute(c, bd[k]);                                       // tile i
+    return cr[(k + 1) % 3].b >= b_end;                       // tile i+1 exists?
   };
   while (true) {
-    if (step(b0, b1)) return;
-    if (step(b1, b0)) return;
+    if (step(RingSlot<0>{})) return;
+    if (step(RingSlot<1>{})) return;
+    if (step(RingSlot<2>{})) return;
   }
 }
 
@@ -362,6 +409,9 @@ __global__ void residual_fill_kernel(float* out, int64_t n, float v) {
 
 // ---------------------------------------------------------------------------------
 // host side
+#ifndef TMS_RES_TOKENS_PER_WAVE
+#define TMS_RES_TOKENS_PER_WAVE 768  // document tokens one wave streams (rounded to whole documents)
+#endif
 static int check_format(const char* fn, int64_t d, int nbits, int64_t ncent, const void* centroids,
                         const void* weights) {
   if (nbits != 1 && nbits != 2 && nbits != 4)
@@ -374,12 +424,16 @@ static int check_format(const char* fn, int64_t d, int nbits, int64_t ncent, con
   return TMS_OK;
 }
 
+#ifndef TMS_RES_QLDS
+#define TMS_RES_QLDS 1  // query fragments in LDS
+#endif
 template <int KS>
 static int launch_fused_ks(const ResArgs& a, int nbits, int64_t grid, hipStream_t st) {
   constexpr int kNSub = 1;
-  if (nbits == 1) hipLaunchKernelGGL((residual_maxsim_kernel<KS, 1, kNSub>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  else if (nbits == 2) hipLaunchKernelGGL((residual_maxsim_kernel<KS, 2, kNSub>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((residual_maxsim_kernel<KS, 4, kNSub>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  constexpr bool kQlds = TMS_RES_QLDS;
+  if (nbits == 1) hipLaunchKernelGGL((residual_maxsim_kernel<KS, 1, kNSub, kQlds>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else if (nbits == 2) hipLaunchKernelGGL((residual_maxsim_kernel<KS, 2, kNSub, kQlds>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((residual_maxsim_kernel<KS, 4, kNSub, kQlds>), dim3((unsigned)grid), dim3(256), 0, st, a);
   return check_launch("residual_maxsim_kernel");
 }
 
@@ -463,13 +517,13 @@ int tms_maxsim_residual(const void* Q, int64_t nq, int64_t d, const void* centro
   a.nbq = (int32_t)((nq + 31) / 32);
   a.d = (int32_t)d;
   a.rb = (int32_t)(d * nbits / 8);
-  // about 192 tokens per wave when documents are ColBERT-sized, at least two rounds of the
-  // chip's resident waves
+  // about TMS_RES_TOKENS_PER_WAVE tokens per wave (whole documents), at least two rounds
+  // of the chip's resident waves
   const int64_t hint = ndocs > 0 ? total_tokens / ndocs : 1;
-  int64_t dpw = hint > 0 ? 192 / hint : 1;
+  int64_t dpw = hint > 0 ? TMS_RES_TOKENS_PER_WAVE / hint : 1;
   if (dpw > 1 && B / dpw < (int64_t)256 * 16 * 2) dpw = B / ((int64_t)256 * 16 * 2);
   if (dpw < 1) dpw = 1;
-  if (dpw > 64) dpw = 64;
+  if (dpw > 64) dpw = 64;  // one lane per document holds its bounds
   a.docs_per_wave = (int32_t)dpw;
   const int64_t grid = ((B + dpw - 1) / dpw + 3) / 4;
   for (int blk = 0; blk < a.nbq; blk++) {

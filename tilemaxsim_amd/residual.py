@@ -126,9 +126,6 @@ def flashmaxsim_score_residual(Q: torch.Tensor, codes: torch.Tensor, residuals: 
     scores = torch.empty(B, dtype=torch.float32, device=dev)
     if B == 0:
         return scores
-    lengths = offsets[1:] - offsets[:-1]
-    if pids is not None:
-        lengths = lengths[pids.clamp(0, max(ndocs - 1, 0))] if ndocs > 0 else lengths.new_zeros(B)
     if validate:
         bad = bool((offsets[1:] < offsets[:-1]).any()) or int(offsets[0]) < 0 or int(offsets[-1]) > T
         if pids is not None and B > 0:
@@ -136,7 +133,12 @@ def flashmaxsim_score_residual(Q: torch.Tensor, codes: torch.Tensor, residuals: 
         if bad:
             raise ValueError("flashmaxsim_score_residual: doc_offsets must be non-decreasing within [0, T] and "
                              "pids within [0, ndocs)")
-    pad_len = int(lengths.max()) if (padding == "zeros" and B > 0) else 0
+    pad_len = 0
+    if padding == "zeros" and ndocs > 0:  # the longest scored document (one host sync)
+        lengths = offsets[1:] - offsets[:-1]
+        if pids is not None:
+            lengths = lengths[pids.clamp(0, ndocs - 1)]
+        pad_len = max(int(lengths.max()), 0)
     lib = _lib.load()
     with torch.cuda.device(dev):
         _lib.check(lib.tms_maxsim_residual(Q2.data_ptr(), Q2.shape[0], d, centroids.data_ptr(), centroids.shape[0],
