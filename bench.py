@@ -143,6 +143,10 @@ class DenseBatched(Dense):
     moves the path from the HBM roof to the MFMA roof."""
     MFMA_PEAK_TFLOPS = 2500.0
 
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        self.kernel = "batched_maxsim_kernel"
+
     def step(self, timer):
         from tilemaxsim_amd import flash_maxsim_batched_queries
         s = timer(lambda: flash_maxsim_batched_queries(self.Q, self.D))
@@ -152,7 +156,7 @@ class DenseBatched(Dense):
     def flops_per_launch(self):
         return 2 * self.nQ * self.Nq * self.B * self.Nd * self.d
 
-    def bytes_per_launch(self):  # every query against one read of the corpus
+    def bytes_per_launch(self):  # algorithmic: every query against one read of the corpus
         return self.nQ * self.Nq * self.d * 2 + self.B * self.Nd * self.d * 2 + self.nQ * self.B * 4
 
     def config(self):
