@@ -10,6 +10,7 @@ import pytest
 
 from oracle import c_oracle
 from oracle import maxsim_oracle as orc
+from oracle import residual_oracle as ro
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -34,6 +35,18 @@ def test_fixtures_reproduce_on_cpu():
     np.testing.assert_allclose(orc.pq_decompress_score(f["Q"], f["codebook"], f["codes"], f64=True), f["scores"],
                                rtol=1e-12)
     np.testing.assert_allclose(orc.pq_build_lut(f["Q"], f["codebook"])[:2], f["lut_q01"], rtol=1e-5, atol=1e-6)
+    f = _load("packed_zeros_d128.npz")
+    np.testing.assert_allclose(orc.maxsim_packed_zero_padded(f["Q"], f["D_packed"], f["lengths"]), f["scores"],
+                               rtol=1e-12)
+    f = _load("residual_d128_nb2.npz")
+    args = (f["codes"], f["residuals"], f["centroids"], f["bucket_weights"], 2)
+    assert np.array_equal(ro.decompress(*args), f["decompressed"])
+    pad = int((f["offsets"][1:] - f["offsets"][:-1])[f["pids"]].max())
+    for name, p in (("scores_zeros", pad), ("scores_mask", 0)):
+        got = ro.maxsim_residual(f["Q"], *args, f["offsets"], f["pids"], p)
+        assert np.array_equal(np.isinf(got), np.isinf(f[name]))
+        fin = ~np.isinf(got)
+        np.testing.assert_allclose(got[fin], f[name][fin], rtol=1e-12)
 
 
 def _close(got, ref):
@@ -61,3 +74,14 @@ def test_fixtures_on_gpu(cuda):
         _close(pq.score_batch(g(f["Q"]), g(f["codes"]), method=method).cpu().numpy(), f["scores"])
     lut = pq.build_distance_table(g(f["Q"])).cpu().numpy()
     np.testing.assert_allclose(lut[:2], f["lut_q01"], rtol=1e-5, atol=1e-5)
+    f = _load("packed_zeros_d128.npz")
+    got = tms.flashmaxsim_score_packed(g(f["Q"]), g(f["D_packed"]), torch.from_numpy(f["lengths"]))
+    _close(got.cpu().numpy(), f["scores"])
+    f = _load("residual_d128_nb2.npz")
+    idx = (g(f["codes"]), g(f["residuals"]), g(f["centroids"]), g(f["bucket_weights"]), 2)
+    dec = tms.decompress_residual(*idx).cpu().numpy()
+    ulps = np.abs(dec.view(np.int16).astype(np.int32) - f["decompressed"].view(np.int16).astype(np.int32))
+    assert ulps.max() <= 1
+    for name, padding in (("scores_zeros", "zeros"), ("scores_mask", "mask")):
+        got = tms.flashmaxsim_score_residual(g(f["Q"]), *idx, g(f["offsets"]), g(f["pids"]), padding=padding)
+        _close(got.cpu().numpy(), f[name])
