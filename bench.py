@@ -317,6 +317,19 @@ class PQ:
     def bytes_per_launch(self):
         return self.B * self.Nd * self.M  # code bytes: the north-star roofline for PQ
 
+    def extra_roofline(self, launch_ms):
+        """Beside the code-bytes roofline: the reference's own PQ IO formula
+        (src/benchmark.py:226: table + codes + output) and the LDS roof of this kernel's
+        codebook gather (16 B per code per token, against 128 B/clk/CU x 256 CUs at
+        2.4 GHz = 78.6 TB/s)."""
+        ref_bytes = self.Nq * self.M * self.K * 4 + self.B * self.Nd * self.M + self.B * self.Nq * 4
+        lds_bytes = self.B * self.Nd * self.M * 16
+        lds_tbs = lds_bytes / (launch_ms * 1e-3) / 1e12
+        return {"bytes_reference_formula": ref_bytes,
+                "gbs_reference_formula": round(ref_bytes / (launch_ms * 1e-3) / 1e9, 1),
+                "lds_gather_bytes_per_launch": lds_bytes, "lds_gather_tbs": round(lds_tbs, 2),
+                "lds_peak_tbs": 78.6, "lds_frac": round(lds_tbs / 78.6, 4)}
+
     def pairs_per_step(self):
         return self.nQ * self.B
 
@@ -458,6 +471,8 @@ def main():
         threads = max(1, min(16, os.cpu_count() or 1))
         log(f"[bench] CPU baseline on {threads} threads, ~{args.cpu_seconds:.0f} s")
         cpu = wl.cpu_baseline(args.cpu_seconds, threads)
+    if hasattr(wl, "extra_roofline"):
+        roofline.update(wl.extra_roofline(k_mean))
     if hasattr(wl, "unfused_ms"):  # after the timed steps: needs a decompressed copy of the corpus
         roofline["unfused_decompress_then_score_ms"] = round(wl.unfused_ms(), 3)
 
