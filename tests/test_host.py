@@ -148,6 +148,33 @@ def test_python_errors_before_device_checks():
         TileMaxSimPQ(torch.zeros(16, 256, 8, dtype=torch.float16))
 
 
+def test_residual_python_errors_before_device_checks():
+    from tilemaxsim_amd import decompress_residual, flashmaxsim_score_residual
+    codes = torch.zeros(10, dtype=torch.int32)
+    res = torch.zeros(10, 32, dtype=torch.uint8)
+    cent = torch.zeros(4, 128, dtype=torch.float16)
+    w = torch.zeros(4, dtype=torch.float16)
+    with pytest.raises(NotImplementedError, match="nbits"):
+        decompress_residual(codes, res, cent, w, 3)
+    with pytest.raises(ValueError, match="residual rows"):
+        decompress_residual(codes, res[:, :16], cent, w, 2)
+    with pytest.raises(ValueError, match="disagree"):
+        decompress_residual(codes[:9], res, cent, w, 2)
+    with pytest.raises(TypeError, match="uint8"):
+        decompress_residual(codes, res.to(torch.int16), cent, w, 2)
+    with pytest.raises(TypeError, match="int32 or int64"):
+        decompress_residual(codes.float(), res, cent, w, 2)
+    with pytest.raises(ValueError, match="2\\*\\*nbits"):
+        decompress_residual(codes, res, cent, w[:3], 2)
+    with pytest.raises(ValueError, match="GPU"):
+        decompress_residual(codes, res, cent, w, 2)  # CPU tensors: no CPU path
+    offs = torch.tensor([0, 4, 10])
+    with pytest.raises(ValueError, match="padding"):
+        flashmaxsim_score_residual(torch.zeros(32, 128), codes, res, cent, w, 2, offs, padding="none")
+    with pytest.raises(ValueError, match="GPU"):
+        flashmaxsim_score_residual(torch.zeros(32, 128), codes, res, cent, w, 2, offs)
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     from tilemaxsim_amd import _lib
     monkeypatch.setattr(_lib, "_lib", None)
