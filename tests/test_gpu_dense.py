@@ -274,10 +274,12 @@ def test_batched_queries(cuda):
     import torch
     from tilemaxsim_amd import flash_maxsim_batched_queries, flash_maxsim_v2_multiquery
     rng = _rng(31)
-    # (5, 32): 5 blocks, query-split kernel; (3, 20): 3 blocks, per-pass kernel;
-    # (4, 70): 3 blocks per query, split with 3 blocks per wave; (37, 32): three split
-    # launches, the last one partial; (6, 128): 4 blocks per query
-    for nQ, Nq in [(5, 32), (3, 20), (4, 70), (37, 32), (6, 128)]:
+    # Batched kernel, 8 waves per workgroup holding 1, 2 or 4 blocks each:
+    # (5, 32): 1 block per wave, 5 of 8 waves used; (12, 32): 2 per wave; (7, 64): 2 per
+    # wave, one query each; (4, 70): 3 blocks per query, 3 per wave; (37, 32): 4 per
+    # wave, two launches, the second partial; (6, 128): 4 blocks per query.
+    # (3, 20): 3 blocks, the per-pass stream kernel.
+    for nQ, Nq in [(5, 32), (12, 32), (7, 64), (3, 20), (4, 70), (37, 32), (6, 128)]:
         Qs = _to_gpu(_randn(rng, (nQ, Nq, 128), normalize=True))
         D = _to_gpu(_randn(rng, (400, 60, 128), normalize=True))
         got = flash_maxsim_batched_queries(Qs, D).cpu().numpy()

@@ -20,6 +20,26 @@
 
 namespace tms {
 
+// Max over lanes l, l^16, l^32, l^48 (the four 16-lane rows) with gfx950's cross-row swaps.
+__device__ __forceinline__ float cross_row_max(float m) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, m), __builtin_bit_cast(unsigned, m), false, false);
+  m = fmaxf(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
+  const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, m), __builtin_bit_cast(unsigned, m), false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)q[0]), __builtin_bit_cast(float, (unsigned)q[1]));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+// Sum over the 16 lanes of a row; every lane of the row receives it.
+__device__ __forceinline__ float row_sum16(float s) {
+  s += dpp_f32<0xB1>(s);   // quad_perm [1,0,3,2]
+  s += dpp_f32<0x4E>(s);   // quad_perm [2,3,0,1]
+  s += dpp_f32<0x141>(s);  // row_half_mirror: the other quad of each half-row
+  s += dpp_f32<0x140>(s);  // row_mirror: the other half of the row
+  return s;
+}
+
 struct StreamArgs {
   const uint8_t* Q;  // (nQ * nq, d)
   const uint8_t* D;  // (B, nd, d)
@@ -192,16 +212,18 @@ struct RingSlotS {
   static constexpr int value = K;
 };
 
-// Batched queries, tiles shared through LDS. The four waves of a workgroup stream the
-// same documents; wave w holds a.nblk query blocks (whole queries) in VGPRs, so one pass
-// over D serves up to 16 blocks. Each 16-token tile is loaded from memory once per
-// workgroup: wave w loads k-step w (lane (r, g): chunk 4 w + g of token r, the MFMA
-// A-operand layout) and stores it to a three-slot LDS ring; after a barrier every wave
-// reads the tile's KS k-steps from LDS. A wave keeps one 16-byte load per lane in
-// flight per tile, PFD tiles ahead, so the workgroup has PFD whole tiles in flight.
-// The barriers fence LDS only, so they never wait for the loads in flight.
+// Batched queries, tiles shared through LDS. The eight waves of a workgroup (one per CU,
+// two per SIMD) stream the same documents; wave w holds a.nblk query blocks (whole
+// queries) in VGPRs, so one pass over D serves up to 8 * a.nblk blocks. Each 16-token
+// tile is loaded from memory once per workgroup: wave w < KS loads k-step w (lane
+// (r, g): chunk 4 w + g of token r, the MFMA A-operand layout) and stores it to a
+// three-slot LDS ring; after a barrier every wave reads the tile's KS k-steps from LDS.
+// A loading wave keeps one 16-byte load per lane in flight per tile, PFD tiles ahead.
+// The barriers fence LDS only, so they never wait for the loads in flight. The MFMA
+// cluster of each tile runs at raised wave priority, so a wave that has its operands
+// keeps the matrix pipe fed ahead of the other wave's bookkeeping.
 template <int DT, int KS, int NB, int PFD>
-__global__ void __launch_bounds__(256, 2) batched_maxsim_kernel(StreamArgs a) {
+__global__ void __launch_bounds__(512, 1) batched_maxsim_kernel(StreamArgs a) {
   static_assert(PFD >= 2, "tile i+1 is stored to LDS after tile i+PFD's load is issued");
   static_assert(PFD <= 6 && PFD % 2 == 0, "the step loop is unrolled PFD (even, <= 6) times");
   constexpr int NS = 3;  // LDS ring slots (two would do: a slot is rewritten only after a barrier that follows its last read)
@@ -240,6 +262,14 @@ __global__ void __launch_bounds__(256, 2) batched_maxsim_kernel(StreamArgs a) {
         qf[j][s][h] = v ? *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2) : u32x4{0u, 0u, 0u, 0u};
     }
 
+  bool qv[NB][2];  // query row 16 h + r of block j exists
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      int64_t row;
+      qv[j][h] = q_valid(j, h, row);
+    }
   float pend[NB];
 #pragma unroll
   for (int j = 0; j < NB; j++) pend[j] = NEG_INF;
@@ -300,34 +330,25 @@ __global__ void __launch_bounds__(256, 2) batched_maxsim_kernel(StreamArgs a) {
       f32x4 acc[NB][2];
 #pragma unroll
       for (int j = 0; j < NB; j++) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int s = 0; s < KS; s++)
 #pragma unroll
         for (int j = 0; j < NB; j++)
 #pragma unroll
           for (int h = 0; h < 2; h++) acc[j][h] = mfma16x16x32<DT>(t[s], qf[j][s][h], acc[j][h]);
+      __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int j = 0; j < NB; j++)
 #pragma unroll
-        for (int h = 0; h < 2; h++)
-          rmax[j][h] = fmaxf(rmax[j][h], fmaxf(fmaxf(acc[j][h][0], acc[j][h][1]), fmaxf(acc[j][h][2], acc[j][h][3])));
+        for (int h = 0; h < 2; h++)  // two v_max3 per fragment
+          rmax[j][h] = fmaxf(fmaxf(fmaxf(fmaxf(rmax[j][h], acc[j][h][0]), acc[j][h][1]), acc[j][h][2]), acc[j][h][3]);
       if (++ct == tpd) {  // document cd done: max over rows, sum over query tokens
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-          float s = 0.f;
-#pragma unroll
-          for (int h = 0; h < 2; h++) {
-            float m = rmax[j][h];
-            m = fmaxf(m, __shfl_xor(m, 16));
-            m = fmaxf(m, __shfl_xor(m, 32));
-            int64_t row;
-            s += q_valid(j, h, row) ? m : 0.f;
-            rmax[j][h] = NEG_INF;
-          }
-          s += __shfl_xor(s, 8);
-          s += __shfl_xor(s, 4);
-          s += __shfl_xor(s, 2);
-          s += __shfl_xor(s, 1);
+          float s = (qv[j][0] ? cross_row_max(rmax[j][0]) : 0.f) + (qv[j][1] ? cross_row_max(rmax[j][1]) : 0.f);
+          rmax[j][0] = rmax[j][1] = NEG_INF;
+          s = row_sum16(s);
           pend[j] = lane == (int)cd ? s : pend[j];
         }
         ct = 0;
@@ -370,9 +391,6 @@ __global__ void __launch_bounds__(256, 2) batched_maxsim_kernel(StreamArgs a) {
 #ifndef TMS_STREAM_PFD
 #define TMS_STREAM_PFD 2  // tiles in flight ahead of the one being scored (single-query path)
 #endif
-#ifndef TMS_SPLIT_BLOCKS
-#define TMS_SPLIT_BLOCKS 4  // query blocks held in VGPRs per wave in the batched-query path
-#endif
 #ifndef TMS_STREAM_TOKENS_PER_WAVE
 #define TMS_STREAM_TOKENS_PER_WAVE 192
 #endif
@@ -384,11 +402,13 @@ static int stream_launch(const StreamArgs& a, int64_t grid, hipStream_t st) {
 }
 
 #ifndef TMS_BATCHED_PFD
-#define TMS_BATCHED_PFD 6  // tiles in flight per workgroup in the batched kernel
+#define TMS_BATCHED_PFD 4  // tiles in flight per workgroup in the batched kernel
 #endif
+#define TMS_BATCHED_WAVES 8
 template <int DT, int KS, int NB>
 static int batched_launch(const StreamArgs& a, int64_t grid, hipStream_t st) {
-  hipLaunchKernelGGL((batched_maxsim_kernel<DT, KS, NB, TMS_BATCHED_PFD>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((batched_maxsim_kernel<DT, KS, NB, TMS_BATCHED_PFD>), dim3((unsigned)grid), dim3(64 * TMS_BATCHED_WAVES), 0,
+                     st, a);
   return check_launch("batched_maxsim_kernel");
 }
 template <int DT, int NB>
@@ -398,6 +418,16 @@ static int batched_ks(const StreamArgs& a, int64_t grid, hipStream_t st) {
     case 2: return batched_launch<DT, 2, NB>(a, grid, st);
     case 3: return batched_launch<DT, 3, NB>(a, grid, st);
     default: return batched_launch<DT, 4, NB>(a, grid, st);
+  }
+}
+// Query blocks held in VGPRs per wave in the batched-query path: 1, 2 or kMaxBlocksPerWave.
+constexpr int kMaxBlocksPerWave = 4;
+template <int DT>
+static int batched_nb(int nb, const StreamArgs& a, int64_t grid, hipStream_t st) {
+  switch (nb) {
+    case 1: return batched_ks<DT, 1>(a, grid, st);
+    case 2: return batched_ks<DT, 2>(a, grid, st);
+    default: return batched_ks<DT, kMaxBlocksPerWave>(a, grid, st);
   }
 }
 
@@ -425,23 +455,32 @@ int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, 
   a.nbq = (int32_t)((nq + 31) / 32);
   a.d = (int32_t)d;
   const int64_t nblocks = nQ * (int64_t)a.nbq;
-  const bool split = a.nbq <= TMS_SPLIT_BLOCKS && nblocks >= 4;
+  const bool split = a.nbq <= kMaxBlocksPerWave && nblocks >= 4;
   if (split) {
-    const int per_wave = (TMS_SPLIT_BLOCKS / a.nbq) * a.nbq;
+    // Blocks per wave: the smallest of 1, 2, 4 whose launch covers every block in one
+    // pass (a wave computes all of its slots, used or not), else 4. A wave holds whole
+    // queries, so a query's blocks never span waves or launches.
+    int nb = kMaxBlocksPerWave;
+    for (int c = 1; c < kMaxBlocksPerWave; c *= 2)
+      if (c >= a.nbq && nblocks <= (int64_t)TMS_BATCHED_WAVES * ((c / a.nbq) * a.nbq)) {
+        nb = c;
+        break;
+      }
+    const int per_wave = (nb / a.nbq) * a.nbq;
     int64_t dpw = nd > 0 ? 4096 / nd : 64;  // long streams: each wave loads up to 32 KB of queries
     if (dpw < 1) dpw = 1;
     if (dpw > 64) dpw = 64;
-    const int64_t min_wgs = (int64_t)256 * 4 * 2;
+    const int64_t min_wgs = (int64_t)256 * 4;  // one workgroup per CU, four rounds
     if (dpw > 1 && B / dpw < min_wgs) dpw = B / min_wgs > 0 ? B / min_wgs : 1;
     a.docs_per_wave = (int32_t)dpw;
     a.nblk = per_wave;
     const int64_t grid = (B + dpw - 1) / dpw;
-    const int64_t per_launch = (int64_t)4 * per_wave;
+    const int64_t per_launch = (int64_t)TMS_BATCHED_WAVES * per_wave;
     for (int64_t b0 = 0; b0 < nblocks; b0 += per_launch) {
       a.blk0 = (int32_t)b0;
       a.blk_end = (int32_t)(nblocks - b0 < per_launch ? nblocks : b0 + per_launch);
-      const int rc = dtype == TMS_DTYPE_F16 ? batched_ks<TMS_DTYPE_F16, TMS_SPLIT_BLOCKS>(a, grid, st)
-                                            : batched_ks<TMS_DTYPE_BF16, TMS_SPLIT_BLOCKS>(a, grid, st);
+      const int rc = dtype == TMS_DTYPE_F16 ? batched_nb<TMS_DTYPE_F16>(nb, a, grid, st)
+                                            : batched_nb<TMS_DTYPE_BF16>(nb, a, grid, st);
       if (rc) return rc;
     }
     return TMS_OK;
