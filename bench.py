@@ -9,7 +9,8 @@ query, as the reference's V2-MQ kernel) and takes the top-100 per query.
 Other workloads (``--config``): c1 (CPU-sized plumbing check), c2b (C2 with all 64
 queries through the batched-query kernel), c3 (2M variable-length documents), c4
 (d-tiled, ``--d 256|512|768``), c5 (PQ/ADC, 5M documents of uint8 codes), c6 (C3's
-corpus as a ColBERTv2 residual-compressed index, fused decode + MaxSim), copy (counter
+corpus as a ColBERTv2 residual-compressed index, fused decode + MaxSim per query), c6b
+(the same index, all queries through the batched residual kernel), copy (counter
 calibration).
 
 Prints ONE JSON line on stdout. ``value`` is (query, document) pairs scored per second
@@ -44,7 +45,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c4", "c5", "c6", "copy"])
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c4", "c5", "c6", "c6b", "copy"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -137,6 +138,26 @@ class Dense:
                          "(restates pytorch_maxsim_naive), repeated")
 
 
+def gemm_ceiling(torch, achieved_tflops):
+    """The practical fp16 MFMA ceiling on this part, measured in the same process: a large
+    square fp16 GEMM through torch (hipBLASLt), which runs at the same power-limited clock
+    as any MFMA-bound kernel."""
+    n = 8192
+    a = torch.randn(n, n, device="cuda").half()
+    b = torch.randn(n, n, device="cuda").half()
+    for _ in range(3):
+        torch.mm(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        torch.mm(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    gemm_tf = 2 * n ** 3 / (e0.elapsed_time(e1) / 20 * 1e-3) / 1e12
+    return {"gemm_fp16_8192_tflops": round(gemm_tf, 1), "frac_of_gemm": round(achieved_tflops / gemm_tf, 4)}
+
+
 class DenseBatched(Dense):
     """C2 data, all queries scored by the batched-query entry point: each workgroup's
     eight waves hold 32 query blocks and share one HBM pass over the documents, which
@@ -159,26 +180,10 @@ class DenseBatched(Dense):
     def bytes_per_launch(self):  # algorithmic: every query against one read of the corpus
         return self.nQ * self.Nq * self.d * 2 + self.B * self.Nd * self.d * 2 + self.nQ * self.B * 4
 
+    launch_desc = "one flash_maxsim_batched_queries call (one kernel per 32 query blocks)"
+
     def extra_roofline(self, launch_ms):
-        """The practical fp16 MFMA ceiling on this part, measured in the same process: a
-        large square fp16 GEMM through torch (hipBLASLt), which runs at the same
-        power-limited clock as any MFMA-bound kernel."""
-        import torch
-        n = 8192
-        a = torch.randn(n, n, device=self.D.device).half()
-        b = torch.randn(n, n, device=self.D.device).half()
-        for _ in range(3):
-            torch.mm(a, b)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(20):
-            torch.mm(a, b)
-        e1.record()
-        torch.cuda.synchronize()
-        gemm_tf = 2 * n ** 3 / (e0.elapsed_time(e1) / 20 * 1e-3) / 1e12
-        ours = self.flops_per_launch() / (launch_ms * 1e-3) / 1e12
-        return {"gemm_fp16_8192_tflops": round(gemm_tf, 1), "frac_of_gemm": round(ours / gemm_tf, 4)}
+        return gemm_ceiling(self.torch, self.flops_per_launch() / (launch_ms * 1e-3) / 1e12)
 
     def config(self):
         c = super().config()
@@ -238,6 +243,7 @@ class Residual(Varlen):
     Each query is scored by the fused decode + MaxSim kernel (flashmaxsim_score_residual,
     plain MaxSim semantics): the decompressed tokens never exist in memory."""
     kernel = "residual_maxsim_kernel"
+    unfused_key = "unfused_decompress_then_score_ms"
 
     def __init__(self, torch, n_queries, B, lo, hi, d=128, nbits=2, ncent=1 << 18, Nq=32, topk=100):
         self.torch, self.nQ, self.B, self.d, self.Nq, self.k = torch, n_queries, B, d, Nq, topk
@@ -312,6 +318,56 @@ class Residual(Varlen):
         return _time_cpu(lambda: ro.maxsim_residual_f32(Q, codes, res, C, w, self.nbits, offs), n, seconds, threads,
                          f"first {n} docs x query 0, numpy decompress (restated codec) then fp32 varlen MaxSim, "
                          "repeated")
+
+
+class ResidualBatched(Residual):
+    """c6's index and queries, all queries scored by one batched call
+    (flashmaxsim_score_residual_batched): each 16-token tile is decoded once per pass and
+    shared through LDS by 32 query blocks, which moves the path to the MFMA roof."""
+    kernel = "residual_batched_kernel"
+    MFMA_PEAK_TFLOPS = 2500.0
+    launch_desc = "one flashmaxsim_score_residual_batched call (one kernel per 32 query blocks)"
+    unfused_key = "per_query_fused_all_queries_ms"
+
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        self.name = "c6b"
+
+    def step(self, timer):
+        from tilemaxsim_amd import flashmaxsim_score_residual_batched
+        s = timer(lambda: flashmaxsim_score_residual_batched(self.Q, self.codes, self.res, self.centroids,
+                                                             self.weights, self.nbits, self.offsets, padding="mask",
+                                                             validate=False))
+        self.scores.copy_(s)
+        return topk_rows(self.scores, self.k)
+
+    def flops_per_launch(self):
+        return 2 * self.nQ * self.Nq * self.T * self.d
+
+    def bytes_per_launch(self):  # the compressed index and the centroid table once for all queries
+        return (self.nQ * self.Nq * self.d * 2 + self.T * (4 + self.rb) + (self.B + 1) * 8
+                + self.nQ * self.B * 4 + self.ncent * self.d * 2)
+
+    def extra_roofline(self, launch_ms):
+        return gemm_ceiling(self.torch, self.flops_per_launch() / (launch_ms * 1e-3) / 1e12)
+
+    def unfused_ms(self):
+        """The per-query fused kernel over the same index, for comparison (outside the
+        timed steps): one flashmaxsim_score_residual call per query, all queries."""
+        torch = self.torch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(self.nQ):
+            self._score(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
+
+    def config(self):
+        c = super().config()
+        c["workload"] = c["workload"].replace("c6:", "c6b:", 1) + " (batched-query kernel)"
+        c["kernel"] = "flashmaxsim_score_residual_batched (tile decoded once into LDS, shared by 32 query blocks)"
+        return c
 
 
 class PQ:
@@ -452,6 +508,8 @@ def main():
         wl = PQ(torch, 32, 5_000_000, 128)
     elif args.config == "c6":
         wl = Residual(torch, 32, 2_000_000, 32, 300)
+    elif args.config == "c6b":
+        wl = ResidualBatched(torch, 32, 2_000_000, 32, 300)
     else:
         wl = Copy(torch)
     torch.cuda.synchronize()
@@ -485,7 +543,7 @@ def main():
         tf = wl.flops_per_launch() / (k_mean * 1e-3) / 1e12
         roofline.update({"bound": "mfma", "achieved": round(tf, 1), "peak": wl.MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / wl.MFMA_PEAK_TFLOPS, 4), "flops_per_launch": wl.flops_per_launch(),
-                         "launch": "one flash_maxsim_batched_queries call (one kernel per 32 query blocks)"})
+                         "launch": wl.launch_desc})
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -494,8 +552,8 @@ def main():
         cpu = wl.cpu_baseline(args.cpu_seconds, threads)
     if hasattr(wl, "extra_roofline"):
         roofline.update(wl.extra_roofline(k_mean))
-    if hasattr(wl, "unfused_ms"):  # after the timed steps: needs a decompressed copy of the corpus
-        roofline["unfused_decompress_then_score_ms"] = round(wl.unfused_ms(), 3)
+    if hasattr(wl, "unfused_ms"):  # after the timed steps (c6: needs a decompressed copy of the corpus)
+        roofline[wl.unfused_key] = round(wl.unfused_ms(), 3)
 
     pairs = wl.pairs_per_step()
     out = {

@@ -163,6 +163,21 @@ int tms_maxsim_residual(const void* Q, int64_t nq, int64_t d, const void* centro
                         int64_t total_tokens, const int64_t* offsets, int64_t ndocs, const int64_t* pids, int64_t B,
                         int64_t pad_len, float* out, void* stream);
 
+/*
+ * Batched-query MaxSim over residual-compressed documents: nQ fp16 queries of nq tokens
+ * (Qs is (nQ, nq, d)) against the same documents, with the arguments and semantics of
+ * tms_maxsim_residual; out is (nQ, B), row-major. Each 16-token tile is decoded once
+ * per pass and shared by up to 32 query blocks of 32 tokens, and the decoded tokens are
+ * rounded to fp16 as the codec rounds them (x = fp16(v * (1 / fp16(|v|)))).
+ * Replaces nQ rounds of ColBERT's decompression followed by flashmaxsim_score_packed
+ * (src/plaid_integration_benchmark.py:154-183) when the queries share their candidates,
+ * as in exhaustive scoring of a compressed collection.
+ */
+int tms_maxsim_residual_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d, const void* centroids,
+                                int64_t ncent, const void* bucket_weights, int nbits, const int32_t* codes,
+                                const uint8_t* residuals, int64_t total_tokens, const int64_t* offsets, int64_t ndocs,
+                                const int64_t* pids, int64_t B, int64_t pad_len, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -176,3 +176,101 @@ def test_edge_sizes(cuda):
     with pytest.raises(NotImplementedError):  # d not in {32, 64, 96, 128}
         Cw = torch.zeros(3, 256, dtype=torch.float16, device="cuda")
         decompress_residual(_gpu(codes), torch.zeros(40, 64, dtype=torch.uint8, device="cuda"), Cw, _gpu(w), nbits)
+
+
+def _queries(rng, nQ, nq, d):
+    Q = rng.standard_normal((nQ, nq, d)).astype(np.float32)
+    Q /= np.linalg.norm(Q, axis=2, keepdims=True)
+    return Q.astype(np.float16)
+
+
+# (nQ, Nq): 1 block per wave with idle waves; 2 per wave; two queries of 2 blocks per
+# wave over two launches; 4 per wave over two launches, the second partial; queries of
+# 4 blocks (Nq not a multiple of 32); Nq = 130 (5 blocks: one query at a time); a single
+# block (the one-query kernel)
+@pytest.mark.parametrize("nQ,nq", [(2, 32), (5, 20), (12, 32), (9, 64), (37, 32), (3, 100), (2, 130), (1, 32)])
+def test_batched_maxsim_matches_oracle(cuda, nQ, nq):
+    from tilemaxsim_amd import flashmaxsim_score_residual, flashmaxsim_score_residual_batched
+    rng = np.random.default_rng(nQ * 100 + nq)
+    d, nbits, ndocs = 128, 2, 700
+    lens = rng.integers(0, 200, ndocs)
+    lens[::29] = 0
+    lens[3] = 1
+    lens[7] = 333
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    C, codes, res, w = _index(rng, int(offsets[-1]), d, nbits, 301)
+    Qs = _queries(rng, nQ, nq, d)
+    idx = (_gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(offsets))
+    for padding in ("zeros", "mask"):
+        got = flashmaxsim_score_residual_batched(_gpu(Qs), *idx, padding=padding).cpu().numpy()
+        assert got.shape == (nQ, ndocs)
+        pad_len = int(lens.max()) if padding == "zeros" else 0
+        for q in range(nQ):
+            ref = ro.maxsim_residual(Qs[q], codes, res, C, w, nbits, offsets, None, pad_len)
+            _assert_scores(got[q], ref, f"batched nQ={nQ} nq={nq} q={q} {padding}")
+        one = flashmaxsim_score_residual(_gpu(Qs[nQ - 1]), *idx, padding=padding).cpu().numpy()
+        _assert_scores(got[nQ - 1], one, "batched vs one query")
+
+
+@pytest.mark.parametrize("nbits", [1, 2, 4])
+@pytest.mark.parametrize("d", [32, 64, 96, 128])
+def test_batched_maxsim_formats(cuda, nbits, d):
+    """Every (d, nbits) instantiation; the decoded tiles are the codec's fp16 tokens, so
+    the scores also match dense MaxSim over tms_residual_decompress's output (to 1e-4: a
+    token whose fp16 norm rounds the other way in the other fp32 summation order moves
+    by one fp16 ulp)."""
+    import torch
+    from tilemaxsim_amd import decompress_residual, flash_maxsim_multi_doc, flashmaxsim_score_residual_batched
+    rng = np.random.default_rng(nbits * 10 + d)
+    ndocs = 500
+    lens = rng.integers(1, 120, ndocs)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    C, codes, res, w = _index(rng, int(offsets[-1]), d, nbits, 211)
+    Qs = _queries(rng, 6, 32, d)
+    got = flashmaxsim_score_residual_batched(_gpu(Qs), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits,
+                                             _gpu(offsets), padding="mask").cpu().numpy()
+    D = decompress_residual(_gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits)
+    for q in range(6):
+        ref = ro.maxsim_residual(Qs[q], codes, res, C, w, nbits, offsets)
+        _assert_scores(got[q], ref, f"nbits={nbits} d={d} q={q}")
+        dense = flash_maxsim_multi_doc(_gpu(Qs[q]), D, torch.from_numpy(offsets)).cpu().numpy()
+        np.testing.assert_allclose(got[q], dense, rtol=1e-4, atol=1e-4)
+
+
+def test_batched_candidates_invalid_and_edges(cuda):
+    from tilemaxsim_amd import flashmaxsim_score_residual_batched
+    rng = np.random.default_rng(12)
+    d, nbits, ndocs = 64, 4, 300
+    lens = rng.integers(0, 90, ndocs)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    C, codes, res, w = _index(rng, int(offsets[-1]), d, nbits, 50)
+    codes[5], codes[9] = 50, -3  # out-of-range centroid ids are clamped
+    clamped = np.clip(codes, 0, 49).astype(np.int32)
+    Qs = _queries(rng, 7, 32, d)
+    idx = (_gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(offsets))
+    pids = rng.integers(0, ndocs, 257).astype(np.int64)
+    pids[4] = pids[5]
+    got = flashmaxsim_score_residual_batched(_gpu(Qs), *idx, pids=_gpu(pids)).cpu().numpy()
+    pad_len = int(lens[pids].max())
+    for q in range(7):
+        _assert_scores(got[q], ro.maxsim_residual(Qs[q], clamped, res, C, w, nbits, offsets, pids, pad_len),
+                       f"candidates q={q}")
+    assert np.array_equal(got[:, 4], got[:, 5])
+    bad = pids.copy()
+    bad[[0, 100, 256]] = [-1, ndocs, 10 ** 9]
+    with pytest.raises(ValueError):
+        flashmaxsim_score_residual_batched(_gpu(Qs), *idx, pids=_gpu(bad))
+    got = flashmaxsim_score_residual_batched(_gpu(Qs), *idx, pids=_gpu(bad), padding="mask",
+                                             validate=False).cpu().numpy()
+    for q in range(7):
+        _assert_scores(got[q], ro.maxsim_residual(Qs[q], clamped, res, C, w, nbits, offsets, bad, 0), f"invalid q={q}")
+    assert np.isnan(got[:, [0, 100, 256]]).all()
+    # all documents empty; no query tokens; no queries; no documents
+    empty = _gpu(np.zeros(70, dtype=np.int64))
+    for padding in ("zeros", "mask"):
+        got = flashmaxsim_score_residual_batched(_gpu(Qs), *idx[:5], empty, padding=padding).cpu().numpy()
+        assert got.shape == (7, 69) and np.all(got == -np.inf)
+    got = flashmaxsim_score_residual_batched(_gpu(Qs[:, :0]), *idx).cpu().numpy()
+    assert got.shape == (7, ndocs) and np.all(got == 0.0)
+    assert flashmaxsim_score_residual_batched(_gpu(Qs[:0]), *idx).shape == (0, ndocs)
+    assert flashmaxsim_score_residual_batched(_gpu(Qs), *idx, pids=_gpu(np.zeros(0, np.int64))).shape == (7, 0)

@@ -11,12 +11,12 @@ from .flash_maxsim_kernel import flash_maxsim_batch, flash_maxsim_multi_doc, fla
 from .flash_maxsim_v2 import flash_maxsim_batched_queries, flash_maxsim_v2, flash_maxsim_v2_multiquery
 from .flash_pqsim_kernel import TileMaxSimPQ
 from .plaid import flashmaxsim_score_packed
-from .residual import decompress_residual, flashmaxsim_score_residual
+from .residual import decompress_residual, flashmaxsim_score_residual, flashmaxsim_score_residual_batched
 from .topk import maxsim_topk, topk
 
 __all__ = [
     "flash_maxsim_v2_multiquery", "flash_maxsim_v2", "flash_maxsim_batched_queries",
     "flash_maxsim_single", "flash_maxsim_batch", "flash_maxsim_multi_doc", "maxsim_score",
     "TileMaxSimPQ", "flashmaxsim_score_packed", "topk", "maxsim_topk",
-    "decompress_residual", "flashmaxsim_score_residual",
+    "decompress_residual", "flashmaxsim_score_residual", "flashmaxsim_score_residual_batched",
 ]

@@ -24,6 +24,34 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
   }
 }
 
+// Cross-lane reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
+// with gfx950's row swaps, and over the 16 lanes of a row with DPP; every lane taking
+// part receives the result.
+__device__ __forceinline__ float cross_row_max(float m) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, m), __builtin_bit_cast(unsigned, m), false, false);
+  m = fmaxf(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
+  const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, m), __builtin_bit_cast(unsigned, m), false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)q[0]), __builtin_bit_cast(float, (unsigned)q[1]));
+}
+// Sum over the four rows, added as (row 0 + row 2) + (row 1 + row 3) in every lane.
+__device__ __forceinline__ float cross_row_sum(float m) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, m), __builtin_bit_cast(unsigned, m), false, false);
+  m = __builtin_bit_cast(float, (unsigned)p[0]) + __builtin_bit_cast(float, (unsigned)p[1]);
+  const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, m), __builtin_bit_cast(unsigned, m), false, false);
+  return __builtin_bit_cast(float, (unsigned)q[0]) + __builtin_bit_cast(float, (unsigned)q[1]);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float row_sum16(float s) {
+  s += dpp_f32<0xB1>(s);   // quad_perm [1,0,3,2]
+  s += dpp_f32<0x4E>(s);   // quad_perm [2,3,0,1]
+  s += dpp_f32<0x141>(s);  // row_half_mirror: the other quad of each half-row
+  s += dpp_f32<0x140>(s);  // row_mirror: the other half of the row
+  return s;
+}
+
 // Per-thread last-error text behind tms_last_error().
 void set_error(const char* fmt, ...);
 int fail(int code, const char* fmt, ...);

@@ -31,7 +31,7 @@ namespace tms {
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;  // every kernel here is launched with 256 threads
+constexpr int kThreads = 256;  // the single-query and decompression kernels' workgroup; the byte table's entries
 
 // Reinterpret a dword as two halves and back. The argument is taken by value: with the
 // ROCm 7.2 clang, __builtin_bit_cast applied directly to a subscripted ext-vector element
@@ -59,6 +59,7 @@ struct ResArgs {
   float* out;                // (B) scores, or (T, d) fp16 for the decompression kernel
   int64_t B, ndocs, T, ncent, pad_len;
   int32_t nq, nbq, blk0, d, rb, docs_per_wave;
+  int32_t nblk, blk_end;  // batched kernel: blocks per wave, one past the launch's last block
 };
 
 // Byte -> fp16 weights of its 8 / NBITS dimensions, in dimension order. The table is
@@ -364,6 +365,299 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
+// Batched queries over residual-compressed documents. One workgroup of eight waves per
+// CU walks a run of documents in 16-token tiles, every wave the same tiles. A tile is
+// decoded once: wave w < KS decodes k-step w (lane (r, g): chunk 4 w + g of token r, the
+// MFMA A-operand layout), the KS partial |v|^2 of each token meet in LDS, and the
+// normalised x = fp16(v * (1 / fp16(|v|))) goes to an LDS ring from which all eight
+// waves score the tile against the query blocks they hold, as the dense batched kernel
+// does. Step i scores tile i behind one LDS-only barrier:
+//   issue the ids of tile i+6 and the centroid chunks / residual bytes of tile i+4 (from
+//   ids issued two steps earlier); normalise tile i+1 (decoded a step earlier, partial
+//   norms visible since the last barrier) into the ring; decode tile i+2 and write its
+//   partial norms; barrier; read tile i+1's fragments; score tile i from the fragments
+//   read a step earlier.
+constexpr int kResBatchedWaves = 8;
+
+template <int KS, int NBITS, int NB>
+__global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_kernel(ResArgs a) {
+  constexpr int NS = 3;  // ring slots: x tiles, partial norms, centroid bodies, ids
+  __shared__ __attribute__((aligned(16))) uint8_t lut[4096];
+  __shared__ u32x4 ring[NS][4][64];
+  __shared__ f32x4 nrm[NS][16];  // partial |v|^2 of token r from decoding wave w, at [slot][r][w]
+  build_lut<NBITS>(lut, a.weights);
+
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar: `decoder` branches stay uniform
+  const bool decoder = wid < KS;
+  const float NEG_INF = -__builtin_inff();
+
+  const int64_t b_begin = wave_uniform((int64_t)blockIdx.x * a.docs_per_wave);
+  const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
+  const int64_t ndocs = b_end - b_begin;  // >= 1: the host launches no empty workgroup
+
+  // Query blocks: wave w holds blocks blk0 + w * nblk + j (whole queries).
+  const int my_blk0 = a.blk0 + wid * a.nblk;
+  int my_nblk = a.blk_end - my_blk0;  // <= 0 for a wave with no query
+  if (my_nblk > a.nblk) my_nblk = a.nblk;
+  u32x4 qf[NB][KS][2];
+  bool qv[NB][2];
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int jb = my_blk0 + j;
+      const int qi = jb / a.nbq;
+      const int tok = (jb - qi * a.nbq) * 32 + 16 * h + r;
+      qv[j][h] = j < my_nblk && tok < a.nq;
+      const int64_t row = qv[j][h] ? (int64_t)qi * a.nq + tok : 0;
+#pragma unroll
+      for (int s = 0; s < KS; s++) {
+        const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2);
+        qf[j][s][h] = qv[j][h] ? v : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+
+  // The workgroup's documents (at most 64): lane j holds document b_begin + j's first
+  // index row and length (-1 for an invalid pid or offsets).
+  int64_t dbase = 0;
+  int32_t dlen = -1;
+  if (lane < ndocs) {
+    const int64_t p = a.pids ? a.pids[b_begin + lane] : b_begin + lane;
+    if (p >= 0 && p < a.ndocs) {
+      const int64_t s0 = a.offsets[p], e0 = a.offsets[p + 1];
+      if (s0 >= 0 && e0 >= s0 && e0 <= a.T && e0 - s0 <= 0x7fffffff) {
+        dbase = s0;
+        dlen = (int32_t)(e0 - s0);
+      }
+    }
+  }
+  // Per-document scores of the wave's blocks: lane j holds document b_begin + j.
+  float pend[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) pend[j] = NEG_INF;
+
+  struct Cur {
+    int64_t b, base;
+    int32_t len, t0;
+  };
+  auto bounds = [&](int64_t b, int64_t& base) -> int32_t {
+    const int j = (int)(b - b_begin);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)dbase, j);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)dbase >> 32), j);
+    base = (int64_t)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_readlane(dlen, j);
+  };
+  // Move to the first document at or after b with a token. With `record`, the empty or
+  // invalid documents passed on the way get their scores. Past the last document the
+  // cursor keeps its last tile's rows, so loads through it stay in bounds.
+  auto seek = [&](Cur& c, int64_t b, bool record) {
+    for (; b < b_end; b++) {
+      int64_t base = 0;
+      const int32_t len = bounds(b, base);
+      if (len > 0) {
+        c.b = b;
+        c.base = base;
+        c.len = len;
+        c.t0 = 0;
+        return;
+      }
+      if (record) {
+        const float v = len < 0 ? __builtin_bit_cast(float, 0x7fc00000u) : (a.pad_len > 0 ? 0.f : NEG_INF);
+#pragma unroll
+        for (int j = 0; j < NB; j++) pend[j] = lane == (int)(b - b_begin) ? v : pend[j];
+      }
+    }
+    c.b = b_end;
+  };
+  auto advance = [&](Cur& c, bool record) {
+    if (c.b >= b_end) return;
+    c.t0 += 16;
+    if (c.t0 >= c.len) seek(c, c.b + 1, record);
+  };
+  auto row_of = [&](const Cur& c) -> int64_t {
+    int32_t t = c.t0 + r;
+    if (t > c.len - 1) t = c.len - 1;
+    return c.base + t;
+  };
+
+  Cur wc, wb, wi;  // scoring (tile i), body loads (tile i+4), id loads (tile i+6)
+  wc.b = b_end;
+  wc.base = 0;
+  wc.len = 1;
+  wc.t0 = 0;
+  seek(wc, b_begin, true);
+
+  // The pipeline, instantiated twice: decoding waves (loads, decode, ring writes) and
+  // scoring-only waves, so each copy's loads are straight-line code whose outstanding
+  // count the compiler tracks exactly (a load under a branch would make it wait for all).
+  auto pipeline = [&](auto dec_tag) {
+    constexpr bool DEC = decltype(dec_tag)::value == 1;
+    wb = wc;
+    wi = wc;
+    __syncthreads();  // the byte table is built
+
+    struct Body {
+      u32x4 cen;
+      uint32_t res;
+    };
+    int32_t ids[NS];
+    Body bd[NS];
+    u32x4 vkeep = {0u, 0u, 0u, 0u};
+    const int chunk = 4 * (DEC ? wid : 0) + g;
+    auto load_ids = [&](int32_t& id) {
+      if constexpr (DEC) id = a.codes[row_of(wi)];
+      advance(wi, false);
+    };
+    auto load_body = [&](const int32_t id, Body& bo) {
+      if constexpr (DEC) {
+        int64_t code = id;
+        code = code < 0 ? 0 : (code >= a.ncent ? a.ncent - 1 : code);
+        bo.cen = *(const u32x4*)(a.centroids + code * a.d * 2 + 16 * chunk);
+        bo.res = load_res<NBITS>(a.residuals + row_of(wb) * a.rb, chunk);
+      }
+      advance(wb, false);
+    };
+    auto decode = [&](const Body& bo, int slot) {
+      if constexpr (DEC) {
+        float n2 = 0.f;
+        vkeep = add_chunk(bo.cen, chunk_weights<NBITS>(lut, bo.res), n2);
+        n2 = cross_row_sum(n2);  // over the wave's 32 dimensions of token r
+        if (g == 0) nrm[slot][r][wid] = n2;
+      }
+    };
+    auto normalise = [&](int slot) {
+      if constexpr (DEC) {
+        const f32x4 p = nrm[slot][r];
+        float n2 = p[0];
+#pragma unroll
+        for (int w = 1; w < KS; w++) n2 += p[w];
+        const float inv = inv_norm(n2);
+        u32x4 x;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const uint32_t vi = vkeep[i];
+          const f16x2 v2 = as_f16x2(vi);
+          f16x2 q;
+          q.x = (_Float16)((float)v2.x * inv);
+          q.y = (_Float16)((float)v2.y * inv);
+          x[i] = as_u32(q);
+        }
+        ring[slot][wid][lane] = x;
+      }
+    };
+    auto sync = [&]() {  // LDS-only fence: the loads in flight are not waited for
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+
+    // prologue: tiles 0 and 1 decoded, tile 0 in the ring, bodies of tiles 2 and 3 and
+    // ids of tiles 4 and 5 in flight
+    load_ids(ids[0]);
+    load_ids(ids[1]);
+    load_ids(ids[2]);
+    load_body(ids[0], bd[0]);
+    load_ids(ids[0]);  // tile 3
+    load_body(ids[1], bd[1]);
+    load_ids(ids[1]);  // tile 4
+    decode(bd[0], 0);
+    load_body(ids[2], bd[2]);
+    load_ids(ids[2]);  // tile 5
+    sync();
+    normalise(0);
+    decode(bd[1], 1);
+    load_body(ids[0], bd[0]);  // tile 3
+    sync();
+    u32x4 frag[2][KS];
+#pragma unroll
+    for (int s = 0; s < KS; s++) frag[0][s] = ring[0][s][lane];
+
+    float rmax[NB][2];
+#pragma unroll
+    for (int j = 0; j < NB; j++) rmax[j][0] = rmax[j][1] = NEG_INF;
+    auto finish = [&]() {  // the document of wc ends with this tile
+      const bool padded = wc.len < a.pad_len;
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        float s = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          float m = cross_row_max(rmax[j][h]);
+          if (padded) m = fmaxf(m, 0.f);
+          s += qv[j][h] ? m : 0.f;
+          rmax[j][h] = NEG_INF;
+        }
+        s = row_sum16(s);
+        pend[j] = lane == (int)(wc.b - b_begin) ? s : pend[j];
+      }
+    };
+    auto step = [&](auto slot) -> bool {
+      constexpr int i = decltype(slot)::value;  // step index mod 6
+      constexpr int s0 = i % NS, s1 = (i + 1) % NS, s2 = (i + 2) % NS;
+      constexpr int f = i & 1;
+      load_ids(ids[s0]);          // tile i+6
+      load_body(ids[s1], bd[s1]);  // tile i+4
+      normalise(s1);               // tile i+1
+      decode(bd[s2], s2);          // tile i+2
+      sync();
+#pragma unroll
+      for (int s = 0; s < KS; s++) frag[f ^ 1][s] = ring[s1][s][lane];  // tile i+1
+      const u32x4(&t)[KS] = frag[f];
+      f32x4 acc[NB][2];
+#pragma unroll
+      for (int j = 0; j < NB; j++) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+          for (int h = 0; h < 2; h++) acc[j][h] = mfma16x16x32<TMS_DTYPE_F16>(t[s], qf[j][s][h], acc[j][h]);
+      __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+          rmax[j][h] = fmaxf(fmaxf(fmaxf(fmaxf(rmax[j][h], acc[j][h][0]), acc[j][h][1]), acc[j][h][2]), acc[j][h][3]);
+      if (wc.t0 + 16 >= wc.len) finish();
+      advance(wc, true);
+      return wc.b >= b_end;
+    };
+    while (true) {
+      if (step(RingSlot<0>{})) break;
+      if (step(RingSlot<1>{})) break;
+      if (step(RingSlot<2>{})) break;
+      if (step(RingSlot<3>{})) break;
+      if (step(RingSlot<4>{})) break;
+      if (step(RingSlot<5>{})) break;
+    }
+  };
+  if (wc.b < b_end) {
+    if (decoder) pipeline(RingSlot<1>{});
+    else pipeline(RingSlot<0>{});
+  }
+
+  // coalesced store: lane i writes document b_begin + i for each of the wave's queries
+  if (my_nblk > 0 && lane < ndocs) {
+    const int64_t b = b_begin + lane;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      if (j >= my_nblk) break;
+      const int jb = my_blk0 + j;
+      const int qi = jb / a.nbq;
+      s += pend[j];
+      if (j == my_nblk - 1 || (jb + 1) / a.nbq != qi) {  // the query's last block
+        a.out[(int64_t)qi * a.B + b] = s;
+        s = 0.f;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
 // Decompression: 16 lanes per token (lane k owns dimensions 8k .. 8k+7), four tokens
 // per wave. Writes x = fp16(v / fp16(|v|)) with fp32 division, as the codec computes.
 template <int NBITS>
@@ -427,6 +721,9 @@ static int check_format(const char* fn, int64_t d, int nbits, int64_t ncent, con
 #ifndef TMS_RES_QLDS
 #define TMS_RES_QLDS 1  // query fragments in LDS
 #endif
+#ifndef TMS_RES_BATCHED_TOKENS
+#define TMS_RES_BATCHED_TOKENS 4096  // document tokens one batched workgroup walks (whole documents)
+#endif
 template <int KS>
 static int launch_fused_ks(const ResArgs& a, int nbits, int64_t grid, hipStream_t st) {
   constexpr int kNSub = 1;
@@ -435,6 +732,72 @@ static int launch_fused_ks(const ResArgs& a, int nbits, int64_t grid, hipStream_
   else if (nbits == 2) hipLaunchKernelGGL((residual_maxsim_kernel<KS, 2, kNSub, kQlds>), dim3((unsigned)grid), dim3(256), 0, st, a);
   else hipLaunchKernelGGL((residual_maxsim_kernel<KS, 4, kNSub, kQlds>), dim3((unsigned)grid), dim3(256), 0, st, a);
   return check_launch("residual_maxsim_kernel");
+}
+
+template <int KS, int NB>
+static int launch_batched_nb(const ResArgs& a, int nbits, int64_t grid, hipStream_t st) {
+  const dim3 blk(64 * kResBatchedWaves);
+  if (nbits == 1) hipLaunchKernelGGL((residual_batched_kernel<KS, 1, NB>), dim3((unsigned)grid), blk, 0, st, a);
+  else if (nbits == 2) hipLaunchKernelGGL((residual_batched_kernel<KS, 2, NB>), dim3((unsigned)grid), blk, 0, st, a);
+  else hipLaunchKernelGGL((residual_batched_kernel<KS, 4, NB>), dim3((unsigned)grid), blk, 0, st, a);
+  return check_launch("residual_batched_kernel");
+}
+constexpr int kResMaxBlocksPerWave = 4;
+template <int KS>
+static int launch_batched_ks(const ResArgs& a, int nbits, int nb, int64_t grid, hipStream_t st) {
+  switch (nb) {
+    case 1: return launch_batched_nb<KS, 1>(a, nbits, grid, st);
+    case 2: return launch_batched_nb<KS, 2>(a, nbits, grid, st);
+    default: return launch_batched_nb<KS, kResMaxBlocksPerWave>(a, nbits, grid, st);
+  }
+}
+
+// Arguments shared by the two MaxSim entry points; returns TMS_OK with `a` filled, or an
+// error (or a negative value: nothing to launch, scores already written or none asked).
+static int prep_maxsim(const char* fn, const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* centroids,
+                       int64_t ncent, const void* bucket_weights, int nbits, const int32_t* codes,
+                       const uint8_t* residuals, int64_t total_tokens, const int64_t* offsets, int64_t ndocs,
+                       const int64_t* pids, int64_t B, int64_t pad_len, float* out, hipStream_t st, ResArgs& a) {
+  if (nQ < 0 || nq < 0 || d < 0 || ncent < 0 || total_tokens < 0 || ndocs < 0 || B < 0 || pad_len < 0)
+    return fail(TMS_ERR_INVALID, "%s: negative size", fn);
+  int rc = check_format(fn, d, nbits, ncent, centroids, bucket_weights);
+  if (rc) return rc;
+  if (B == 0 || nQ == 0) return -1;
+  if (!out) return fail(TMS_ERR_INVALID, "%s: out is NULL", fn);
+  if (!pids && B > ndocs) return fail(TMS_ERR_INVALID, "%s: B=%lld > ndocs=%lld without pids", fn, (long long)B,
+                                      (long long)ndocs);
+  if (!offsets) return fail(TMS_ERR_INVALID, "%s: offsets is NULL", fn);
+  if (nq == 0) {
+    const int64_t n = nQ * B;
+    hipLaunchKernelGGL(residual_fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, n, 0.f);
+    rc = check_launch("residual_fill_kernel");
+    return rc ? rc : -1;
+  }
+  if (!Q) return fail(TMS_ERR_INVALID, "%s: Q is NULL", fn);
+  if (total_tokens > 0 && (!codes || !residuals)) return fail(TMS_ERR_INVALID, "%s: codes / residuals is NULL", fn);
+  if (((uintptr_t)Q & 15) != 0) return fail(TMS_ERR_INVALID, "%s: Q must be 16-byte aligned", fn);
+  if ((((uintptr_t)residuals) & (nbits - 1)) != 0)
+    return fail(TMS_ERR_INVALID, "%s: residuals must be %d-byte aligned", fn, nbits);
+  if (nq > ((int64_t)1 << 24)) return fail(TMS_ERR_UNSUPPORTED, "%s: too many query tokens", fn);
+  memset(&a, 0, sizeof(a));
+  a.Q = (const uint8_t*)Q;
+  a.centroids = (const uint8_t*)centroids;
+  a.codes = codes;
+  a.residuals = residuals;
+  a.offsets = offsets;
+  a.pids = pids;
+  a.weights = (const uint16_t*)bucket_weights;
+  a.out = out;
+  a.B = B;
+  a.ndocs = ndocs;
+  a.T = total_tokens;
+  a.ncent = ncent;
+  a.pad_len = pad_len;
+  a.nq = (int32_t)nq;
+  a.nbq = (int32_t)((nq + 31) / 32);
+  a.d = (int32_t)d;
+  a.rb = (int32_t)(d * nbits / 8);
+  return TMS_OK;
 }
 
 }  // namespace tms
@@ -477,46 +840,11 @@ int tms_maxsim_residual(const void* Q, int64_t nq, int64_t d, const void* centro
                         int64_t total_tokens, const int64_t* offsets, int64_t ndocs, const int64_t* pids, int64_t B,
                         int64_t pad_len, float* out, void* stream) {
   using namespace tms;
-  const char* fn = "tms_maxsim_residual";
-  if (nq < 0 || d < 0 || ncent < 0 || total_tokens < 0 || ndocs < 0 || B < 0 || pad_len < 0)
-    return fail(TMS_ERR_INVALID, "%s: negative size", fn);
-  int rc = check_format(fn, d, nbits, ncent, centroids, bucket_weights);
-  if (rc) return rc;
-  if (B == 0) return TMS_OK;
-  if (!out) return fail(TMS_ERR_INVALID, "%s: out is NULL", fn);
-  if (!pids && B > ndocs) return fail(TMS_ERR_INVALID, "%s: B=%lld > ndocs=%lld without pids", fn, (long long)B,
-                                      (long long)ndocs);
-  if (!offsets) return fail(TMS_ERR_INVALID, "%s: offsets is NULL", fn);
   hipStream_t st = (hipStream_t)stream;
-  if (nq == 0) {
-    hipLaunchKernelGGL(residual_fill_kernel, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, st, out, B, 0.f);
-    return check_launch("residual_fill_kernel");
-  }
-  if (!Q) return fail(TMS_ERR_INVALID, "%s: Q is NULL", fn);
-  if (total_tokens > 0 && (!codes || !residuals)) return fail(TMS_ERR_INVALID, "%s: codes / residuals is NULL", fn);
-  if (((uintptr_t)Q & 15) != 0) return fail(TMS_ERR_INVALID, "%s: Q must be 16-byte aligned", fn);
-  if ((((uintptr_t)residuals) & (nbits - 1)) != 0)
-    return fail(TMS_ERR_INVALID, "%s: residuals must be %d-byte aligned", fn, nbits);
-  if (nq > ((int64_t)1 << 24)) return fail(TMS_ERR_UNSUPPORTED, "%s: too many query tokens", fn);
   ResArgs a;
-  memset(&a, 0, sizeof(a));
-  a.Q = (const uint8_t*)Q;
-  a.centroids = (const uint8_t*)centroids;
-  a.codes = codes;
-  a.residuals = residuals;
-  a.offsets = offsets;
-  a.pids = pids;
-  a.weights = (const uint16_t*)bucket_weights;
-  a.out = out;
-  a.B = B;
-  a.ndocs = ndocs;
-  a.T = total_tokens;
-  a.ncent = ncent;
-  a.pad_len = pad_len;
-  a.nq = (int32_t)nq;
-  a.nbq = (int32_t)((nq + 31) / 32);
-  a.d = (int32_t)d;
-  a.rb = (int32_t)(d * nbits / 8);
+  int rc = prep_maxsim("tms_maxsim_residual", Q, 1, nq, d, centroids, ncent, bucket_weights, nbits, codes, residuals,
+                       total_tokens, offsets, ndocs, pids, B, pad_len, out, st, a);
+  if (rc) return rc < 0 ? TMS_OK : rc;
   // about TMS_RES_TOKENS_PER_WAVE tokens per wave (whole documents), at least two rounds
   // of the chip's resident waves
   const int64_t hint = ndocs > 0 ? total_tokens / ndocs : 1;
@@ -533,6 +861,61 @@ int tms_maxsim_residual(const void* Q, int64_t nq, int64_t d, const void* centro
       case 2: rc = launch_fused_ks<2>(a, nbits, grid, st); break;
       case 3: rc = launch_fused_ks<3>(a, nbits, grid, st); break;
       default: rc = launch_fused_ks<4>(a, nbits, grid, st); break;
+    }
+    if (rc) return rc;
+  }
+  return TMS_OK;
+}
+
+int tms_maxsim_residual_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d, const void* centroids,
+                                int64_t ncent, const void* bucket_weights, int nbits, const int32_t* codes,
+                                const uint8_t* residuals, int64_t total_tokens, const int64_t* offsets, int64_t ndocs,
+                                const int64_t* pids, int64_t B, int64_t pad_len, float* out, void* stream) {
+  using namespace tms;
+  const char* fn = "tms_maxsim_residual_batched";
+  hipStream_t st = (hipStream_t)stream;
+  ResArgs a;
+  int rc = prep_maxsim(fn, Qs, nQ, nq, d, centroids, ncent, bucket_weights, nbits, codes, residuals, total_tokens,
+                       offsets, ndocs, pids, B, pad_len, out, st, a);
+  if (rc) return rc < 0 ? TMS_OK : rc;
+  const int64_t nblocks = nQ * (int64_t)a.nbq;
+  if (a.nbq > kResMaxBlocksPerWave || nblocks < 2) {  // one query at a time
+    for (int64_t qi = 0; qi < nQ; qi++) {
+      rc = tms_maxsim_residual((const uint8_t*)Qs + qi * nq * d * 2, nq, d, centroids, ncent, bucket_weights, nbits,
+                               codes, residuals, total_tokens, offsets, ndocs, pids, B, pad_len, out + qi * B, stream);
+      if (rc) return rc;
+    }
+    return TMS_OK;
+  }
+  if (nblocks > ((int64_t)1 << 30)) return fail(TMS_ERR_UNSUPPORTED, "%s: too many queries", fn);
+  // Blocks per wave: the smallest of 1, 2, 4 whose launch covers every block in one pass
+  // (a wave computes all of its slots, used or not), else 4. A wave holds whole queries.
+  int nb = kResMaxBlocksPerWave;
+  for (int c = 1; c < kResMaxBlocksPerWave; c *= 2)
+    if (c >= a.nbq && nblocks <= (int64_t)kResBatchedWaves * ((c / a.nbq) * a.nbq)) {
+      nb = c;
+      break;
+    }
+  a.nblk = (nb / a.nbq) * a.nbq;
+  // about TMS_RES_BATCHED_TOKENS tokens per workgroup (whole documents, at most 64), at
+  // least four rounds of one workgroup per CU
+  const int64_t hint = ndocs > 0 ? total_tokens / ndocs : 1;
+  int64_t dpw = hint > 0 ? TMS_RES_BATCHED_TOKENS / hint : 1;
+  if (dpw > 1 && B / dpw < (int64_t)256 * 4) dpw = B / ((int64_t)256 * 4);
+  if (dpw < 1) dpw = 1;
+  if (dpw > 64) dpw = 64;
+  a.docs_per_wave = (int32_t)dpw;
+  const int64_t grid = (B + dpw - 1) / dpw;
+  if (grid > 0x7fffffff) return fail(TMS_ERR_UNSUPPORTED, "%s: too many documents", fn);
+  const int64_t per_launch = (int64_t)kResBatchedWaves * a.nblk;
+  for (int64_t b0 = 0; b0 < nblocks; b0 += per_launch) {
+    a.blk0 = (int32_t)b0;
+    a.blk_end = (int32_t)(nblocks - b0 < per_launch ? nblocks : b0 + per_launch);
+    switch (d / 32) {
+      case 1: rc = launch_batched_ks<1>(a, nbits, nb, grid, st); break;
+      case 2: rc = launch_batched_ks<2>(a, nbits, nb, grid, st); break;
+      case 3: rc = launch_batched_ks<3>(a, nbits, nb, grid, st); break;
+      default: rc = launch_batched_ks<4>(a, nbits, nb, grid, st); break;
     }
     if (rc) return rc;
   }

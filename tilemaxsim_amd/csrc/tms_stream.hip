@@ -20,26 +20,6 @@
 
 namespace tms {
 
-// Max over lanes l, l^16, l^32, l^48 (the four 16-lane rows) with gfx950's cross-row swaps.
-__device__ __forceinline__ float cross_row_max(float m) {
-  const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, m), __builtin_bit_cast(unsigned, m), false, false);
-  m = fmaxf(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
-  const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, m), __builtin_bit_cast(unsigned, m), false, false);
-  return fmaxf(__builtin_bit_cast(float, (unsigned)q[0]), __builtin_bit_cast(float, (unsigned)q[1]));
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
-}
-// Sum over the 16 lanes of a row; every lane of the row receives it.
-__device__ __forceinline__ float row_sum16(float s) {
-  s += dpp_f32<0xB1>(s);   // quad_perm [1,0,3,2]
-  s += dpp_f32<0x4E>(s);   // quad_perm [2,3,0,1]
-  s += dpp_f32<0x141>(s);  // row_half_mirror: the other quad of each half-row
-  s += dpp_f32<0x140>(s);  // row_mirror: the other half of the row
-  return s;
-}
-
 struct StreamArgs {
   const uint8_t* Q;  // (nQ * nq, d)
   const uint8_t* D;  // (B, nd, d)

@@ -17,7 +17,8 @@ bucket weights. This module takes the index arrays as ColBERT holds them:
 :func:`decompress_residual` is the drop-in for ``ResidualCodec.decompress``.
 :func:`flashmaxsim_score_residual` replaces "decompress the candidates, then
 ``flashmaxsim_score_packed``" with one kernel that decodes in registers and never
-writes the decompressed tokens.
+writes the decompressed tokens; :func:`flashmaxsim_score_residual_batched` does the same
+for many queries over the same documents, decoding each tile once for all of them.
 """
 from __future__ import annotations
 
@@ -75,6 +76,42 @@ def decompress_residual(codes: torch.Tensor, residuals: torch.Tensor, centroids:
     return out
 
 
+def _prep_docs(fn: str, doc_offsets, pids, dev, T: int, padding: str, validate: bool):
+    """Offsets, pids, B and pad_len for the MaxSim entry points (shared checks)."""
+    if padding not in ("zeros", "mask"):
+        raise ValueError(f"padding must be 'zeros' or 'mask', got {padding!r}")
+    _check.tensor("doc_offsets", doc_offsets)
+    if doc_offsets.dim() != 1 or doc_offsets.numel() < 1:
+        raise ValueError("doc_offsets must be (ndocs + 1,)")
+    if doc_offsets.dtype.is_floating_point or doc_offsets.dtype == torch.bool:
+        raise TypeError(f"doc_offsets must be integer, got {doc_offsets.dtype}")
+    offsets = doc_offsets.to(device=dev, dtype=torch.int64).contiguous()
+    ndocs = offsets.numel() - 1
+    if pids is not None:
+        _check.tensor("pids", pids)
+        if pids.dim() != 1 or pids.dtype.is_floating_point or pids.dtype == torch.bool:
+            raise ValueError("pids must be a 1-D integer tensor")
+        pids = pids.to(device=dev, dtype=torch.int64).contiguous()
+        B = pids.numel()
+    else:
+        B = ndocs
+    if B == 0:
+        return offsets, pids, ndocs, B, 0
+    if validate:
+        bad = bool((offsets[1:] < offsets[:-1]).any()) or int(offsets[0]) < 0 or int(offsets[-1]) > T
+        if pids is not None:
+            bad = bad or bool(((pids < 0) | (pids >= ndocs)).any())
+        if bad:
+            raise ValueError(f"{fn}: doc_offsets must be non-decreasing within [0, T] and pids within [0, ndocs)")
+    pad_len = 0
+    if padding == "zeros" and ndocs > 0:  # the longest scored document (one host sync)
+        lengths = offsets[1:] - offsets[:-1]
+        if pids is not None:
+            lengths = lengths[pids.clamp(0, ndocs - 1)]
+        pad_len = max(int(lengths.max()), 0)
+    return offsets, pids, ndocs, B, pad_len
+
+
 def flashmaxsim_score_residual(Q: torch.Tensor, codes: torch.Tensor, residuals: torch.Tensor,
                                centroids: torch.Tensor, bucket_weights: torch.Tensor, nbits: int,
                                doc_offsets: torch.Tensor, pids: torch.Tensor | None = None,
@@ -100,45 +137,19 @@ def flashmaxsim_score_residual(Q: torch.Tensor, codes: torch.Tensor, residuals: 
     if padding not in ("zeros", "mask"):
         raise ValueError(f"padding must be 'zeros' or 'mask', got {padding!r}")
     _check.tensor("Q", Q)
-    _check.tensor("doc_offsets", doc_offsets)
     codes, residuals, centroids, bucket_weights, d, dev = _prep_codec(codes, residuals, centroids, bucket_weights,
                                                                       nbits)
     Q2 = Q.squeeze(0) if Q.dim() == 3 else Q
     if Q2.dim() != 2:
         raise ValueError(f"Q must be (1, Nq, d) or (Nq, d), got {tuple(Q.shape)}")
     assert Q2.shape[1] == d, f"flashmaxsim_score_residual: Q width {Q2.shape[1]} != centroid width {d}"
-    if doc_offsets.dim() != 1 or doc_offsets.numel() < 1:
-        raise ValueError("doc_offsets must be (ndocs + 1,)")
-    if doc_offsets.dtype.is_floating_point or doc_offsets.dtype == torch.bool:
-        raise TypeError(f"doc_offsets must be integer, got {doc_offsets.dtype}")
-    offsets = doc_offsets.to(device=dev, dtype=torch.int64).contiguous()
-    ndocs = offsets.numel() - 1
-    if pids is not None:
-        _check.tensor("pids", pids)
-        if pids.dim() != 1 or pids.dtype.is_floating_point or pids.dtype == torch.bool:
-            raise ValueError("pids must be a 1-D integer tensor")
-        pids = pids.to(device=dev, dtype=torch.int64).contiguous()
-        B = pids.numel()
-    else:
-        B = ndocs
-    Q2 = _check.query_like(Q2.to(dev), torch.float16)
     T = codes.shape[0]
+    offsets, pids, ndocs, B, pad_len = _prep_docs("flashmaxsim_score_residual", doc_offsets, pids, dev, T, padding,
+                                                  validate)
+    Q2 = _check.query_like(Q2.to(dev), torch.float16)
     scores = torch.empty(B, dtype=torch.float32, device=dev)
     if B == 0:
         return scores
-    if validate:
-        bad = bool((offsets[1:] < offsets[:-1]).any()) or int(offsets[0]) < 0 or int(offsets[-1]) > T
-        if pids is not None and B > 0:
-            bad = bad or bool(((pids < 0) | (pids >= ndocs)).any())
-        if bad:
-            raise ValueError("flashmaxsim_score_residual: doc_offsets must be non-decreasing within [0, T] and "
-                             "pids within [0, ndocs)")
-    pad_len = 0
-    if padding == "zeros" and ndocs > 0:  # the longest scored document (one host sync)
-        lengths = offsets[1:] - offsets[:-1]
-        if pids is not None:
-            lengths = lengths[pids.clamp(0, ndocs - 1)]
-        pad_len = max(int(lengths.max()), 0)
     lib = _lib.load()
     with torch.cuda.device(dev):
         _lib.check(lib.tms_maxsim_residual(Q2.data_ptr(), Q2.shape[0], d, centroids.data_ptr(), centroids.shape[0],
@@ -146,4 +157,44 @@ def flashmaxsim_score_residual(Q: torch.Tensor, codes: torch.Tensor, residuals: 
                                            T, offsets.data_ptr(), ndocs,
                                            pids.data_ptr() if pids is not None else None, B, pad_len,
                                            scores.data_ptr(), _lib.stream_of(Q2)))
+    return scores
+
+
+def flashmaxsim_score_residual_batched(Qs: torch.Tensor, codes: torch.Tensor, residuals: torch.Tensor,
+                                       centroids: torch.Tensor, bucket_weights: torch.Tensor, nbits: int,
+                                       doc_offsets: torch.Tensor, pids: torch.Tensor | None = None,
+                                       padding: str = "zeros", validate: bool = True) -> torch.Tensor:
+    """Score ``nQ`` queries against the same residual-compressed documents:
+    ``Qs`` (nQ, Nq, d) -> (nQ, B) float32.
+
+    Arguments and semantics are those of :func:`flashmaxsim_score_residual`, query by
+    query. Each tile of documents is decoded once per pass and shared by up to 32 query
+    blocks of 32 tokens, so the decode cost is paid once for all the queries (exhaustive
+    scoring of a compressed collection, or queries that share PLAID candidates). The
+    decoded tokens are rounded to fp16 as the codec rounds them, so the scores equal
+    MaxSim over :func:`decompress_residual`'s output up to the summation order.
+    """
+    if padding not in ("zeros", "mask"):
+        raise ValueError(f"padding must be 'zeros' or 'mask', got {padding!r}")
+    _check.tensor("Qs", Qs)
+    codes, residuals, centroids, bucket_weights, d, dev = _prep_codec(codes, residuals, centroids, bucket_weights,
+                                                                      nbits)
+    if Qs.dim() != 3:
+        raise ValueError(f"Qs must be (nQ, Nq, d), got {tuple(Qs.shape)}")
+    assert Qs.shape[2] == d, f"flashmaxsim_score_residual_batched: Q width {Qs.shape[2]} != centroid width {d}"
+    T = codes.shape[0]
+    offsets, pids, ndocs, B, pad_len = _prep_docs("flashmaxsim_score_residual_batched", doc_offsets, pids, dev, T,
+                                                  padding, validate)
+    Qs = _check.query_like(Qs.to(dev), torch.float16)
+    nQ, Nq = Qs.shape[0], Qs.shape[1]
+    scores = torch.empty(nQ, B, dtype=torch.float32, device=dev)
+    if B == 0 or nQ == 0:
+        return scores
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        _lib.check(lib.tms_maxsim_residual_batched(Qs.data_ptr(), nQ, Nq, d, centroids.data_ptr(), centroids.shape[0],
+                                                   bucket_weights.data_ptr(), nbits, codes.data_ptr(),
+                                                   residuals.data_ptr(), T, offsets.data_ptr(), ndocs,
+                                                   pids.data_ptr() if pids is not None else None, B, pad_len,
+                                                   scores.data_ptr(), _lib.stream_of(Qs)))
     return scores
