@@ -1,4 +1,4 @@
-"""Parity at BASELINE's full sizes (C2-C5, c6, top-k over C2's score matrix).
+"""Parity at BASELINE's full sizes (C2-C5, c6/c6b, top-k over C2's score matrix).
 
 Each test builds one configuration at its benchmark size on the GPU, scores it through
 the public entry points, and checks a seeded sample of documents, always including the
@@ -112,9 +112,10 @@ def test_c5_pq_fullsize(cuda):
 
 
 def test_c6_residual_fullsize(cuda):
-    """c6: C3's corpus as a ColBERTv2 index (nbits=2, 262,144 centroids, 12 GB)."""
+    """c6: C3's corpus as a ColBERTv2 index (nbits=2, 262,144 centroids, 12 GB), one query
+    through the fused kernel; c6b: 32 queries through the batched kernel."""
     import torch
-    from tilemaxsim_amd import flashmaxsim_score_residual
+    from tilemaxsim_amd import flashmaxsim_score_residual, flashmaxsim_score_residual_batched
     rng = np.random.default_rng(77)
     lens = rng.integers(32, 301, size=2_000_000)
     offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
@@ -133,6 +134,14 @@ def test_c6_residual_fullsize(cuda):
     ref = ro.maxsim_residual(Q.cpu().numpy(), codes[rows].cpu().numpy(), res[rows].cpu().numpy(), cent.cpu().numpy(),
                              w.cpu().numpy(), 2, sub_offs)
     np.testing.assert_allclose(got[idx], ref, rtol=RTOL, atol=ATOL)
+    # c6b: all 32 queries through the batched kernel, checked on the same sample
+    Qs = _normal_fp16(torch, (32, 32, 128), 54)
+    gotb = flashmaxsim_score_residual_batched(Qs, codes, res, cent, w, 2, torch.from_numpy(offs).cuda(),
+                                              padding="mask", validate=False).cpu().numpy()
+    sub = (codes[rows].cpu().numpy(), res[rows].cpu().numpy(), cent.cpu().numpy(), w.cpu().numpy())
+    for q in (0, 17, 31):
+        refq = ro.maxsim_residual(Qs[q].cpu().numpy(), *sub, 2, sub_offs)
+        np.testing.assert_allclose(gotb[q][idx], refq, rtol=RTOL, atol=ATOL)
     del codes, res
     _release(torch)
 

@@ -113,6 +113,26 @@ def test_residual_c_abi_rejects_bad_arguments():
     assert rc == 1 and "negative" in msg
     rc, _ = _c_call("tms_maxsim_residual", 16, 32, 128, 16, 4, 16, 2, 16, 16, 10, 16, 3, None, 0, 0, None, None)
     assert rc == 0  # no documents to score
+    # tms_maxsim_residual_batched(Qs, nQ, nq, d, centroids, ncent, weights, nbits, codes, residuals, T,
+    #                             offsets, ndocs, pids, B, pad_len, out, stream)
+    rc, msg = _c_call("tms_maxsim_residual_batched", 16, -1, 32, 128, 16, 4, 16, 2, 16, 16, 10, 16, 3, None, 3, 0, 16,
+                      None)
+    assert rc == 1 and "negative" in msg and "batched" in msg
+    rc, msg = _c_call("tms_maxsim_residual_batched", 16, 4, 32, 128, 16, 4, 16, 3, 16, 16, 10, 16, 3, None, 3, 0, 16,
+                      None)
+    assert rc == 2 and "nbits" in msg
+    rc, msg = _c_call("tms_maxsim_residual_batched", 16, 4, 32, 128, 16, 4, 16, 2, 16, 16, 10, 16, 3, None, 5, 0, 16,
+                      None)
+    assert rc == 1 and "ndocs" in msg
+    rc, msg = _c_call("tms_maxsim_residual_batched", 16, 4, 32, 128, 16, 4, 16, 2, 16, 16, 10, None, 3, None, 3, 0,
+                      16, None)
+    assert rc == 1 and "offsets" in msg
+    rc, msg = _c_call("tms_maxsim_residual_batched", 24, 4, 32, 128, 16, 4, 16, 2, 16, 16, 10, 16, 3, None, 3, 0, 16,
+                      None)
+    assert rc == 1 and "aligned" in msg
+    rc, _ = _c_call("tms_maxsim_residual_batched", 16, 0, 32, 128, 16, 4, 16, 2, 16, 16, 10, 16, 3, None, 3, 0, None,
+                    None)
+    assert rc == 0  # no queries: nothing to do, no HIP call
 
 
 def test_python_errors_before_device_checks():
@@ -173,6 +193,13 @@ def test_residual_python_errors_before_device_checks():
         flashmaxsim_score_residual(torch.zeros(32, 128), codes, res, cent, w, 2, offs, padding="none")
     with pytest.raises(ValueError, match="GPU"):
         flashmaxsim_score_residual(torch.zeros(32, 128), codes, res, cent, w, 2, offs)
+    from tilemaxsim_amd import flashmaxsim_score_residual_batched
+    with pytest.raises(ValueError, match="padding"):
+        flashmaxsim_score_residual_batched(torch.zeros(2, 32, 128), codes, res, cent, w, 2, offs, padding="pad")
+    with pytest.raises(NotImplementedError, match="nbits"):
+        flashmaxsim_score_residual_batched(torch.zeros(2, 32, 128), codes, res, cent, w, 3, offs)
+    with pytest.raises(ValueError, match="GPU"):
+        flashmaxsim_score_residual_batched(torch.zeros(2, 32, 128), codes, res, cent, w, 2, offs)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

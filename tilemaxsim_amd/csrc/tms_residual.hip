@@ -371,17 +371,22 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
 // MFMA A-operand layout), the KS partial |v|^2 of each token meet in LDS, and the
 // normalised x = fp16(v * (1 / fp16(|v|))) goes to an LDS ring from which all eight
 // waves score the tile against the query blocks they hold, as the dense batched kernel
-// does. Step i scores tile i behind one LDS-only barrier:
-//   issue the ids of tile i+6 and the centroid chunks / residual bytes of tile i+4 (from
-//   ids issued two steps earlier); normalise tile i+1 (decoded a step earlier, partial
-//   norms visible since the last barrier) into the ring; decode tile i+2 and write its
-//   partial norms; barrier; read tile i+1's fragments; score tile i from the fragments
-//   read a step earlier.
+// does. With NS ring slots, step i scores tile i behind one LDS-only barrier:
+//   issue the ids of tile i + 2 NS and the centroid chunks / residual bytes of tile
+//   i + 1 + NS (from ids issued NS - 1 steps earlier); normalise tile i+1 (decoded a step
+//   earlier, partial norms visible since the last barrier) into the ring; decode tile
+//   i+2 (its body issued NS - 1 steps earlier) and write its partial norms; barrier; read
+//   tile i+1's fragments; score tile i from the fragments read a step earlier.
 constexpr int kResBatchedWaves = 8;
+#ifndef TMS_RES_RING
+#define TMS_RES_RING 3  // ring slots; loads run NS - 1 steps ahead of their use
+#endif
 
 template <int KS, int NBITS, int NB>
 __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_kernel(ResArgs a) {
-  constexpr int NS = 3;  // ring slots: x tiles, partial norms, centroid bodies, ids
+  constexpr int NS = TMS_RES_RING;  // ring slots: x tiles, partial norms, centroid bodies, ids
+  static_assert(NS >= 3 && NS <= 6 && NS != 5, "the step loop is unrolled lcm(NS, 2) <= 6 times");
+  constexpr int U = NS % 2 == 0 ? NS : 2 * NS;  // steps per loop iteration (slot indices are constants)
   __shared__ __attribute__((aligned(16))) uint8_t lut[4096];
   __shared__ u32x4 ring[NS][4][64];
   __shared__ f32x4 nrm[NS][16];  // partial |v|^2 of token r from decoding wave w, at [slot][r][w]
@@ -553,22 +558,23 @@ __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_ker
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
 
-    // prologue: tiles 0 and 1 decoded, tile 0 in the ring, bodies of tiles 2 and 3 and
-    // ids of tiles 4 and 5 in flight
-    load_ids(ids[0]);
-    load_ids(ids[1]);
-    load_ids(ids[2]);
+    // prologue: tiles 0 and 1 decoded, tile 0 in the ring, the bodies of tiles 2 .. NS and
+    // the ids of tiles NS+1 .. 2 NS - 1 in flight (tile t always sits in slot t % NS)
+#pragma unroll
+    for (int t = 0; t < NS; t++) load_ids(ids[t]);
     load_body(ids[0], bd[0]);
-    load_ids(ids[0]);  // tile 3
+    load_ids(ids[0]);  // tile NS
     load_body(ids[1], bd[1]);
-    load_ids(ids[1]);  // tile 4
+    load_ids(ids[1]);  // tile NS + 1
     decode(bd[0], 0);
-    load_body(ids[2], bd[2]);
-    load_ids(ids[2]);  // tile 5
+#pragma unroll
+    for (int t = 2; t <= NS; t++) {
+      load_body(ids[t % NS], bd[t % NS]);
+      if (t < NS) load_ids(ids[t]);  // tile t + NS
+    }
     sync();
     normalise(0);
     decode(bd[1], 1);
-    load_body(ids[0], bd[0]);  // tile 3
     sync();
     u32x4 frag[2][KS];
 #pragma unroll
@@ -594,11 +600,11 @@ __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_ker
       }
     };
     auto step = [&](auto slot) -> bool {
-      constexpr int i = decltype(slot)::value;  // step index mod 6
+      constexpr int i = decltype(slot)::value;  // step index mod U
       constexpr int s0 = i % NS, s1 = (i + 1) % NS, s2 = (i + 2) % NS;
       constexpr int f = i & 1;
-      load_ids(ids[s0]);          // tile i+6
-      load_body(ids[s1], bd[s1]);  // tile i+4
+      load_ids(ids[s0]);           // tile i + 2 NS
+      load_body(ids[s1], bd[s1]);  // tile i + 1 + NS
       normalise(s1);               // tile i+1
       decode(bd[s2], s2);          // tile i+2
       sync();
@@ -628,10 +634,12 @@ __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_ker
     while (true) {
       if (step(RingSlot<0>{})) break;
       if (step(RingSlot<1>{})) break;
-      if (step(RingSlot<2>{})) break;
-      if (step(RingSlot<3>{})) break;
-      if (step(RingSlot<4>{})) break;
-      if (step(RingSlot<5>{})) break;
+      if (step(RingSlot<2 % U>{})) break;
+      if (step(RingSlot<3 % U>{})) break;
+      if constexpr (U > 4) {
+        if (step(RingSlot<4>{})) break;
+        if (step(RingSlot<5>{})) break;
+      }
     }
   };
   if (wc.b < b_end) {
