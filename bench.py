@@ -7,7 +7,8 @@ every document with ``flash_maxsim_v2_multiquery`` (one HBM pass over the corpus
 query, as the reference's V2-MQ kernel) and takes the top-100 per query.
 
 Other workloads (``--config``): c1 (CPU-sized plumbing check), c2b (C2 with all 64
-queries through the batched-query kernel), c3 (2M variable-length documents), c4
+queries through the batched-query kernel), c3 (2M variable-length documents), c3b (c3
+through the batched-query kernel), c4
 (d-tiled, ``--d 256|512|768``), c5 (PQ/ADC, 5M documents of uint8 codes), c6 (C3's
 corpus as a ColBERTv2 residual-compressed index, fused decode + MaxSim per query), c6b
 (the same index, all queries through the batched residual kernel), copy (counter
@@ -45,7 +46,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c4", "c5", "c6", "c6b", "copy"])
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c6", "c6b", "copy"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -166,7 +167,7 @@ class DenseBatched(Dense):
 
     def __init__(self, *args, **kw):
         super().__init__(*args, **kw)
-        self.kernel = "batched_maxsim_kernel"
+        self.kernel = "varlen_batched_kernel"  # fixed-length documents at implicit offsets
 
     def step(self, timer):
         from tilemaxsim_amd import flash_maxsim_batched_queries
@@ -234,6 +235,40 @@ class Varlen(Dense):
         Dflat = self.D[: int(offs[-1])].cpu().numpy()
         return _time_cpu(lambda: orc.maxsim_varlen(Q, Dflat, offs), n, seconds, threads,
                          f"first {n} docs x query 0, numpy fp32 per-token sims + segmented max, repeated")
+
+
+class VarlenBatched(Varlen):
+    """C3's corpus and queries, all queries scored by one batched call
+    (flash_maxsim_multi_doc_batched): each tile is loaded once per workgroup and scored
+    from LDS by 32 query blocks, which moves the path to the MFMA roof."""
+    kernel = "varlen_batched_kernel"
+    MFMA_PEAK_TFLOPS = 2500.0
+    launch_desc = "one flash_maxsim_multi_doc_batched call (one kernel per 32 query blocks)"
+
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        self.name = "c3b"
+
+    def step(self, timer):
+        from tilemaxsim_amd import flash_maxsim_multi_doc_batched
+        s = timer(lambda: flash_maxsim_multi_doc_batched(self.Q, self.D, self.offsets, validate=False))
+        self.scores.copy_(s)
+        return topk_rows(self.scores, self.k)
+
+    def flops_per_launch(self):
+        return 2 * self.nQ * self.Nq * self.T * self.d
+
+    def bytes_per_launch(self):
+        return self.nQ * self.Nq * self.d * 2 + self.T * self.d * 2 + (self.B + 1) * 8 + self.nQ * self.B * 4
+
+    def extra_roofline(self, launch_ms):
+        return gemm_ceiling(self.torch, self.flops_per_launch() / (launch_ms * 1e-3) / 1e12)
+
+    def config(self):
+        c = super().config()
+        c["workload"] = c["workload"].replace("c3:", "c3b:", 1) + " (batched-query kernel)"
+        c["kernel"] = "flash_maxsim_multi_doc_batched (tiles shared through LDS by 32 query blocks)"
+        return c
 
 
 class Residual(Varlen):
@@ -396,16 +431,23 @@ class PQ:
 
     def extra_roofline(self, launch_ms):
         """Beside the code-bytes roofline: the reference's own PQ IO formula
-        (src/benchmark.py:226: table + codes + output) and the LDS roof of this kernel's
+        (src/benchmark.py:226: table + codes + output), the LDS roof of this kernel's
         codebook gather (16 B per code per token, against 128 B/clk/CU x 256 CUs at
-        2.4 GHz = 78.6 TB/s)."""
+        2.4 GHz = 78.6 TB/s), and the MFMA rate of scoring the decoded tokens beside an
+        fp16 GEMM measured in the same process."""
         ref_bytes = self.Nq * self.M * self.K * 4 + self.B * self.Nd * self.M + self.B * self.Nq * 4
         lds_bytes = self.B * self.Nd * self.M * 16
         lds_tbs = lds_bytes / (launch_ms * 1e-3) / 1e12
-        return {"bytes_reference_formula": ref_bytes,
-                "gbs_reference_formula": round(ref_bytes / (launch_ms * 1e-3) / 1e9, 1),
-                "lds_gather_bytes_per_launch": lds_bytes, "lds_gather_tbs": round(lds_tbs, 2),
-                "lds_peak_tbs": 78.6, "lds_frac": round(lds_tbs / 78.6, 4)}
+        # the decoded tokens are scored on MFMA: 2 Nq d flops per token, as dense MaxSim
+        flops = 2 * self.Nq * self.M * self.dsub * self.B * self.Nd
+        mfma_tf = flops / (launch_ms * 1e-3) / 1e12
+        out = {"bytes_reference_formula": ref_bytes,
+               "gbs_reference_formula": round(ref_bytes / (launch_ms * 1e-3) / 1e9, 1),
+               "lds_gather_bytes_per_launch": lds_bytes, "lds_gather_tbs": round(lds_tbs, 2),
+               "lds_peak_tbs": 78.6, "lds_frac": round(lds_tbs / 78.6, 4),
+               "mfma_flops_per_launch": flops, "mfma_tflops": round(mfma_tf, 1)}
+        out.update(gemm_ceiling(self.torch, mfma_tf))
+        return out
 
     def pairs_per_step(self):
         return self.nQ * self.B
@@ -502,6 +544,8 @@ def main():
         wl = DenseBatched(torch, 64, 1_000_000, 180, 128, name="c2b")
     elif args.config == "c3":
         wl = Varlen(torch, 32, 2_000_000, 32, 300, 128)
+    elif args.config == "c3b":
+        wl = VarlenBatched(torch, 32, 2_000_000, 32, 300, 128)
     elif args.config == "c4":
         wl = Dense(torch, 16, 200_000, 128, args.d, name=f"c4_d{args.d}")
     elif args.config == "c5":

@@ -86,6 +86,21 @@ int tms_maxsim_dense_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d, 
                              int64_t nd, int dtype, float* out, void* stream);
 
 /*
+ * Batched-query MaxSim over variable-length documents: nQ queries of nq tokens (Qs is
+ * (nQ, nq, d)) against the documents of tms_maxsim_varlen / tms_maxsim_varlen_padded
+ * (pad_len 0: empty documents score -inf; pad_len > 0: the zero-padding semantics);
+ * out is (nQ, B), row-major. With d in {32, 64, 96, 128}, 16-byte aligned Qs and
+ * D_flat and at most 128 tokens per query, up to 32 query blocks of 32 tokens share
+ * each pass over D_flat.
+ * Replaces nQ calls of flash_maxsim_multi_doc (src/flash_maxsim_kernel.py:248-273) or of
+ * flashmaxsim_score_packed (src/plaid_integration_benchmark.py:154-183) over the same
+ * documents.
+ */
+int tms_maxsim_varlen_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d, const void* D_flat,
+                              int64_t total_tokens, const int64_t* offsets, int64_t B, int64_t pad_len, int dtype,
+                              float* out, void* stream);
+
+/*
  * PQ distance table lut[q, m, k] = sum_j Q[q, m*dsub + j] * codebook[m, k, j] (fp32).
  * Replaces TileMaxSimPQ.build_distance_table (src/flash_pqsim_kernel.py:190-211) and
  * _build_distance_table_kernel (:31-67).

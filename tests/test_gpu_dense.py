@@ -230,6 +230,85 @@ def test_varlen_bad_offsets(cuda):
     assert np.isnan(got[1]) and got[0] == 4 * 64 and got[2] == 4 * 64
 
 
+# (nQ, Nq): 1 block per wave with idle waves; 2 per wave; 4 per wave over two launches;
+# queries of 3 blocks; queries of 4 blocks; 2 blocks in all (the per-pass kernel);
+# 5 blocks per query (the per-pass kernel)
+@pytest.mark.parametrize("nQ,nq", [(5, 32), (12, 32), (37, 32), (4, 70), (6, 128), (2, 32), (3, 150)])
+def test_varlen_batched(cuda, nQ, nq):
+    import torch
+    from tilemaxsim_amd import flash_maxsim_multi_doc, flash_maxsim_multi_doc_batched
+    rng = _rng(nQ * 1000 + nq)
+    B = 1500
+    lens = rng.integers(0, 260, size=B)
+    lens[rng.random(B) < 0.1] = 0
+    lens[:2] = 0
+    lens[5] = 1
+    lens[-1] = 0
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(offsets[-1])
+    Qs = _randn(rng, (nQ, nq, 128), normalize=True)
+    Dflat = _randn(rng, (T, 128), normalize=True)
+    got = flash_maxsim_multi_doc_batched(_to_gpu(Qs), _to_gpu(Dflat), torch.from_numpy(offsets)).cpu().numpy()
+    assert got.shape == (nQ, B)
+    for q in range(nQ):
+        _assert_scores(got[q], orc.maxsim_varlen(Qs[q], Dflat, offsets, f64=True), f"varlen batched q={q}")
+    one = flash_maxsim_multi_doc(_to_gpu(Qs[-1]), _to_gpu(Dflat), torch.from_numpy(offsets)).cpu().numpy()
+    _assert_scores(got[-1], one, "batched vs one query")
+
+
+@pytest.mark.parametrize("d", [32, 64, 96, 80, 256])
+def test_varlen_batched_widths_bf16_and_invalid(cuda, d):
+    """Every k-step count of the batched kernel (d = 32 .. 128), widths it does not take
+    (80, 256: the per-pass kernel), bf16 documents and invalid offsets (NaN)."""
+    import torch
+    from tilemaxsim_amd import flash_maxsim_multi_doc_batched
+    rng = _rng(d)
+    lens = rng.integers(0, 100, size=400)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(offsets[-1])
+    Qs = _randn(rng, (9, 32, d), normalize=True)
+    Dflat = _randn(rng, (T, d), normalize=True)
+    for dt in (torch.float16, torch.bfloat16):
+        D = _to_gpu(Dflat, dt)
+        got = flash_maxsim_multi_doc_batched(_to_gpu(Qs), D, torch.from_numpy(offsets)).cpu().numpy()
+        Dr = D.float().cpu().numpy()
+        Qr = _to_gpu(Qs, dt).float().cpu().numpy()
+        for q in range(9):
+            _assert_scores(got[q], orc.maxsim_varlen(Qr[q], Dr, offsets, f64=True), f"d={d} {dt} q={q}")
+    bad = offsets.copy()
+    bad[10] = bad[11] + 5  # document 9 ends after document 10 starts, document 10 is reversed
+    got = flash_maxsim_multi_doc_batched(_to_gpu(Qs), _to_gpu(Dflat), torch.from_numpy(bad),
+                                         validate=False).cpu().numpy()
+    assert np.isnan(got[:, 10]).all() and not np.isnan(np.delete(got, 10, axis=1)).any()
+    with pytest.raises(ValueError):
+        flash_maxsim_multi_doc_batched(_to_gpu(Qs), _to_gpu(Dflat), torch.from_numpy(bad))
+
+
+def test_packed_batched_both_paddings(cuda):
+    import torch
+    from tilemaxsim_amd import flashmaxsim_score_packed, flashmaxsim_score_packed_batched
+    rng = _rng(4242)
+    lens = rng.integers(0, 150, size=900)
+    lens[7] = 0
+    T = int(lens.sum())
+    Qs = _randn(rng, (20, 32, 128), normalize=True)
+    Dp = _randn(rng, (T, 128), normalize=True)
+    for padding in ("zeros", "mask"):
+        got = flashmaxsim_score_packed_batched(_to_gpu(Qs), _to_gpu(Dp), torch.from_numpy(lens),
+                                               padding=padding).cpu().numpy()
+        offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        for q in (0, 11, 19):
+            if padding == "zeros":
+                ref = orc.maxsim_packed_zero_padded(Qs[q], Dp, lens)
+            else:
+                ref = orc.maxsim_varlen(Qs[q], Dp, offsets, f64=True)
+            _assert_scores(got[q], ref, f"packed batched {padding} q={q}")
+            one = flashmaxsim_score_packed(_to_gpu(Qs[q][None]), _to_gpu(Dp), torch.from_numpy(lens),
+                                           padding=padding).cpu().numpy()
+            _assert_scores(got[q], one, "packed batched vs one query")
+        assert got[:, 7].tolist() == ([0.0] * 20 if padding == "zeros" else [-np.inf] * 20)
+
+
 def test_masked(cuda):
     import torch
     from tilemaxsim_amd import maxsim_score

@@ -66,6 +66,13 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     # masked without a mask
     rc, msg = _c_call("tms_maxsim_masked", 16, 32, 128, 16, None, 10, 5, 0, 16, None)
     assert rc == 1 and "mask" in msg
+    # tms_maxsim_varlen_batched(Qs, nQ, nq, d, D_flat, T, offsets, B, pad_len, dtype, out, stream)
+    rc, msg = _c_call("tms_maxsim_varlen_batched", 16, 4, 32, 128, 16, 100, None, 10, 0, 0, 16, None)
+    assert rc == 1 and "offsets" in msg and "varlen_batched" in msg
+    rc, msg = _c_call("tms_maxsim_varlen_batched", 16, 4, 32, 128, 16, 100, 16, 10, -1, 0, 16, None)
+    assert rc == 1 and "pad_len" in msg
+    rc, _ = _c_call("tms_maxsim_varlen_batched", 16, 0, 32, 128, 16, 100, 16, 10, 0, 0, None, None)
+    assert rc == 0  # no queries
     # PQ: K beyond uint8 codes, unsupported MFMA shape
     rc, msg = _c_call("tms_pq_score", 16, 32, 16, 16, 300, 8, 0, 16, 10, 5, 16, None)
     assert rc == 2 and "256" in msg
@@ -160,6 +167,15 @@ def test_python_errors_before_device_checks():
         flash_maxsim_multi_doc(Q, D[0], torch.zeros(2, 2, dtype=torch.int64))
     with pytest.raises(ValueError):
         maxsim_score(Q, D, torch.ones(4, 9, dtype=torch.bool))
+    from tilemaxsim_amd import flash_maxsim_multi_doc_batched, flashmaxsim_score_packed_batched
+    with pytest.raises(ValueError, match="nQ, Nq, d"):
+        flash_maxsim_multi_doc_batched(Q, D[0], torch.tensor([0, 10]))
+    with pytest.raises(TypeError):
+        flash_maxsim_multi_doc_batched(Q[None], D[0], torch.tensor([0.0, 10.0]))
+    with pytest.raises(ValueError, match="GPU"):
+        flash_maxsim_multi_doc_batched(Q[None], D[0], torch.tensor([0, 10]))
+    with pytest.raises(ValueError, match="padding"):
+        flashmaxsim_score_packed_batched(Q[None], D[0], torch.tensor([10]), padding="none")
     with pytest.raises(ValueError):
         TileMaxSimPQ(torch.zeros(16, 256, dtype=torch.float16))
     with pytest.raises(TypeError):

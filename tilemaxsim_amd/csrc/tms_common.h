@@ -24,6 +24,14 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
   }
 }
 
+// A value the whole wave shares, moved to scalar registers (so control flow that depends
+// on it is uniform to the compiler).
+__device__ __forceinline__ int64_t wave_uniform(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Cross-lane reductions over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48)
 // with gfx950's row swaps, and over the 16 lanes of a row with DPP; every lane taking
 // part receives the result.

@@ -32,6 +32,10 @@ namespace tms {
 // Fixed-length documents with d in {32, 64, 96, 128} (tms_stream.hip).
 int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype,
                float* out, hipStream_t st);
+// Variable-length documents, d in {32, 64, 96, 128}, several query blocks (tms_stream.hip).
+int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t T,
+                       const int64_t* offsets, int64_t nd, int64_t B, int64_t pad_len, int dtype, float* out,
+                       hipStream_t st);
 
 static thread_local char g_err[512];
 
@@ -550,6 +554,8 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
   const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
   if (mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, dtype, out, st);
+  if (mode == MODE_VARLEN && qreg && a.nbq <= 4 && nQ * a.nbq >= 4)  // one pass for up to 32 blocks
+    return run_varlen_batched(Q, nQ, nq, d, D, total_tokens, offsets, 0, B, pad_len, dtype, out, st);
   if (dtype == TMS_DTYPE_F16) return run_dense<TMS_DTYPE_F16>(a, nQ, mode, aligned, st);
   return run_dense<TMS_DTYPE_BF16>(a, nQ, mode, aligned, st);
 }
@@ -583,6 +589,13 @@ int tms_maxsim_varlen(const void* Q, int64_t nq, int64_t d, const void* D_flat, 
 int tms_maxsim_varlen_padded(const void* Q, int64_t nq, int64_t d, const void* D_flat, int64_t total_tokens,
                              const int64_t* offsets, int64_t B, int64_t pad_len, int dtype, float* out, void* stream) {
   return tms::dense_entry("tms_maxsim_varlen_padded", Q, 1, nq, d, D_flat, B, 0, total_tokens, offsets, nullptr,
+                          tms::MODE_VARLEN, dtype, out, stream, pad_len);
+}
+
+int tms_maxsim_varlen_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d, const void* D_flat,
+                              int64_t total_tokens, const int64_t* offsets, int64_t B, int64_t pad_len, int dtype,
+                              float* out, void* stream) {
+  return tms::dense_entry("tms_maxsim_varlen_batched", Qs, nQ, nq, d, D_flat, B, 0, total_tokens, offsets, nullptr,
                           tms::MODE_VARLEN, dtype, out, stream, pad_len);
 }
 

@@ -40,14 +40,6 @@ constexpr int kThreads = 256;  // the single-query and decompression kernels' wo
 __device__ __forceinline__ f16x2 as_f16x2(uint32_t x) { return __builtin_bit_cast(f16x2, x); }
 __device__ __forceinline__ uint32_t as_u32(f16x2 x) { return __builtin_bit_cast(uint32_t, x); }
 
-// A value the whole wave shares, moved to scalar registers (so control flow that depends
-// on it is uniform to the compiler).
-__device__ __forceinline__ int64_t wave_uniform(int64_t x) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
-  return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
 struct ResArgs {
   const uint8_t* Q;          // (nq, d) fp16
   const uint8_t* centroids;  // (ncent, d) fp16

@@ -12,7 +12,8 @@
 //  * scores are staged in registers (lane i holds document i of the wave's run) and
 //    stored once, coalesced, after the loop.
 // Every wave streams its own documents with the same (one or two) query blocks. Batched
-// queries use batched_maxsim_kernel below, whose workgroups share tiles through LDS.
+// queries use varlen_batched_kernel below, whose workgroups share tiles through LDS (for
+// fixed-length documents at implicit offsets b * nd).
 //
 // Semantics as tms_dense.hip: fp32 accumulation, query rows past nq contribute 0, an
 // empty document scores -inf.
@@ -30,7 +31,7 @@ struct StreamArgs {
   int32_t blk_end;   // one past the last block of this launch
   int32_t nblk;      // blocks per wave
   int32_t d;         // 32 * KS
-  int32_t docs_per_wave;  // documents per wave (per workgroup in the batched kernel); <= 64
+  int32_t docs_per_wave;  // documents per wave; <= 64
 };
 
 template <int DT, int KS, int NB, int PFD>
@@ -192,120 +193,193 @@ struct RingSlotS {
   static constexpr int value = K;
 };
 
-// Batched queries, tiles shared through LDS. The eight waves of a workgroup (one per CU,
-// two per SIMD) stream the same documents; wave w holds a.nblk query blocks (whole
-// queries) in VGPRs, so one pass over D serves up to 8 * a.nblk blocks. Each 16-token
-// tile is loaded from memory once per workgroup: wave w < KS loads k-step w (lane
-// (r, g): chunk 4 w + g of token r, the MFMA A-operand layout) and stores it to a
-// three-slot LDS ring; after a barrier every wave reads the tile's KS k-steps from LDS.
-// A loading wave keeps one 16-byte load per lane in flight per tile, PFD tiles ahead.
-// The barriers fence LDS only, so they never wait for the loads in flight. The MFMA
-// cluster of each tile runs at raised wave priority, so a wave that has its operands
-// keeps the matrix pipe fed ahead of the other wave's bookkeeping.
-template <int DT, int KS, int NB, int PFD>
-__global__ void __launch_bounds__(512, 1) batched_maxsim_kernel(StreamArgs a) {
-  static_assert(PFD >= 2, "tile i+1 is stored to LDS after tile i+PFD's load is issued");
-  static_assert(PFD <= 6 && PFD % 2 == 0, "the step loop is unrolled PFD (even, <= 6) times");
-  constexpr int NS = 3;  // LDS ring slots (two would do: a slot is rewritten only after a barrier that follows its last read)
+#ifndef TMS_STREAM_PFD
+#define TMS_STREAM_PFD 2  // tiles in flight ahead of the one being scored (single-query path)
+#endif
+#ifndef TMS_STREAM_TOKENS_PER_WAVE
+#define TMS_STREAM_TOKENS_PER_WAVE 192
+#endif
+
+template <int DT, int KS, int NB>
+static int stream_launch(const StreamArgs& a, int64_t grid, hipStream_t st) {
+  hipLaunchKernelGGL((stream_maxsim_kernel<DT, KS, NB, TMS_STREAM_PFD>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  return check_launch("stream_maxsim_kernel");
+}
+
+#define TMS_BATCHED_WAVES 8        // waves per workgroup (one workgroup per CU) in the batched kernel
+constexpr int kMaxBlocksPerWave = 4;  // query blocks held in VGPRs per wave there: 1, 2 or 4
+
+template <int DT, int NB>
+static int stream_ks(const StreamArgs& a, int64_t grid, hipStream_t st) {
+  switch (a.d / 32) {
+    case 1: return stream_launch<DT, 1, NB>(a, grid, st);
+    case 2: return stream_launch<DT, 2, NB>(a, grid, st);
+    case 3: return stream_launch<DT, 3, NB>(a, grid, st);
+    default: return stream_launch<DT, 4, NB>(a, grid, st);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Batched queries: many query blocks share each document tile through LDS. One workgroup
+// of eight waves per CU (two per SIMD) walks a run of at most 64 documents (document b is
+// rows [offsets[b], offsets[b+1]) of D, or [b nd, (b+1) nd) for fixed-length documents)
+// in 16-token tiles, every wave the same tiles; the last tile of a document repeats its
+// last token, which cannot change a max. Wave w holds a.nblk query blocks (whole
+// queries) in VGPRs, so one pass over D serves up to 8 * a.nblk blocks. Wave w < KS
+// loads k-step w of each tile (lane (r, g): chunk 4 w + g of token r, the MFMA A-operand
+// layout) NS tiles ahead; step i writes tile i+1 to the LDS ring, passes one LDS-only
+// barrier (the loads in flight are not waited for), reads tile i+1's fragments and
+// scores tile i. The MFMA cluster runs at raised wave priority, so a wave that has its
+// operands keeps the matrix pipe fed ahead of the other wave's bookkeeping; the running
+// max takes two v_max3 per fragment and each document's reduction uses the row swaps and
+// DPP. pad_len > 0 gives the zero-padding semantics of tms_maxsim_varlen_padded; invalid
+// offsets score NaN.
+struct VarlenBatchedArgs {
+  const uint8_t* Q;        // (nQ * nq, d)
+  const uint8_t* D;        // (T, d)
+  const int64_t* offsets;  // (B + 1), or null: document b is rows [b * nd, (b + 1) * nd)
+  float* out;              // (nQ, B)
+  int64_t B, T, pad_len, nd;
+  int32_t nq, nbq, blk0, blk_end, nblk, d, docs_per_wg;
+};
+
+template <int DT, int KS, int NB>
+__global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) varlen_batched_kernel(VarlenBatchedArgs a) {
+  constexpr int NS = 4;  // LDS ring slots and load lead, in tiles
   __shared__ u32x4 ring[NS][4][64];
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g = lane >> 4;
-  const int wid = threadIdx.x >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const float NEG_INF = -__builtin_inff();
 
-  // A wave with no query block still loads its share of every tile.
+  const int64_t b_begin = wave_uniform((int64_t)blockIdx.x * a.docs_per_wg);
+  const int64_t b_end = (b_begin + a.docs_per_wg < a.B) ? b_begin + a.docs_per_wg : a.B;
+  const int64_t ndocs = b_end - b_begin;  // >= 1: the host launches no empty workgroup
+
   const int my_blk0 = a.blk0 + wid * a.nblk;
-  int my_nblk = a.blk_end - my_blk0;
+  int my_nblk = a.blk_end - my_blk0;  // <= 0 for a wave with no query
   if (my_nblk > a.nblk) my_nblk = a.nblk;
-
-  const int64_t b_begin = (int64_t)blockIdx.x * a.docs_per_wave;
-  if (b_begin >= a.B) return;  // whole workgroup
-  const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
-  const int64_t ndocs = b_end - b_begin;
-
-  auto q_valid = [&](int j, int h, int64_t& row) -> bool {
-    const int jb = my_blk0 + j;
-    const int qi = jb / a.nbq;
-    const int tok = (jb - qi * a.nbq) * 32 + 16 * h + r;
-    row = (int64_t)qi * a.nq + tok;
-    return j < my_nblk && tok < a.nq;
-  };
   u32x4 qf[NB][KS][2];
+  bool qv[NB][2];
 #pragma unroll
   for (int j = 0; j < NB; j++)
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      int64_t row;
-      const bool v = q_valid(j, h, row);
+      const int jb = my_blk0 + j;
+      const int qi = jb / a.nbq;
+      const int tok = (jb - qi * a.nbq) * 32 + 16 * h + r;
+      qv[j][h] = j < my_nblk && tok < a.nq;
+      const int64_t row = qv[j][h] ? (int64_t)qi * a.nq + tok : 0;
 #pragma unroll
-      for (int s = 0; s < KS; s++)
-        qf[j][s][h] = v ? *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2) : u32x4{0u, 0u, 0u, 0u};
+      for (int s = 0; s < KS; s++) {
+        const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2);
+        qf[j][s][h] = qv[j][h] ? v : u32x4{0u, 0u, 0u, 0u};
+      }
     }
 
-  bool qv[NB][2];  // query row 16 h + r of block j exists
-#pragma unroll
-  for (int j = 0; j < NB; j++)
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-      int64_t row;
-      qv[j][h] = q_valid(j, h, row);
+  // lane j holds document b_begin + j's first row and length (-1: invalid offsets)
+  int64_t dbase = 0;
+  int32_t dlen = -1;
+  if (lane < ndocs) {
+    const int64_t b = b_begin + lane;
+    const int64_t s0 = a.offsets ? a.offsets[b] : b * a.nd, e0 = a.offsets ? a.offsets[b + 1] : (b + 1) * a.nd;
+    if (s0 >= 0 && e0 >= s0 && e0 <= a.T && e0 - s0 <= 0x7fffffff) {
+      dbase = s0;
+      dlen = (int32_t)(e0 - s0);
     }
-  float pend[NB];
+  }
+  float pend[NB];  // lane j: scores of document b_begin + j
 #pragma unroll
   for (int j = 0; j < NB; j++) pend[j] = NEG_INF;
 
-  if (a.nd > 0) {
-    const int64_t tpd = (a.nd + 15) / 16;  // tiles per document
-    const int64_t total = ndocs * tpd;
-    const int64_t row_bytes = (int64_t)a.d * 2;
-    const bool loader = wid < KS;          // d < 128 has fewer k-steps than waves
-    const int ks = loader ? wid : 0;
-    const uint8_t* base = a.D + b_begin * a.nd * row_bytes + (int64_t)(4 * ks + g) * 16;
+  struct Cur {
+    int64_t b, base;
+    int32_t len, t0;
+  };
+  auto bounds = [&](int64_t b, int64_t& base) -> int32_t {
+    const int j = (int)(b - b_begin);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)dbase, j);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)dbase >> 32), j);
+    base = (int64_t)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_readlane(dlen, j);
+  };
+  // First document at or after b with a token; with `record`, the empty or invalid ones
+  // passed on the way get their scores. Past the end the cursor keeps its last tile.
+  auto seek = [&](Cur& c, int64_t b, bool record) {
+    for (; b < b_end; b++) {
+      int64_t base = 0;
+      const int32_t len = bounds(b, base);
+      if (len > 0) {
+        c.b = b;
+        c.base = base;
+        c.len = len;
+        c.t0 = 0;
+        return;
+      }
+      if (record) {
+        const float v = len < 0 ? __builtin_bit_cast(float, 0x7fc00000u) : (a.pad_len > 0 ? 0.f : NEG_INF);
+#pragma unroll
+        for (int j = 0; j < NB; j++) pend[j] = lane == (int)(b - b_begin) ? v : pend[j];
+      }
+    }
+    c.b = b_end;
+  };
+  auto advance = [&](Cur& c, bool record) {
+    if (c.b >= b_end) return;
+    c.t0 += 16;
+    if (c.t0 >= c.len) seek(c, c.b + 1, record);
+  };
 
-    // load cursor (tile pd * tpd + pt), saturating at the last tile
-    int64_t pd = 0, pt = 0, pf = 0;
-    auto load_next = [&]() -> u32x4 {
-      int64_t tok = pt * 16 + r;
-      if (tok > a.nd - 1) tok = a.nd - 1;
+  Cur wc, wl;  // scoring (tile i), loads (tile i + NS)
+  wc.b = b_end;
+  wc.base = 0;
+  wc.len = 1;
+  wc.t0 = 0;
+  seek(wc, b_begin, true);
+
+  // Instantiated for loading and non-loading waves, so each copy's loads are straight-line
+  // code whose outstanding count the compiler tracks exactly.
+  auto pipeline = [&](auto ld_tag) {
+    constexpr bool LD = decltype(ld_tag)::value == 1;
+    wl = wc;
+    const uint8_t* dcol = a.D + 16 * (4 * (LD ? wid : 0) + g);
+    const int64_t row_bytes = (int64_t)a.d * 2;
+    auto load = [&]() -> u32x4 {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (loader) v = *(const u32x4*)(base + (pd * a.nd + tok) * row_bytes);
-      const bool more = pf < total - 1;
-      pf += more ? 1 : 0;
-      pt += more ? 1 : 0;
-      const bool wrap = pt == tpd;
-      pt = wrap ? 0 : pt;
-      pd += wrap ? 1 : 0;
+      if constexpr (LD) {
+        int32_t t = wl.t0 + r;
+        if (t > wl.len - 1) t = wl.len - 1;
+        v = *(const u32x4*)(dcol + (wl.base + t) * row_bytes);
+      }
+      advance(wl, false);
       return v;
     };
-
-    u32x4 stg[PFD];
-#pragma unroll
-    for (int k = 0; k < PFD; k++) stg[k] = load_next();
-    if (loader) ring[0][ks][lane] = stg[0];
     auto sync = [&]() {  // LDS-only fence: the loads in flight are not waited for
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
-    // Fragments of the tile being scored and of the next one: after the barrier of step i
-    // the tile i+1 fragments are read, and tile i's MFMAs hide that LDS latency.
-    u32x4 frag[2][KS];
+    u32x4 stg[NS];
+#pragma unroll
+    for (int t = 0; t < NS; t++) stg[t] = load();
+    if constexpr (LD) ring[0][wid][lane] = stg[0];
     sync();
+    u32x4 frag[2][KS];
 #pragma unroll
     for (int s = 0; s < KS; s++) frag[0][s] = ring[0][s][lane];
-
     float rmax[NB][2];
 #pragma unroll
     for (int j = 0; j < NB; j++) rmax[j][0] = rmax[j][1] = NEG_INF;
-    int64_t i = 0, cd = 0, ct = 0;  // tile being scored: document cd, tile ct
+
     auto step = [&](auto slot) -> bool {
-      constexpr int k = decltype(slot)::value;  // tile i's load was stg[k]
-      constexpr int f = k & 1;                   // tile i's fragments are frag[f] (PFD is even)
-      stg[k] = load_next();                      // tile i + PFD
-      if (loader && i + 1 < total) ring[(i + 1) % NS][ks][lane] = stg[(k + 1) % PFD];
+      constexpr int i = decltype(slot)::value;  // step index mod NS
+      constexpr int s1 = (i + 1) % NS;
+      constexpr int f = i & 1;
+      stg[i] = load();  // tile i + NS (stg[i] was tile i, in the ring since the last step)
+      if constexpr (LD) ring[s1][wid][lane] = stg[s1];  // tile i+1
       sync();
 #pragma unroll
-      for (int s = 0; s < KS; s++) frag[f ^ 1][s] = ring[(i + 1) % NS][s][lane];  // tile i+1 (unused past the end)
+      for (int s = 0; s < KS; s++) frag[f ^ 1][s] = ring[s1][s][lane];
       const u32x4(&t)[KS] = frag[f];
       f32x4 acc[NB][2];
 #pragma unroll
@@ -321,36 +395,41 @@ __global__ void __launch_bounds__(512, 1) batched_maxsim_kernel(StreamArgs a) {
 #pragma unroll
       for (int j = 0; j < NB; j++)
 #pragma unroll
-        for (int h = 0; h < 2; h++)  // two v_max3 per fragment
+        for (int h = 0; h < 2; h++)
           rmax[j][h] = fmaxf(fmaxf(fmaxf(fmaxf(rmax[j][h], acc[j][h][0]), acc[j][h][1]), acc[j][h][2]), acc[j][h][3]);
-      if (++ct == tpd) {  // document cd done: max over rows, sum over query tokens
+      if (wc.t0 + 16 >= wc.len) {  // document wc.b ends with this tile
+        const bool padded = wc.len < a.pad_len;
 #pragma unroll
         for (int j = 0; j < NB; j++) {
-          float s = (qv[j][0] ? cross_row_max(rmax[j][0]) : 0.f) + (qv[j][1] ? cross_row_max(rmax[j][1]) : 0.f);
-          rmax[j][0] = rmax[j][1] = NEG_INF;
+          float s = 0.f;
+#pragma unroll
+          for (int h = 0; h < 2; h++) {
+            float m = cross_row_max(rmax[j][h]);
+            if (padded) m = fmaxf(m, 0.f);
+            s += qv[j][h] ? m : 0.f;
+            rmax[j][h] = NEG_INF;
+          }
           s = row_sum16(s);
-          pend[j] = lane == (int)cd ? s : pend[j];
+          pend[j] = lane == (int)(wc.b - b_begin) ? s : pend[j];
         }
-        ct = 0;
-        cd++;
       }
-      return ++i == total;
+      advance(wc, true);
+      return wc.b >= b_end;
     };
-    bool done = false;
-    while (!done) {
-      done = step(RingSlotS<0>{});
-      if (!done && PFD > 1) done = step(RingSlotS<1 % PFD>{});
-      if (!done && PFD > 2) done = step(RingSlotS<2 % PFD>{});
-      if (!done && PFD > 3) done = step(RingSlotS<3 % PFD>{});
-      if (!done && PFD > 4) done = step(RingSlotS<4 % PFD>{});
-      if (!done && PFD > 5) done = step(RingSlotS<5 % PFD>{});
+    while (true) {
+      if (step(RingSlotS<0>{})) break;
+      if (step(RingSlotS<1>{})) break;
+      if (step(RingSlotS<2>{})) break;
+      if (step(RingSlotS<3>{})) break;
     }
+  };
+  if (wc.b < b_end) {
+    if (wid < KS) pipeline(RingSlotS<1>{});
+    else pipeline(RingSlotS<0>{});
   }
 
-  if (my_nblk <= 0) return;
-  // coalesced store: lane i writes document b_begin + i, per query (blocks of one query
-  // summed in order; a query that began in an earlier launch accumulates)
-  if (lane < ndocs) {
+  // coalesced store: lane i writes document b_begin + i for each of the wave's queries
+  if (my_nblk > 0 && lane < ndocs) {
     const int64_t b = b_begin + lane;
     float s = 0.f;
 #pragma unroll
@@ -359,66 +438,82 @@ __global__ void __launch_bounds__(512, 1) batched_maxsim_kernel(StreamArgs a) {
       const int jb = my_blk0 + j;
       const int qi = jb / a.nbq;
       s += pend[j];
-      if (j == my_nblk - 1 || (jb + 1) / a.nbq != qi) {
-        float* o = a.out + (int64_t)qi * a.B + b;
-        *o = (qi * a.nbq < my_blk0) ? *o + s : s;
+      if (j == my_nblk - 1 || (jb + 1) / a.nbq != qi) {  // the query's last block
+        a.out[(int64_t)qi * a.B + b] = s;
         s = 0.f;
       }
     }
   }
 }
 
-#ifndef TMS_STREAM_PFD
-#define TMS_STREAM_PFD 2  // tiles in flight ahead of the one being scored (single-query path)
-#endif
-#ifndef TMS_STREAM_TOKENS_PER_WAVE
-#define TMS_STREAM_TOKENS_PER_WAVE 192
-#endif
-
-template <int DT, int KS, int NB>
-static int stream_launch(const StreamArgs& a, int64_t grid, hipStream_t st) {
-  hipLaunchKernelGGL((stream_maxsim_kernel<DT, KS, NB, TMS_STREAM_PFD>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  return check_launch("stream_maxsim_kernel");
-}
-
-#ifndef TMS_BATCHED_PFD
-#define TMS_BATCHED_PFD 4  // tiles in flight per workgroup in the batched kernel
-#endif
-#define TMS_BATCHED_WAVES 8
-template <int DT, int KS, int NB>
-static int batched_launch(const StreamArgs& a, int64_t grid, hipStream_t st) {
-  hipLaunchKernelGGL((batched_maxsim_kernel<DT, KS, NB, TMS_BATCHED_PFD>), dim3((unsigned)grid), dim3(64 * TMS_BATCHED_WAVES), 0,
-                     st, a);
-  return check_launch("batched_maxsim_kernel");
-}
 template <int DT, int NB>
-static int batched_ks(const StreamArgs& a, int64_t grid, hipStream_t st) {
+static int varlen_batched_ks(const VarlenBatchedArgs& a, int64_t grid, hipStream_t st) {
+  const dim3 blk(64 * TMS_BATCHED_WAVES);
   switch (a.d / 32) {
-    case 1: return batched_launch<DT, 1, NB>(a, grid, st);
-    case 2: return batched_launch<DT, 2, NB>(a, grid, st);
-    case 3: return batched_launch<DT, 3, NB>(a, grid, st);
-    default: return batched_launch<DT, 4, NB>(a, grid, st);
+    case 1: hipLaunchKernelGGL((varlen_batched_kernel<DT, 1, NB>), dim3((unsigned)grid), blk, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((varlen_batched_kernel<DT, 2, NB>), dim3((unsigned)grid), blk, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((varlen_batched_kernel<DT, 3, NB>), dim3((unsigned)grid), blk, 0, st, a); break;
+    default: hipLaunchKernelGGL((varlen_batched_kernel<DT, 4, NB>), dim3((unsigned)grid), blk, 0, st, a); break;
   }
+  return check_launch("varlen_batched_kernel");
 }
-// Query blocks held in VGPRs per wave in the batched-query path: 1, 2 or kMaxBlocksPerWave.
-constexpr int kMaxBlocksPerWave = 4;
 template <int DT>
-static int batched_nb(int nb, const StreamArgs& a, int64_t grid, hipStream_t st) {
+static int varlen_batched_nb(int nb, const VarlenBatchedArgs& a, int64_t grid, hipStream_t st) {
   switch (nb) {
-    case 1: return batched_ks<DT, 1>(a, grid, st);
-    case 2: return batched_ks<DT, 2>(a, grid, st);
-    default: return batched_ks<DT, kMaxBlocksPerWave>(a, grid, st);
+    case 1: return varlen_batched_ks<DT, 1>(a, grid, st);
+    case 2: return varlen_batched_ks<DT, 2>(a, grid, st);
+    default: return varlen_batched_ks<DT, kMaxBlocksPerWave>(a, grid, st);
   }
 }
 
-template <int DT, int NB>
-static int stream_ks(const StreamArgs& a, int64_t grid, hipStream_t st) {
-  switch (a.d / 32) {
-    case 1: return stream_launch<DT, 1, NB>(a, grid, st);
-    case 2: return stream_launch<DT, 2, NB>(a, grid, st);
-    case 3: return stream_launch<DT, 3, NB>(a, grid, st);
-    default: return stream_launch<DT, 4, NB>(a, grid, st);
+#ifndef TMS_VARLEN_BATCHED_TOKENS
+#define TMS_VARLEN_BATCHED_TOKENS 4096  // document tokens one workgroup walks (whole documents, at most 64)
+#endif
+
+// Batched-query entry (tms_dense.hip for variable-length documents, run_stream for fixed
+// ones): d in {32, 64, 96, 128}, 16-byte aligned Q and D, queries of at most 4 blocks.
+int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t T,
+                       const int64_t* offsets, int64_t nd, int64_t B, int64_t pad_len, int dtype, float* out,
+                       hipStream_t st) {
+  VarlenBatchedArgs a;
+  a.Q = (const uint8_t*)Q;
+  a.D = (const uint8_t*)D;
+  a.offsets = offsets;
+  a.out = out;
+  a.B = B;
+  a.T = T;
+  a.pad_len = pad_len;
+  a.nd = nd;
+  a.nq = (int32_t)nq;
+  a.nbq = (int32_t)((nq + 31) / 32);
+  a.d = (int32_t)d;
+  const int64_t nblocks = nQ * (int64_t)a.nbq;
+  // Blocks per wave: the smallest of 1, 2, 4 whose launch covers every block in one pass
+  // (a wave computes all of its slots, used or not), else 4. A wave holds whole queries.
+  int nb = kMaxBlocksPerWave;
+  for (int c = 1; c < kMaxBlocksPerWave; c *= 2)
+    if (c >= a.nbq && nblocks <= (int64_t)TMS_BATCHED_WAVES * ((c / a.nbq) * a.nbq)) {
+      nb = c;
+      break;
+    }
+  a.nblk = (nb / a.nbq) * a.nbq;
+  const int64_t hint = B > 0 ? T / B : 1;
+  int64_t dpw = hint > 0 ? TMS_VARLEN_BATCHED_TOKENS / hint : 64;
+  if (dpw > 1 && B / dpw < (int64_t)256 * 4) dpw = B / ((int64_t)256 * 4);
+  if (dpw < 1) dpw = 1;
+  if (dpw > 64) dpw = 64;
+  a.docs_per_wg = (int32_t)dpw;
+  const int64_t grid = (B + dpw - 1) / dpw;
+  if (grid > 0x7fffffff) return fail(TMS_ERR_UNSUPPORTED, "varlen batched: too many documents");
+  const int64_t per_launch = (int64_t)TMS_BATCHED_WAVES * a.nblk;
+  for (int64_t b0 = 0; b0 < nblocks; b0 += per_launch) {
+    a.blk0 = (int32_t)b0;
+    a.blk_end = (int32_t)(nblocks - b0 < per_launch ? nblocks : b0 + per_launch);
+    const int rc = dtype == TMS_DTYPE_F16 ? varlen_batched_nb<TMS_DTYPE_F16>(nb, a, grid, st)
+                                          : varlen_batched_nb<TMS_DTYPE_BF16>(nb, a, grid, st);
+    if (rc) return rc;
   }
+  return TMS_OK;
 }
 
 // Entry used by tms_dense.hip for fixed-length documents with d in {32, 64, 96, 128},
@@ -435,36 +530,8 @@ int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, 
   a.nbq = (int32_t)((nq + 31) / 32);
   a.d = (int32_t)d;
   const int64_t nblocks = nQ * (int64_t)a.nbq;
-  const bool split = a.nbq <= kMaxBlocksPerWave && nblocks >= 4;
-  if (split) {
-    // Blocks per wave: the smallest of 1, 2, 4 whose launch covers every block in one
-    // pass (a wave computes all of its slots, used or not), else 4. A wave holds whole
-    // queries, so a query's blocks never span waves or launches.
-    int nb = kMaxBlocksPerWave;
-    for (int c = 1; c < kMaxBlocksPerWave; c *= 2)
-      if (c >= a.nbq && nblocks <= (int64_t)TMS_BATCHED_WAVES * ((c / a.nbq) * a.nbq)) {
-        nb = c;
-        break;
-      }
-    const int per_wave = (nb / a.nbq) * a.nbq;
-    int64_t dpw = nd > 0 ? 4096 / nd : 64;  // long streams: each wave loads up to 32 KB of queries
-    if (dpw < 1) dpw = 1;
-    if (dpw > 64) dpw = 64;
-    const int64_t min_wgs = (int64_t)256 * 4;  // one workgroup per CU, four rounds
-    if (dpw > 1 && B / dpw < min_wgs) dpw = B / min_wgs > 0 ? B / min_wgs : 1;
-    a.docs_per_wave = (int32_t)dpw;
-    a.nblk = per_wave;
-    const int64_t grid = (B + dpw - 1) / dpw;
-    const int64_t per_launch = (int64_t)TMS_BATCHED_WAVES * per_wave;
-    for (int64_t b0 = 0; b0 < nblocks; b0 += per_launch) {
-      a.blk0 = (int32_t)b0;
-      a.blk_end = (int32_t)(nblocks - b0 < per_launch ? nblocks : b0 + per_launch);
-      const int rc = dtype == TMS_DTYPE_F16 ? batched_nb<TMS_DTYPE_F16>(nb, a, grid, st)
-                                            : batched_nb<TMS_DTYPE_BF16>(nb, a, grid, st);
-      if (rc) return rc;
-    }
-    return TMS_OK;
-  }
+  if (a.nbq <= kMaxBlocksPerWave && nblocks >= 4)  // batched: documents at implicit offsets b * nd
+    return run_varlen_batched(Q, nQ, nq, d, D, B * nd, nullptr, nd, B, 0, dtype, out, st);
   int64_t dpw = nd > 0 ? TMS_STREAM_TOKENS_PER_WAVE / nd : 1;
   const int64_t min_waves = (int64_t)256 * 16 * 2;
   if (dpw > 1 && B / dpw < min_waves) dpw = B / min_waves;

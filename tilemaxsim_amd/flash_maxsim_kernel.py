@@ -4,7 +4,9 @@ the masked scorer of ``src/e2e_retrieval_quality.py``.
 * :func:`flash_maxsim_single` / :func:`flash_maxsim_batch` -- fixed-length documents
   (``tms_maxsim_dense``).
 * :func:`flash_maxsim_multi_doc` -- variable-length documents in a flat token buffer
-  with offsets, scored by one kernel launch with no padding (``tms_maxsim_varlen``).
+  with offsets, scored by one kernel launch with no padding (``tms_maxsim_varlen``);
+  :func:`flash_maxsim_multi_doc_batched` scores many queries in one pass over them
+  (``tms_maxsim_varlen_batched``).
 * :func:`maxsim_score` -- padded documents with a token mask (``tms_maxsim_masked``).
 """
 from __future__ import annotations
@@ -98,6 +100,58 @@ def flash_maxsim_multi_doc(Q: torch.Tensor, D_flat: torch.Tensor, doc_offsets: t
         _lib.check(lib.tms_maxsim_varlen(Q.data_ptr(), Nq, d, D_flat.data_ptr(), T, offsets.data_ptr(), num_docs,
                                          _lib.dtype_code(D_flat.dtype), scores.data_ptr(), _lib.stream_of(Q)))
     return scores
+
+
+def _varlen_batched(fn: str, Qs: torch.Tensor, D_flat: torch.Tensor, doc_offsets: torch.Tensor, validate: bool,
+                    zero_pad: bool) -> torch.Tensor:
+    _check.tensor("Qs", Qs)
+    _check.tensor("D_flat", D_flat)
+    _check.tensor("doc_offsets", doc_offsets)
+    if Qs.dim() != 3 or D_flat.dim() != 2:
+        raise ValueError(f"{fn}: Qs must be (nQ, Nq, d) and D_flat (total_tokens, d)")
+    if doc_offsets.dim() != 1 or doc_offsets.shape[0] < 1:
+        raise ValueError(f"{fn}: doc_offsets must be a 1-D tensor of num_docs + 1 entries")
+    if doc_offsets.dtype.is_floating_point or doc_offsets.dtype == torch.bool:
+        raise TypeError(f"{fn}: doc_offsets must be integer, got {doc_offsets.dtype}")
+    T, d = D_flat.shape
+    nQ, Nq = Qs.shape[0], Qs.shape[1]
+    assert Qs.shape[2] == d, f"{fn}: Q width {Qs.shape[2]} != D width {d}"
+    _check.embedding_dtype("D_flat", D_flat)
+    _check.contiguous("D_flat", D_flat)
+    _check.on_gpu("Qs", Qs)
+    _check.on_gpu("D_flat", D_flat)
+    _check.same_device(Qs=Qs, D_flat=D_flat)
+    Qs = _check.query_like(Qs, D_flat.dtype)
+    offsets = doc_offsets.to(device=Qs.device, dtype=torch.int64).contiguous()
+    B = offsets.shape[0] - 1
+    if (validate or zero_pad) and B > 0:
+        bad = (offsets[0] < 0) | (offsets[-1] > T) | (offsets[1:] < offsets[:-1]).any()
+        if bool(bad):
+            raise ValueError(f"{fn}: doc_offsets must be non-decreasing within [0, total_tokens]")
+    pad_len = int((offsets[1:] - offsets[:-1]).max()) if zero_pad and B > 0 else 0
+    out = torch.empty(nQ, B, dtype=torch.float32, device=Qs.device)
+    if B == 0 or nQ == 0:
+        return out
+    lib = _lib.load()
+    with torch.cuda.device(Qs.device):
+        _lib.check(lib.tms_maxsim_varlen_batched(Qs.data_ptr(), nQ, Nq, d, D_flat.data_ptr(), T, offsets.data_ptr(), B,
+                                                 pad_len, _lib.dtype_code(D_flat.dtype), out.data_ptr(),
+                                                 _lib.stream_of(Qs)))
+    return out
+
+
+def flash_maxsim_multi_doc_batched(Qs: torch.Tensor, D_flat: torch.Tensor, doc_offsets: torch.Tensor,
+                                   validate: bool = True) -> torch.Tensor:
+    """:func:`flash_maxsim_multi_doc` for ``nQ`` queries at once: ``Qs`` (nQ, Nq, d) ->
+    (nQ, num_docs) float32.
+
+    Up to 32 blocks of 32 query tokens share each pass over the documents (one tile
+    load per workgroup, scored from LDS by all of them), which makes the call MFMA-bound
+    instead of one HBM pass per query. Empty documents score -inf; with
+    ``validate=False`` a document with invalid offsets scores NaN.
+    No reference counterpart (the reference loops over queries).
+    """
+    return _varlen_batched("flash_maxsim_multi_doc_batched", Qs, D_flat, doc_offsets, validate, False)
 
 
 def maxsim_score(Q: torch.Tensor, D: torch.Tensor, D_mask: torch.Tensor | None = None) -> torch.Tensor:

@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 
 from . import _check, _lib
-from .flash_maxsim_kernel import flash_maxsim_multi_doc
+from .flash_maxsim_kernel import _varlen_batched, flash_maxsim_multi_doc
 
 
 def lengths_to_offsets(D_lengths: torch.Tensor, device: torch.device) -> torch.Tensor:
@@ -77,3 +77,24 @@ def flashmaxsim_score_packed(Q: torch.Tensor, D_packed: torch.Tensor, D_lengths:
                                                 offsets.data_ptr(), B, pad_len, _lib.TMS_DTYPE_F16,
                                                 scores.data_ptr(), _lib.stream_of(Q2)))
     return scores
+
+
+def flashmaxsim_score_packed_batched(Qs: torch.Tensor, D_packed: torch.Tensor, D_lengths: torch.Tensor,
+                                     padding: str = "zeros") -> torch.Tensor:
+    """:func:`flashmaxsim_score_packed` for ``nQ`` queries over the same packed documents:
+    ``Qs`` (nQ, Nq, d) -> (nQ, B) float32, one pass over the tokens for up to 32 query
+    blocks. ``padding`` as in :func:`flashmaxsim_score_packed`."""
+    if padding not in ("zeros", "mask"):
+        raise ValueError(f"padding must be 'zeros' or 'mask', got {padding!r}")
+    _check.tensor("Qs", Qs)
+    _check.tensor("D_packed", D_packed)
+    _check.tensor("D_lengths", D_lengths)
+    if D_lengths.dim() != 1 or D_lengths.dtype.is_floating_point or D_lengths.dtype == torch.bool:
+        raise TypeError("flashmaxsim_score_packed_batched: D_lengths must be a 1-D integer tensor")
+    if D_packed.dtype != torch.float16:
+        D_packed = D_packed.half()
+    D_packed = D_packed.contiguous()
+    _check.on_gpu("D_packed", D_packed)
+    offsets = lengths_to_offsets(D_lengths, D_packed.device)
+    return _varlen_batched("flashmaxsim_score_packed_batched", Qs.to(D_packed.device).half(), D_packed, offsets,
+                           True, padding == "zeros")
