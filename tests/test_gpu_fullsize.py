@@ -1,4 +1,4 @@
-"""Parity at BASELINE's full sizes (C2-C5, c6/c6b, top-k over C2's score matrix).
+"""Parity at BASELINE's full sizes (C2-C5 with c2b/c3b, c6/c6b, top-k over C2's score matrix).
 
 Each test builds one configuration at its benchmark size on the GPU, scores it through
 the public entry points, and checks a seeded sample of documents, always including the
@@ -60,9 +60,10 @@ def test_c2_dense_and_batched_fullsize(cuda):
 
 
 def test_c3_varlen_fullsize(cuda):
-    """C3: 2M docs, Nd ~ U[32, 300] (332M tokens, 85 GB), int64 offsets."""
+    """C3: 2M docs, Nd ~ U[32, 300] (332M tokens, 85 GB), int64 offsets; one query through
+    the varlen kernel and 32 through the batched kernel (c3b)."""
     import torch
-    from tilemaxsim_amd import flash_maxsim_multi_doc
+    from tilemaxsim_amd import flash_maxsim_multi_doc, flash_maxsim_multi_doc_batched
     rng = np.random.default_rng(77)
     lens = rng.integers(32, 301, size=2_000_000)
     offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
@@ -75,6 +76,12 @@ def test_c3_varlen_fullsize(cuda):
     sub_offs = np.concatenate([[0], np.cumsum(lens[idx])]).astype(np.int64)
     ref = orc.maxsim_varlen(Q.cpu().numpy(), sub, sub_offs, f64=True)
     np.testing.assert_allclose(got[idx], ref, rtol=RTOL, atol=ATOL)
+    # c3b: 32 queries through the batched kernel, three of them checked on the sample
+    Qs = _normal_fp16(torch, (32, 32, 128), 23)
+    gotb = flash_maxsim_multi_doc_batched(Qs, D, torch.from_numpy(offs).cuda(), validate=False).cpu().numpy()
+    for q in (0, 13, 31):
+        refq = orc.maxsim_varlen(Qs[q].cpu().numpy(), sub, sub_offs, f64=True)
+        np.testing.assert_allclose(gotb[q][idx], refq, rtol=RTOL, atol=ATOL)
     del D
     _release(torch)
 

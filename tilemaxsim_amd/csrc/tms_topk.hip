@@ -7,9 +7,12 @@
 // so descending key order is "value descending, then index ascending" -- deterministic,
 // and compared as integers (no float NaN semantics involved).
 //
-// Tournament: a workgroup sorts a chunk of kChunk keys in LDS (bitonic network) and keeps
-// its best k; each level shrinks a row by kChunk / k until one chunk holds it, whose sorted
-// head is the answer. Intermediate keys live in a caller-provided workspace.
+// Tournament: a workgroup selects the best k of a chunk of kChunk keys and each level
+// shrinks a row by kChunk / k until one chunk holds it; the last level sorts its k keys.
+// Intermediate keys live in a caller-provided workspace. Selection is a radix select on
+// the 64-bit keys held in registers (16 per thread): one 256-bin LDS histogram per 8-bit
+// digit, from the top, narrowed to the keys that share the digits fixed so far, until
+// the k-th largest key is known or a whole bin is needed (usually 3-4 passes).
 #include <string.h>
 
 #include "tms_common.h"
@@ -30,52 +33,128 @@ __device__ __forceinline__ float key_value(uint32_t k) {
 }
 
 // FIRST: input is fp32 scores (row stride in_stride), indices are positions in the row.
-// Otherwise input is keys. LAST: write (value, index) pairs; otherwise write the best k keys.
+// Otherwise input is keys. LAST: write (value, index) pairs in descending order;
+// otherwise write the best k keys of the chunk, in no particular order.
+constexpr int kPerThread = kChunk / kTopkThreads;  // 16 keys per thread
+static_assert(kTopkThreads == 256, "one histogram bin per thread; wave 0 scans four bins per lane");
+
 template <bool FIRST, bool LAST>
 __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* __restrict__ vals,
                                                                   const uint64_t* __restrict__ keys_in, int64_t n_in,
                                                                   int64_t in_stride, uint64_t* __restrict__ keys_out,
                                                                   int64_t out_stride, float* __restrict__ out_vals,
                                                                   int64_t* __restrict__ out_idx, int k) {
-  __shared__ uint64_t s[kChunk];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t pick[3];  // digit, keys above its bin, keys in its bin
+  __shared__ uint32_t n_gt, n_eq;
+  __shared__ uint64_t sel[LAST ? kMaxK : 1];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t row = blockIdx.y;
   const int64_t c0 = (int64_t)blockIdx.x * kChunk;
-  for (int i = threadIdx.x; i < kChunk; i += kTopkThreads) {
-    const int64_t p = c0 + i;
-    uint64_t key = 0;  // below every real element
+  uint64_t key[kPerThread];
+#pragma unroll
+  for (int e = 0; e < kPerThread; e++) {
+    const int64_t p = c0 + e * kTopkThreads + tid;
+    key[e] = 0;  // below every real element
     if (p < n_in) {
       if constexpr (FIRST) {
-        key = ((uint64_t)order_key(vals[row * in_stride + p]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)p);
+        key[e] = ((uint64_t)order_key(vals[row * in_stride + p]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)p);
       } else {
-        key = keys_in[row * in_stride + p];
+        key[e] = keys_in[row * in_stride + p];
       }
     }
-    s[i] = key;
+  }
+
+  // Radix select. After a pass, `prefix` holds the digits fixed so far and `need` the
+  // number of keys still to take among the keys that share them.
+  uint64_t prefix = 0;
+  uint32_t need = (uint32_t)k;
+  int shift = 64;
+  bool whole_bin = false;  // the selection is every key >= prefix << shift
+  while (shift > 0) {
+    shift -= 8;
+    hist[tid] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kPerThread; e++)
+      if (shift == 56 || (key[e] >> (shift + 8)) == prefix) atomicAdd(&hist[(uint32_t)(key[e] >> shift) & 255u], 1u);
+    __syncthreads();
+    if (wid == 0) {  // lane l scans bins 255 - 4l .. 252 - 4l, high to low
+      uint32_t c[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) c[j] = hist[255 - 4 * lane - j];
+      const uint32_t own = c[0] + c[1] + c[2] + c[3];
+      uint32_t incl = own;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      const uint32_t excl = incl - own;
+      if (excl < need && need <= incl) {  // exactly one lane: the need-th key is in its bins
+        uint32_t above = excl;
+        int j = 0;
+        while (above + c[j] < need) above += c[j++];
+        pick[0] = (uint32_t)(255 - 4 * lane - j);
+        pick[1] = above;
+        pick[2] = c[j];
+      }
+    }
+    __syncthreads();
+    const uint32_t d = pick[0], above = pick[1], cnt = pick[2];
+    need -= above;
+    prefix = (prefix << 8) | d;
+    if (cnt == need && prefix != 0) {  // the whole bin is needed (keys are unique but padding)
+      whole_bin = true;
+      break;
+    }
+  }
+  // Selection: every key > T, then `need` keys equal to T (only padding keys repeat).
+  const uint64_t T = whole_bin ? (prefix << shift) - 1 : prefix;
+  const uint32_t need_eq = whole_bin ? 0u : need;
+  if (tid == 0) {
+    n_gt = 0u;
+    n_eq = 0u;
   }
   __syncthreads();
-  // bitonic sort, descending
-  for (int size = 2; size <= kChunk; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < kChunk / 2; i += kTopkThreads) {
-        const int pos = 2 * i - (i & (stride - 1));
-        const int partner = pos + stride;
-        const bool desc = (pos & size) == 0;
-        const uint64_t a = s[pos], b = s[partner];
-        if ((a < b) == desc) {
-          s[pos] = b;
-          s[partner] = a;
-        }
-      }
-      __syncthreads();
+  auto put = [&](uint32_t pos, uint64_t kv) {
+    if constexpr (LAST) sel[pos] = kv;
+    else keys_out[row * out_stride + (int64_t)blockIdx.x * k + pos] = kv;
+  };
+#pragma unroll
+  for (int e = 0; e < kPerThread; e++) {
+    if (key[e] > T) {
+      const uint32_t pos = atomicAdd(&n_gt, 1u);
+      if (pos < (uint32_t)k - need_eq) put(pos, key[e]);  // always true; bounds every write
+    } else if (key[e] == T && need_eq > 0u) {
+      const uint32_t j = atomicAdd(&n_eq, 1u);
+      if (j < need_eq) put((uint32_t)k - need_eq + j, key[e]);
     }
   }
-  for (int i = threadIdx.x; i < k; i += kTopkThreads) {
-    const uint64_t key = s[i];
-    if constexpr (LAST) {
-      out_vals[row * k + i] = key_value((uint32_t)(key >> 32));
-      out_idx[row * k + i] = (int64_t)(0xffffffffu - (uint32_t)key);
-    } else {
-      keys_out[row * out_stride + (int64_t)blockIdx.x * k + i] = key;
+  if constexpr (LAST) {
+    int P = 1;  // bitonic sort of the k survivors, padded to a power of two
+    while (P < k) P <<= 1;
+    for (int i = k + tid; i < P; i += kTopkThreads) sel[i] = 0;
+    __syncthreads();
+    for (int size = 2; size <= P; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < P / 2; i += kTopkThreads) {
+          const int pos = 2 * i - (i & (stride - 1));
+          const int partner = pos + stride;
+          const bool desc = (pos & size) == 0;
+          const uint64_t a = sel[pos], b = sel[partner];
+          if ((a < b) == desc) {
+            sel[pos] = b;
+            sel[partner] = a;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int i = tid; i < k; i += kTopkThreads) {
+      const uint64_t kv = sel[i];
+      out_vals[row * k + i] = key_value((uint32_t)(kv >> 32));
+      out_idx[row * k + i] = (int64_t)(0xffffffffu - (uint32_t)kv);
     }
   }
 }
