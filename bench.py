@@ -9,7 +9,8 @@ query, as the reference's V2-MQ kernel) and takes the top-100 per query.
 Other workloads (``--config``): c1 (CPU-sized plumbing check), c2b (C2 with all 64
 queries through the batched-query kernel), c3 (2M variable-length documents), c3b (c3
 through the batched-query kernel), c4
-(d-tiled, ``--d 256|512|768``), c5 (PQ/ADC, 5M documents of uint8 codes), c6 (C3's
+(d-tiled, ``--d 256|512|768``), c5 (PQ/ADC, 5M documents of uint8 codes), c5b (c5
+through the batched-query kernel), c6 (C3's
 corpus as a ColBERTv2 residual-compressed index, fused decode + MaxSim per query), c6b
 (the same index, all queries through the batched residual kernel), copy (counter
 calibration).
@@ -46,7 +47,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c6", "c6b", "copy"])
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "copy"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -146,7 +147,7 @@ class Dense:
         step_ms = float(np.mean([a.elapsed_time(c) for a, _, c in calls]))
         tf = 2 * self.nQ * self.Nq * self.B * self.Nd * self.d / (call_ms * 1e-3) / 1e12
         line = {"value": round(self.pairs_per_step() / (step_ms * 1e-3), 1), "unit": "docs/s", "ms_per_step": round(step_ms, 3),
-                "steps": steps, "kernel": "varlen_batched_kernel", "launch_ms_mean": round(call_ms, 4),
+                "steps": steps, "kernel": "batched_tile_kernel", "launch_ms_mean": round(call_ms, 4),
                 "achieved_tflops": round(tf, 1), "peak_tflops": 2500.0, "frac": round(tf / 2500.0, 4),
                 "note": "flash_maxsim_batched_queries: 32 queries share each HBM pass (see --config c2b)"}
         line.update(gemm_ceiling(torch, tf))
@@ -196,7 +197,7 @@ class DenseBatched(Dense):
 
     def __init__(self, *args, **kw):
         super().__init__(*args, **kw)
-        self.kernel = "varlen_batched_kernel"  # fixed-length documents at implicit offsets
+        self.kernel = "batched_tile_kernel"  # fixed-length documents at implicit offsets
 
     def step(self, timer):
         from tilemaxsim_amd import flash_maxsim_batched_queries
@@ -270,7 +271,7 @@ class VarlenBatched(Varlen):
     """C3's corpus and queries, all queries scored by one batched call
     (flash_maxsim_multi_doc_batched): each tile is loaded once per workgroup and scored
     from LDS by 32 query blocks, which moves the path to the MFMA roof."""
-    kernel = "varlen_batched_kernel"
+    kernel = "batched_tile_kernel"
     MFMA_PEAK_TFLOPS = 2500.0
     launch_desc = "one flash_maxsim_multi_doc_batched call (one kernel per 32 query blocks)"
 
@@ -499,6 +500,43 @@ class PQ:
                          f"{n} docs x query 0, numpy decompress-then-score (restates pytorch_pqsim_baseline), repeated")
 
 
+class PQBatched(PQ):
+    """c5's codes and queries, all queries scored by one batched call
+    (TileMaxSimPQ.score_batch_queries): each tile of codes is decoded once per pass
+    through the codebook in LDS and shared by 32 query blocks, so the decode is paid once
+    for all the queries and the call is MFMA-bound."""
+    kernel = "batched_tile_kernel"
+    MFMA_PEAK_TFLOPS = 2500.0
+    launch_desc = "one TileMaxSimPQ.score_batch_queries call (one kernel per 32 query blocks)"
+
+    def step(self, timer):
+        s = timer(lambda: self.pq.score_batch_queries(self.Q, self.codes, validate=False))
+        self.scores.copy_(s)
+        return topk_rows(self.scores, self.k)
+
+    def flops_per_launch(self):
+        return 2 * self.nQ * self.Nq * self.M * self.dsub * self.B * self.Nd
+
+    def bytes_per_launch(self):  # the codes once for all queries
+        return self.nQ * self.Nq * self.M * self.dsub * 2 + self.B * self.Nd * self.M + self.nQ * self.B * 4
+
+    def extra_roofline(self, launch_ms):
+        """The north-star view per query: code bytes scored per second for each query
+        (nQ passes' worth of codes in one call) against the 8 TB/s HBM peak, and the MFMA
+        rate beside an fp16 GEMM measured in the same process."""
+        per_query_gbs = self.nQ * self.B * self.Nd * self.M / (launch_ms * 1e-3) / 1e9
+        out = {"code_bytes_per_query_gbs": round(per_query_gbs, 1),
+               "code_bytes_per_query_frac_of_hbm": round(per_query_gbs / HBM_PEAK_GBS, 4)}
+        out.update(gemm_ceiling(self.torch, self.flops_per_launch() / (launch_ms * 1e-3) / 1e12))
+        return out
+
+    def config(self):
+        c = super().config()
+        c["workload"] = c["workload"].replace("c5:", "c5b:", 1) + " (batched-query kernel)"
+        c["kernel"] = "TileMaxSimPQ.score_batch_queries (tiles decoded once into LDS, shared by 32 query blocks)"
+        return c
+
+
 class Copy:
     """Plain device-to-device copy of a known size (torch's copy kernel): the reference
     point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes."""
@@ -579,6 +617,8 @@ def main():
         wl = Dense(torch, 16, 200_000, 128, args.d, name=f"c4_d{args.d}")
     elif args.config == "c5":
         wl = PQ(torch, 32, 5_000_000, 128)
+    elif args.config == "c5b":
+        wl = PQBatched(torch, 32, 5_000_000, 128)
     elif args.config == "c6":
         wl = Residual(torch, 32, 2_000_000, 32, 300)
     elif args.config == "c6b":

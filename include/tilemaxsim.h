@@ -126,6 +126,18 @@ int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int
                  const uint8_t* codes, int64_t B, int64_t nd, float* out, void* stream);
 
 /*
+ * Batched-query PQ scoring: nQ queries of nq tokens (Qs is (nQ, nq, M*dsub)) against the
+ * same uint8 codes; out is (nQ, B), row-major. Shapes as tms_pq_score (its MFMA path);
+ * with at most 128 tokens per query, each 16-token tile is decoded once per pass (codes
+ * gathered through the codebook in LDS) and shared by up to 32 query blocks of 32
+ * tokens. Replaces nQ calls of TileMaxSimPQ.score_batch (src/flash_pqsim_kernel.py:213-252)
+ * over the same codes.
+ */
+int tms_pq_score_batched(const void* Qs, int64_t nQ, int64_t nq, const void* codebook, int64_t M, int64_t K,
+                         int64_t dsub, int dtype, const uint8_t* codes, int64_t B, int64_t nd, float* out,
+                         void* stream);
+
+/*
  * Row-wise top-k of an fp32 score matrix (nrows, n): values (nrows, k) descending with
  * int64 indices; equal values come out in ascending index order and NaN ranks above
  * +inf. Needs tms_topk_workspace_size(nrows, n, k) bytes of device workspace (0 when a

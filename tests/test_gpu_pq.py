@@ -139,3 +139,65 @@ def test_pq_methods_agree_and_rank(cuda):
         diff = set(orc.topk(got, 100)[1].tolist()) ^ set(orc.topk(ref, 100)[1].tolist())
         for i in diff:
             assert abs(ref[i] - kth) <= RTOL * abs(kth) + ATOL
+
+
+# (M, K, dsub): every codeword width of the MFMA shapes, K < 256, d < 128
+@pytest.mark.parametrize("M,K,dsub", [(16, 256, 8), (32, 256, 4), (64, 100, 2), (8, 256, 16), (4, 128, 32),
+                                      (8, 256, 8), (12, 64, 8)])
+def test_pq_batched_queries_formats(cuda, M, K, dsub):
+    """tms_pq_score_batched: each tile decoded once and shared by the query blocks."""
+    from tilemaxsim_amd import TileMaxSimPQ
+    rng = np.random.default_rng(M * 1000 + K + dsub)
+    Q, C, codes = _mk(M + dsub, M, K, dsub, 32, 700, 45)
+    Qs = np.stack([Q] + [rng.standard_normal(Q.shape, dtype=np.float32).astype(np.float16) for _ in range(5)])
+    pq = TileMaxSimPQ(_gpu(C))
+    got = pq.score_batch_queries(_gpu(Qs), _gpu(codes)).cpu().numpy()
+    assert got.shape == (6, 700)
+    for q in range(6):
+        _check(got[q], orc.pq_decompress_score(Qs[q], C, codes, f64=True), f"M={M} K={K} dsub={dsub} q={q}")
+    one = pq.score_batch(_gpu(Qs[5]), _gpu(codes)).cpu().numpy()
+    _check(got[5], one, "batched vs one query")
+
+
+# (nQ, Nq): 1 block per wave; 2 per wave; 4 per wave over two launches; 3 blocks per
+# query; 4 blocks per query; 5 blocks per query (query by query); a single block
+@pytest.mark.parametrize("nQ,nq", [(5, 32), (12, 32), (37, 32), (4, 70), (6, 128), (2, 150), (1, 32)])
+def test_pq_batched_queries_shapes(cuda, nQ, nq):
+    from tilemaxsim_amd import TileMaxSimPQ
+    rng = np.random.default_rng(nQ * 100 + nq)
+    _, C, codes = _mk(nQ + nq, 16, 256, 8, 1, 1500, 77)
+    Qs = rng.standard_normal((nQ, nq, 128), dtype=np.float32)
+    Qs = (Qs / np.linalg.norm(Qs, axis=-1, keepdims=True)).astype(np.float16)
+    got = TileMaxSimPQ(_gpu(C)).score_batch_queries(_gpu(Qs), _gpu(codes)).cpu().numpy()
+    for q in range(nQ):
+        _check(got[q], orc.pq_decompress_score(Qs[q], C, codes, f64=True), f"nQ={nQ} nq={nq} q={q}")
+
+
+def test_pq_batched_queries_edges(cuda):
+    import torch
+    from tilemaxsim_amd import TileMaxSimPQ
+    Q, C, codes = _mk(9, 16, 200, 8, 32, 300, 33)
+    Qs = np.stack([Q, Q[::-1].copy(), Q * 2])
+    pq = TileMaxSimPQ(_gpu(C))
+    # codes >= K: rejected when validated, clamped into the table otherwise
+    bad = codes.copy()
+    bad[3, 5, 7] = 250
+    with pytest.raises(ValueError):
+        pq.score_batch_queries(_gpu(Qs), _gpu(bad))
+    got = pq.score_batch_queries(_gpu(Qs), _gpu(bad), validate=False).cpu().numpy()
+    for q in range(3):
+        _check(got[q], orc.pq_decompress_score(Qs[q], C, np.minimum(bad, 199), f64=True), f"clamped q={q}")
+    # bf16 codebook and queries
+    pqb = TileMaxSimPQ(_gpu(C).to(torch.bfloat16))
+    got = pqb.score_batch_queries(_gpu(Qs).to(torch.bfloat16), _gpu(codes)).cpu().numpy()
+    Cb = _gpu(C).to(torch.bfloat16).float().cpu().numpy()
+    Qb = _gpu(Qs).to(torch.bfloat16).float().cpu().numpy()
+    for q in range(3):
+        _check(got[q], orc.pq_decompress_score(Qb[q], Cb, codes, f64=True), f"bf16 q={q}")
+    # no document tokens; no query tokens; no documents; no queries
+    got = pq.score_batch_queries(_gpu(Qs), _gpu(codes[:, :0])).cpu().numpy()
+    assert got.shape == (3, 300) and np.all(got == -np.inf)
+    got = pq.score_batch_queries(_gpu(Qs[:, :0]), _gpu(codes)).cpu().numpy()
+    assert np.all(got == 0.0)
+    assert pq.score_batch_queries(_gpu(Qs), _gpu(codes[:0])).shape == (3, 0)
+    assert pq.score_batch_queries(_gpu(Qs[:0]), _gpu(codes)).shape == (0, 300)

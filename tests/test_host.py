@@ -80,6 +80,13 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert rc == 2 and "tms_pq_score_lut" in msg
     rc, msg = _c_call("tms_pq_score_lut", 16, 32, 1000, 256, 16, 10, 5, 16, None)
     assert rc == 2 and "LDS" in msg
+    # tms_pq_score_batched(Qs, nQ, nq, codebook, M, K, dsub, dtype, codes, B, nd, out, stream)
+    rc, msg = _c_call("tms_pq_score_batched", 16, -2, 32, 16, 16, 256, 8, 0, 16, 10, 5, 16, None)
+    assert rc == 1 and "negative" in msg
+    rc, msg = _c_call("tms_pq_score_batched", 16, 3, 32, 16, 16, 256, 3, 0, 16, 10, 5, 16, None)
+    assert rc == 2 and "tms_pq_score_lut" in msg
+    rc, _ = _c_call("tms_pq_score_batched", 16, 0, 32, 16, 16, 256, 8, 0, 16, 10, 5, None, None)
+    assert rc == 0  # no queries
 
 
 def test_topk_workspace_sizes():

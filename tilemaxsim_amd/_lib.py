@@ -45,6 +45,8 @@ SIGNATURES = {
                             _c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tms_maxsim_varlen_batched": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _int,
                                   _c_void_p, _c_void_p],
+    "tms_pq_score_batched": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _i64, _i64,
+                             _c_void_p, _c_void_p],
     "tms_maxsim_residual_batched": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _int, _c_void_p,
                                     _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
 }

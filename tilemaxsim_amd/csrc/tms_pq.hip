@@ -409,6 +409,10 @@ static int build_lut(const void* Q, int64_t nq, const void* C, int64_t M, int64_
 }
 
 static int fill_scores(float* out, int64_t n, float v, hipStream_t st);
+// Batched queries over PQ codes (tms_stream.hip): the shared-tile kernel with the codebook
+// gather as its tile source.
+int run_pq_batched(const void* Q, int64_t nQ, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub,
+                   int dtype, const uint8_t* codes, int64_t B, int64_t nd, float* out, hipStream_t st);
 
 template <int QG>
 static int launch_lut_score(const LutArgs& a, hipStream_t st) {
@@ -584,6 +588,40 @@ int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int
               "%s: shape M=%lld K=%lld dsub=%lld (or alignment) not supported by the MFMA kernel; "
               "use tms_pq_build_lut + tms_pq_score_lut",
               fn, (long long)M, (long long)K, (long long)dsub);
+}
+
+int tms_pq_score_batched(const void* Qs, int64_t nQ, int64_t nq, const void* codebook, int64_t M, int64_t K,
+                         int64_t dsub, int dtype, const uint8_t* codes, int64_t B, int64_t nd, float* out,
+                         void* stream) {
+  const char* fn = "tms_pq_score_batched";
+  if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16) return fail(TMS_ERR_UNSUPPORTED, "%s: unsupported dtype %d", fn, dtype);
+  if (nQ < 0) return fail(TMS_ERR_INVALID, "%s: negative size", fn);
+  int rc = pq_common_checks(fn, nq, M, K, dsub, B, nd);
+  if (rc) return rc;
+  if (B == 0 || nQ == 0) return TMS_OK;
+  if (!out) return fail(TMS_ERR_INVALID, "%s: out is NULL", fn);
+  if (nd > 0 && M > 0 && !codes) return fail(TMS_ERR_INVALID, "%s: codes is NULL", fn);
+  if (nq > 0 && (!Qs || !codebook)) return fail(TMS_ERR_INVALID, "%s: Q or codebook is NULL", fn);
+  if (M == 0 || K == 0 || dsub == 0) return fail(TMS_ERR_UNSUPPORTED, "%s: M, K and dsub must be positive", fn);
+  if (nq > ((int64_t)1 << 24) || nQ > ((int64_t)1 << 20)) return fail(TMS_ERR_UNSUPPORTED, "%s: too many queries", fn);
+  hipStream_t st = (hipStream_t)stream;
+  if (nq == 0 || nd == 0) return fill_scores(out, nQ * B, nq == 0 ? 0.f : -__builtin_inff(), st);
+  if (!mfma_supported(Qs, codebook, codes, M, K, dsub))
+    return fail(TMS_ERR_UNSUPPORTED,
+                "%s: shape M=%lld K=%lld dsub=%lld (or alignment) not supported by the MFMA kernels; score per "
+                "query with tms_pq_build_lut + tms_pq_score_lut",
+                fn, (long long)M, (long long)K, (long long)dsub);
+  const int64_t nbq = (nq + 31) / 32;
+  if (nbq > 4 || nQ * nbq < 2) {  // one query at a time
+    const int64_t qbytes = nq * M * dsub * 2;
+    for (int64_t q = 0; q < nQ; q++) {
+      rc = tms_pq_score((const uint8_t*)Qs + q * qbytes, nq, codebook, M, K, dsub, dtype, codes, B, nd, out + q * B,
+                        stream);
+      if (rc) return rc;
+    }
+    return TMS_OK;
+  }
+  return run_pq_batched(Qs, nQ, nq, codebook, M, K, dsub, dtype, codes, B, nd, out, st);
 }
 
 }  // extern "C"

@@ -12,11 +12,13 @@
 //  * scores are staged in registers (lane i holds document i of the wave's run) and
 //    stored once, coalesced, after the loop.
 // Every wave streams its own documents with the same (one or two) query blocks. Batched
-// queries use varlen_batched_kernel below, whose workgroups share tiles through LDS (for
+// queries use batched_tile_kernel below, whose workgroups share tiles through LDS (for
 // fixed-length documents at implicit offsets b * nd).
 //
 // Semantics as tms_dense.hip: fp32 accumulation, query rows past nq contribute 0, an
 // empty document scores -inf.
+#include <string.h>
+
 #include "tms_common.h"
 
 namespace tms {
@@ -234,23 +236,81 @@ static int stream_ks(const StreamArgs& a, int64_t grid, hipStream_t st) {
 // max takes two v_max3 per fragment and each document's reduction uses the row swaps and
 // DPP. pad_len > 0 gives the zero-padding semantics of tms_maxsim_varlen_padded; invalid
 // offsets score NaN.
-struct VarlenBatchedArgs {
-  const uint8_t* Q;        // (nQ * nq, d)
-  const uint8_t* D;        // (T, d)
-  const int64_t* offsets;  // (B + 1), or null: document b is rows [b * nd, (b + 1) * nd)
-  float* out;              // (nQ, B)
+struct BatchedArgs {
+  const uint8_t* Q;         // (nQ * nq, d)
+  const uint8_t* D;         // (T, d) tokens, or (T, M) PQ codes
+  const int64_t* offsets;   // (B + 1), or null: document b is rows [b * nd, (b + 1) * nd)
+  const uint8_t* codebook;  // PQ: (M, K, dsub) elements of the input dtype
+  float* out;               // (nQ, B)
   int64_t B, T, pad_len, nd;
-  int32_t nq, nbq, blk0, blk_end, nblk, d, docs_per_wg;
+  int32_t nq, nbq, blk0, blk_end, nblk, d, docs_per_wg, M, K;
 };
 
-template <int DT, int KS, int NB>
-__global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) varlen_batched_kernel(VarlenBatchedArgs a) {
+// Tile sources. A loading wave fetches, per tile, the raw data of its lane's 8-dimension
+// chunk c of token `row`; the source turns it into the MFMA A-operand fragment.
+struct DenseTiles {  // fp16 / bf16 rows, stored to the ring as loaded
+  static constexpr bool kDirect = true;
+  typedef u32x4 Raw;
+  __device__ static Raw load(const BatchedArgs& a, int64_t row, int c) {
+    return *(const u32x4*)(a.D + row * a.d * 2 + 16 * c);
+  }
+  __device__ static u32x4 decode(const u32x4*, int, Raw raw, int) { return raw; }
+};
+// uint8 PQ codes (M per token), decoded through the codebook held in LDS: chunk c covers
+// subspaces 8c / DSUB .. (8c + 7) / DSUB. Codes >= K are clamped into the table.
+template <int DSUB>
+struct PqTiles {
+  static constexpr bool kDirect = false;
+  typedef uint32_t Raw;
+  __device__ static Raw load(const BatchedArgs& a, int64_t row, int c) {
+    const uint8_t* p = a.D + row * a.M;
+    if constexpr (DSUB == 8) return p[c];
+    else if constexpr (DSUB == 4) return *(const uint16_t*)(p + 2 * c);
+    else if constexpr (DSUB == 2) return *(const uint32_t*)(p + 4 * c);
+    else return p[c / (DSUB / 8)];
+  }
+  __device__ static u32x4 decode(const u32x4* cb, int K, Raw raw, int c) {
+    auto code = [&](int i) -> uint32_t {
+      const uint32_t x = (raw >> (8 * i)) & 0xffu;
+      return x < (uint32_t)K ? x : (uint32_t)K - 1u;
+    };
+    if constexpr (DSUB >= 8) {
+      constexpr int P = DSUB / 8;  // 16-byte pieces per codeword
+      return cb[((int64_t)(c / P) * K + code(0)) * P + c % P];
+    } else if constexpr (DSUB == 4) {
+      const uint2* cb8 = (const uint2*)cb;
+      u32x4 v;
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const uint2 x = cb8[(int64_t)(2 * c + i) * K + code(i)];
+        v[2 * i] = x.x;
+        v[2 * i + 1] = x.y;
+      }
+      return v;
+    } else {
+      const uint32_t* cb4 = (const uint32_t*)cb;
+      u32x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = cb4[(int64_t)(4 * c + i) * K + code(i)];
+      return v;
+    }
+  }
+};
+
+template <int DT, int KS, int NB, class SRC>
+__global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel(BatchedArgs a) {
   constexpr int NS = 4;  // LDS ring slots and load lead, in tiles
   __shared__ u32x4 ring[NS][4][64];
+  extern __shared__ u32x4 cb[];  // PQ codebook
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g = lane >> 4;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const float NEG_INF = -__builtin_inff();
+  if constexpr (!SRC::kDirect) {  // codebook -> LDS (d * K elements, a multiple of 16 bytes)
+    const int n16 = a.d * a.K * 2 / 16;
+    for (int i = threadIdx.x; i < n16; i += 64 * TMS_BATCHED_WAVES) cb[i] = ((const u32x4*)a.codebook)[i];
+    __syncthreads();
+  }
 
   const int64_t b_begin = wave_uniform((int64_t)blockIdx.x * a.docs_per_wg);
   const int64_t b_end = (b_begin + a.docs_per_wg < a.B) ? b_begin + a.docs_per_wg : a.B;
@@ -342,14 +402,14 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) varlen_batched_kern
   auto pipeline = [&](auto ld_tag) {
     constexpr bool LD = decltype(ld_tag)::value == 1;
     wl = wc;
-    const uint8_t* dcol = a.D + 16 * (4 * (LD ? wid : 0) + g);
-    const int64_t row_bytes = (int64_t)a.d * 2;
-    auto load = [&]() -> u32x4 {
-      u32x4 v = {0u, 0u, 0u, 0u};
+    const int chunk = 4 * (LD ? wid : 0) + g;
+    typedef typename SRC::Raw Raw;
+    auto load = [&]() -> Raw {
+      Raw v{};
       if constexpr (LD) {
         int32_t t = wl.t0 + r;
         if (t > wl.len - 1) t = wl.len - 1;
-        v = *(const u32x4*)(dcol + (wl.base + t) * row_bytes);
+        v = SRC::load(a, wl.base + t, chunk);
       }
       advance(wl, false);
       return v;
@@ -359,10 +419,17 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) varlen_batched_kern
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
-    u32x4 stg[NS];
+    // Direct sources store tile i+1 from its load slot at step i; decoding sources decode
+    // tile i+2 at step i into `ahead` (the LDS gathers overlap the step) and store it a
+    // step later.
+    Raw stg[NS];
+    u32x4 ahead = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int t = 0; t < NS; t++) stg[t] = load();
-    if constexpr (LD) ring[0][wid][lane] = stg[0];
+    if constexpr (LD) {
+      ring[0][wid][lane] = SRC::decode(cb, a.K, stg[0], chunk);
+      if constexpr (!SRC::kDirect) ahead = SRC::decode(cb, a.K, stg[1], chunk);
+    }
     sync();
     u32x4 frag[2][KS];
 #pragma unroll
@@ -376,7 +443,14 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) varlen_batched_kern
       constexpr int s1 = (i + 1) % NS;
       constexpr int f = i & 1;
       stg[i] = load();  // tile i + NS (stg[i] was tile i, in the ring since the last step)
-      if constexpr (LD) ring[s1][wid][lane] = stg[s1];  // tile i+1
+      if constexpr (LD) {
+        if constexpr (SRC::kDirect) {
+          ring[s1][wid][lane] = stg[s1];  // tile i+1
+        } else {
+          ring[s1][wid][lane] = ahead;                               // tile i+1
+          ahead = SRC::decode(cb, a.K, stg[(i + 2) % NS], chunk);  // tile i+2
+        }
+      }
       sync();
 #pragma unroll
       for (int s = 0; s < KS; s++) frag[f ^ 1][s] = ring[s1][s][lane];
@@ -446,24 +520,52 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) varlen_batched_kern
   }
 }
 
-template <int DT, int NB>
-static int varlen_batched_ks(const VarlenBatchedArgs& a, int64_t grid, hipStream_t st) {
+template <int DT, int NB, class SRC>
+static int batched_ks(const BatchedArgs& a, int64_t grid, size_t lds, hipStream_t st) {
   const dim3 blk(64 * TMS_BATCHED_WAVES);
   switch (a.d / 32) {
-    case 1: hipLaunchKernelGGL((varlen_batched_kernel<DT, 1, NB>), dim3((unsigned)grid), blk, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((varlen_batched_kernel<DT, 2, NB>), dim3((unsigned)grid), blk, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((varlen_batched_kernel<DT, 3, NB>), dim3((unsigned)grid), blk, 0, st, a); break;
-    default: hipLaunchKernelGGL((varlen_batched_kernel<DT, 4, NB>), dim3((unsigned)grid), blk, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((batched_tile_kernel<DT, 1, NB, SRC>), dim3((unsigned)grid), blk, lds, st, a); break;
+    case 2: hipLaunchKernelGGL((batched_tile_kernel<DT, 2, NB, SRC>), dim3((unsigned)grid), blk, lds, st, a); break;
+    case 3: hipLaunchKernelGGL((batched_tile_kernel<DT, 3, NB, SRC>), dim3((unsigned)grid), blk, lds, st, a); break;
+    default: hipLaunchKernelGGL((batched_tile_kernel<DT, 4, NB, SRC>), dim3((unsigned)grid), blk, lds, st, a); break;
   }
-  return check_launch("varlen_batched_kernel");
+  return check_launch("batched_tile_kernel");
 }
-template <int DT>
-static int varlen_batched_nb(int nb, const VarlenBatchedArgs& a, int64_t grid, hipStream_t st) {
+template <int DT, class SRC>
+static int batched_nb(int nb, const BatchedArgs& a, int64_t grid, size_t lds, hipStream_t st) {
   switch (nb) {
-    case 1: return varlen_batched_ks<DT, 1>(a, grid, st);
-    case 2: return varlen_batched_ks<DT, 2>(a, grid, st);
-    default: return varlen_batched_ks<DT, kMaxBlocksPerWave>(a, grid, st);
+    case 1: return batched_ks<DT, 1, SRC>(a, grid, lds, st);
+    case 2: return batched_ks<DT, 2, SRC>(a, grid, lds, st);
+    default: return batched_ks<DT, kMaxBlocksPerWave, SRC>(a, grid, lds, st);
   }
+}
+template <class SRC>
+static int batched_dt(int dtype, int nb, const BatchedArgs& a, int64_t grid, size_t lds, hipStream_t st) {
+  return dtype == TMS_DTYPE_F16 ? batched_nb<TMS_DTYPE_F16, SRC>(nb, a, grid, lds, st)
+                                : batched_nb<TMS_DTYPE_BF16, SRC>(nb, a, grid, lds, st);
+}
+
+// Blocks per wave and launches over the query blocks, shared by the entry points below:
+// the smallest of 1, 2, 4 blocks per wave whose launch covers every block in one pass (a
+// wave computes all of its slots, used or not), else 4; a wave holds whole queries.
+template <class LAUNCH>
+static int batched_launches(BatchedArgs& a, int64_t nQ, LAUNCH launch) {
+  const int64_t nblocks = nQ * (int64_t)a.nbq;
+  int nb = kMaxBlocksPerWave;
+  for (int c = 1; c < kMaxBlocksPerWave; c *= 2)
+    if (c >= a.nbq && nblocks <= (int64_t)TMS_BATCHED_WAVES * ((c / a.nbq) * a.nbq)) {
+      nb = c;
+      break;
+    }
+  a.nblk = (nb / a.nbq) * a.nbq;
+  const int64_t per_launch = (int64_t)TMS_BATCHED_WAVES * a.nblk;
+  for (int64_t b0 = 0; b0 < nblocks; b0 += per_launch) {
+    a.blk0 = (int32_t)b0;
+    a.blk_end = (int32_t)(nblocks - b0 < per_launch ? nblocks : b0 + per_launch);
+    const int rc = launch(nb);
+    if (rc) return rc;
+  }
+  return TMS_OK;
 }
 
 #ifndef TMS_VARLEN_BATCHED_TOKENS
@@ -475,7 +577,8 @@ static int varlen_batched_nb(int nb, const VarlenBatchedArgs& a, int64_t grid, h
 int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t T,
                        const int64_t* offsets, int64_t nd, int64_t B, int64_t pad_len, int dtype, float* out,
                        hipStream_t st) {
-  VarlenBatchedArgs a;
+  BatchedArgs a;
+  memset(&a, 0, sizeof(a));
   a.Q = (const uint8_t*)Q;
   a.D = (const uint8_t*)D;
   a.offsets = offsets;
@@ -487,16 +590,6 @@ int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const v
   a.nq = (int32_t)nq;
   a.nbq = (int32_t)((nq + 31) / 32);
   a.d = (int32_t)d;
-  const int64_t nblocks = nQ * (int64_t)a.nbq;
-  // Blocks per wave: the smallest of 1, 2, 4 whose launch covers every block in one pass
-  // (a wave computes all of its slots, used or not), else 4. A wave holds whole queries.
-  int nb = kMaxBlocksPerWave;
-  for (int c = 1; c < kMaxBlocksPerWave; c *= 2)
-    if (c >= a.nbq && nblocks <= (int64_t)TMS_BATCHED_WAVES * ((c / a.nbq) * a.nbq)) {
-      nb = c;
-      break;
-    }
-  a.nblk = (nb / a.nbq) * a.nbq;
   const int64_t hint = B > 0 ? T / B : 1;
   int64_t dpw = hint > 0 ? TMS_VARLEN_BATCHED_TOKENS / hint : 64;
   if (dpw > 1 && B / dpw < (int64_t)256 * 4) dpw = B / ((int64_t)256 * 4);
@@ -504,16 +597,42 @@ int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const v
   if (dpw > 64) dpw = 64;
   a.docs_per_wg = (int32_t)dpw;
   const int64_t grid = (B + dpw - 1) / dpw;
-  if (grid > 0x7fffffff) return fail(TMS_ERR_UNSUPPORTED, "varlen batched: too many documents");
-  const int64_t per_launch = (int64_t)TMS_BATCHED_WAVES * a.nblk;
-  for (int64_t b0 = 0; b0 < nblocks; b0 += per_launch) {
-    a.blk0 = (int32_t)b0;
-    a.blk_end = (int32_t)(nblocks - b0 < per_launch ? nblocks : b0 + per_launch);
-    const int rc = dtype == TMS_DTYPE_F16 ? varlen_batched_nb<TMS_DTYPE_F16>(nb, a, grid, st)
-                                          : varlen_batched_nb<TMS_DTYPE_BF16>(nb, a, grid, st);
-    if (rc) return rc;
-  }
-  return TMS_OK;
+  if (grid > 0x7fffffff) return fail(TMS_ERR_UNSUPPORTED, "batched MaxSim: too many documents");
+  return batched_launches(a, nQ, [&](int nb) { return batched_dt<DenseTiles>(dtype, nb, a, grid, 0, st); });
+}
+
+// PQ batched entry (tms_pq.hip): fixed-length documents of uint8 codes, the codebook
+// (d * K elements, at most 64 KiB) copied to LDS by each workgroup, which walks 64
+// documents. Shapes as the single-query MFMA PQ kernel's.
+int run_pq_batched(const void* Q, int64_t nQ, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub,
+                   int dtype, const uint8_t* codes, int64_t B, int64_t nd, float* out, hipStream_t st) {
+  BatchedArgs a;
+  memset(&a, 0, sizeof(a));
+  a.Q = (const uint8_t*)Q;
+  a.D = codes;
+  a.codebook = (const uint8_t*)codebook;
+  a.out = out;
+  a.B = B;
+  a.T = B * nd;
+  a.nd = nd;
+  a.nq = (int32_t)nq;
+  a.nbq = (int32_t)((nq + 31) / 32);
+  a.d = (int32_t)(M * dsub);
+  a.M = (int32_t)M;
+  a.K = (int32_t)K;
+  a.docs_per_wg = 64;  // the most a workgroup's lanes hold; amortises the codebook copy
+  const int64_t grid = (B + 63) / 64;
+  if (grid > 0x7fffffff) return fail(TMS_ERR_UNSUPPORTED, "batched PQ: too many documents");
+  const size_t lds = (size_t)a.d * K * 2;
+  return batched_launches(a, nQ, [&](int nb) {
+    switch (dsub) {
+      case 2: return batched_dt<PqTiles<2>>(dtype, nb, a, grid, lds, st);
+      case 4: return batched_dt<PqTiles<4>>(dtype, nb, a, grid, lds, st);
+      case 8: return batched_dt<PqTiles<8>>(dtype, nb, a, grid, lds, st);
+      case 16: return batched_dt<PqTiles<16>>(dtype, nb, a, grid, lds, st);
+      default: return batched_dt<PqTiles<32>>(dtype, nb, a, grid, lds, st);
+    }
+  });
 }
 
 // Entry used by tms_dense.hip for fixed-length documents with d in {32, 64, 96, 128},

@@ -119,6 +119,43 @@ class TileMaxSimPQ:
                                                 scores.data_ptr(), stream))
         return scores
 
+    def score_batch_queries(self, Qs: torch.Tensor, codes: torch.Tensor, validate: bool = True) -> torch.Tensor:
+        """Score ``nQ`` queries against the same PQ codes: ``Qs`` (nQ, Nq, d) -> (nQ, B).
+
+        Equivalent to stacking :meth:`score_batch` over the queries. On the MFMA shapes
+        each 16-token tile of codes is decoded once per pass through the codebook in LDS
+        and shared by up to 32 query blocks of 32 tokens (``tms_pq_score_batched``);
+        other shapes score query by query. No reference counterpart.
+        """
+        _check.tensor("Qs", Qs)
+        _check.tensor("codes", codes)
+        if Qs.dim() != 3:
+            raise ValueError(f"Qs must be (nQ, Nq, d), got shape {tuple(Qs.shape)}")
+        if codes.dim() != 3:
+            raise ValueError(f"codes must be (B, Nd, M), got shape {tuple(codes.shape)}")
+        B, Nd, M = codes.shape
+        assert M == self.M, f"codes have M={M} subspaces, codebook has {self.M}"
+        assert Qs.shape[2] == self.d, f"Q width {Qs.shape[2]} != M*dsub = {self.d}"
+        _check.on_gpu("Qs", Qs)
+        _check.same_device(Qs=Qs, codebook=self.codebook)
+        Qs = _check.query_like(Qs, self.codebook.dtype)
+        codes = self._codes(codes, validate)
+        nQ, Nq = Qs.shape[0], Qs.shape[1]
+        scores = torch.empty(nQ, B, dtype=torch.float32, device=Qs.device)
+        if B == 0 or nQ == 0:
+            return scores
+        aligned = all(t.data_ptr() % 16 == 0 for t in (Qs, self.codebook, codes))
+        if not (_mfma_shape_ok(self.M, self.K, self.dsub) and aligned):
+            for q in range(nQ):
+                scores[q] = self.score_batch(Qs[q], codes, validate=False)
+            return scores
+        lib = _lib.load()
+        with torch.cuda.device(Qs.device):
+            _lib.check(lib.tms_pq_score_batched(Qs.data_ptr(), nQ, Nq, self.codebook.data_ptr(), self.M, self.K,
+                                                self.dsub, _lib.dtype_code(self.codebook.dtype), codes.data_ptr(), B,
+                                                Nd, scores.data_ptr(), _lib.stream_of(Qs)))
+        return scores
+
     def score_single(self, Q: torch.Tensor, codes: torch.Tensor, method: str = "auto") -> torch.Tensor:
         """Score one PQ-compressed document (``src/flash_pqsim_kernel.py:254-280``).
 
