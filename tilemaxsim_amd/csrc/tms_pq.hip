@@ -185,8 +185,8 @@ __global__ void __launch_bounds__(kPqThreads) pq_mfma_score_kernel(PqArgs a) {
     }
   __syncthreads();
 
-  const int64_t wave = (int64_t)blockIdx.x * (kPqThreads / 64) + (threadIdx.x >> 6);
-  const int64_t b_begin = wave * a.docs_per_wave;
+  const int64_t wave = (int64_t)blockIdx.x * (kPqThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b_begin = wave_uniform(wave * a.docs_per_wave);
   if (b_begin >= a.B) return;
   const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
   const float NEG_INF = -__builtin_inff();
@@ -202,6 +202,9 @@ __global__ void __launch_bounds__(kPqThreads) pq_mfma_score_kernel(PqArgs a) {
       *o = (a.blk0 > 0) ? (*o + s_total) : s_total;
     }
   };
+  // Max over the document's tokens (the 4 accumulator rows of a lane, then the four
+  // 16-lane row groups) and sum over the query tokens (the 16 columns of a row). The
+  // cross-lane steps use row swaps and DPP, which leave the LDS to the gathers.
   auto finish_doc = [&](int64_t b) {
     float s = 0.f;
 #pragma unroll
@@ -209,30 +212,30 @@ __global__ void __launch_bounds__(kPqThreads) pq_mfma_score_kernel(PqArgs a) {
 #pragma unroll
       for (int h = 0; h < 2; h++) {
         float m = fmaxf(fmaxf(rmax[j][h][0], rmax[j][h][1]), fmaxf(rmax[j][h][2], rmax[j][h][3]));
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
+        m = cross_row_max(m);
         bool valid;
         (void)q_row(j, h, r, valid);
         s += valid ? m : 0.f;
         rmax[j][h] = f32x4{NEG_INF, NEG_INF, NEG_INF, NEG_INF};
       }
-    s += __shfl_xor(s, 8);
-    s += __shfl_xor(s, 4);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 1);
-    write_doc(b, s);
+    write_doc(b, row_sum16(s));
   };
 
   // Code words of this lane for UT subtiles of 16 tokens starting at token t0 of doc b.
   struct Codes {
     uint32_t w[UT][CW];
   };
+  // b and t0 are wave-uniform, so the unit's base address is scalar; each lane adds a
+  // 32-bit offset (the host guarantees nd * M < 2^31). Tokens past the document's end
+  // are clamped to its last token.
   auto load_codes = [&](Codes& c, int64_t b, int64_t t0) {
+    const uint8_t* base = a.codes + (b * nd + t0) * M;
+    const int64_t left = nd - 1 - t0;
+    const int last = left < 16 * UT ? (int)left : 16 * UT - 1;
 #pragma unroll
     for (int u = 0; u < UT; u++) {
-      int64_t t = t0 + 16 * u + r;
-      if (t > nd - 1) t = nd - 1;
-      const uint8_t* p = a.codes + (b * nd + t) * M + g * CB;
+      const int tr = min(16 * u + r, last);
+      const uint8_t* p = base + (uint32_t)(tr * M + g * CB);
       if constexpr (CB == 4) {
         c.w[u][0] = *(const uint32_t*)p;
       } else if constexpr (CB == 8) {
@@ -460,10 +463,12 @@ static int launch_mfma_dsub(const PqArgs& a, int dsub, int ks, int64_t grid, siz
 }
 
 // The fast kernel needs: d = M*dsub in {32, 64, 96, 128}, dsub in {2, 4, 8, 16, 32}
-// with M a multiple of 4, K <= 256, a codebook that fits 64 KiB of LDS, and
-// 16-byte aligned Q / codebook / code rows.
-static bool mfma_supported(const void* Q, const void* C, const uint8_t* codes, int64_t M, int64_t K, int64_t dsub) {
+// with M a multiple of 4, K <= 256, a codebook that fits 64 KiB of LDS, 16-byte
+// aligned Q / codebook / code rows, and fewer than 2^31 code bytes per document.
+static bool mfma_supported(const void* Q, const void* C, const uint8_t* codes, int64_t M, int64_t K, int64_t dsub,
+                           int64_t nd) {
   const int64_t d = M * dsub;
+  if (nd * M >= ((int64_t)1 << 31)) return false;  // a document's code bytes are addressed with 32-bit offsets
   if (!(dsub == 2 || dsub == 4 || dsub == 8 || dsub == 16 || dsub == 32)) return false;
   if (d % 32 != 0 || d > 128 || d == 0 || M % 4 != 0) return false;
   if (K > 256 || K < 1 || d * K * 2 > 64 * 1024) return false;
@@ -547,7 +552,7 @@ int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int
   hipStream_t st = (hipStream_t)stream;
   // no query tokens: 0; no document tokens: -inf (the running max never moves)
   if (nq == 0 || nd == 0) return fill_scores(out, B, nq == 0 ? 0.f : -__builtin_inff(), st);
-  if (mfma_supported(Q, codebook, codes, M, K, dsub)) {
+  if (mfma_supported(Q, codebook, codes, M, K, dsub, nd)) {
     PqArgs a;
     memset(&a, 0, sizeof(a));
     a.Q = (const uint8_t*)Q;
@@ -606,7 +611,7 @@ int tms_pq_score_batched(const void* Qs, int64_t nQ, int64_t nq, const void* cod
   if (nq > ((int64_t)1 << 24) || nQ > ((int64_t)1 << 20)) return fail(TMS_ERR_UNSUPPORTED, "%s: too many queries", fn);
   hipStream_t st = (hipStream_t)stream;
   if (nq == 0 || nd == 0) return fill_scores(out, nQ * B, nq == 0 ? 0.f : -__builtin_inff(), st);
-  if (!mfma_supported(Qs, codebook, codes, M, K, dsub))
+  if (!mfma_supported(Qs, codebook, codes, M, K, dsub, nd))
     return fail(TMS_ERR_UNSUPPORTED,
                 "%s: shape M=%lld K=%lld dsub=%lld (or alignment) not supported by the MFMA kernels; score per "
                 "query with tms_pq_build_lut + tms_pq_score_lut",

@@ -105,7 +105,9 @@ class TileMaxSimPQ:
         if method not in ("auto", "mfma", "lut"):
             raise ValueError(f"method must be 'auto', 'mfma' or 'lut', got {method!r}")
         aligned = all(t.data_ptr() % 16 == 0 for t in (Q, self.codebook, codes))
-        use_mfma = method == "mfma" or (method == "auto" and _mfma_shape_ok(self.M, self.K, self.dsub) and aligned)
+        small_docs = Nd * M < 2**31  # the MFMA kernel addresses a document's codes with 32-bit offsets
+        use_mfma = method == "mfma" or (method == "auto" and _mfma_shape_ok(self.M, self.K, self.dsub) and aligned
+                                        and small_docs)
         lib = _lib.load()
         with torch.cuda.device(Q.device):
             stream = _lib.stream_of(Q)
@@ -145,7 +147,7 @@ class TileMaxSimPQ:
         if B == 0 or nQ == 0:
             return scores
         aligned = all(t.data_ptr() % 16 == 0 for t in (Qs, self.codebook, codes))
-        if not (_mfma_shape_ok(self.M, self.K, self.dsub) and aligned):
+        if not (_mfma_shape_ok(self.M, self.K, self.dsub) and aligned and Nd * M < 2**31):
             for q in range(nQ):
                 scores[q] = self.score_batch(Qs[q], codes, validate=False)
             return scores
