@@ -26,6 +26,28 @@ def test_topk_matches_oracle(cuda, n, k):
     _check_row(v.cpu().numpy(), i.cpu().numpy(), x, k)
 
 
+@pytest.mark.parametrize("dist", ["pq_scores", "clustered", "negative", "tiny_spread", "mixed_sign"])
+def test_topk_concentrated_values(cuda, dist):
+    """Rows whose keys share many leading bits (one query's MaxSim scores do): the
+    selection skips the shared digits, which must not change the result. The last chunk
+    of each row holds fewer than k keys in some rows, where nothing is skipped."""
+    import torch
+    from tilemaxsim_amd import topk
+    rng = np.random.default_rng(11)
+    n = 4096 * 7 + 37
+    base = {"pq_scores": 83.0 + 2.0 * rng.standard_normal((3, n)),
+            "clustered": 10.0 + 1e-3 * rng.random((3, n)),
+            "negative": -50.0 - rng.random((3, n)),
+            "tiny_spread": 1.0 + 1e-6 * rng.integers(0, 4, size=(3, n)),  # few distinct values: ties by index
+            "mixed_sign": 1e-3 * rng.standard_normal((3, n))}[dist]
+    rows = base.astype(np.float32)
+    for k in (1, 100, 1024):
+        v, i = topk(torch.from_numpy(rows).cuda(), k)
+        v, i = v.cpu().numpy(), i.cpu().numpy()
+        for r in range(3):
+            _check_row(v[r], i[r], rows[r], k)
+
+
 def test_topk_rows_ties_nan_inf(cuda):
     import torch
     from tilemaxsim_amd import topk
