@@ -87,6 +87,34 @@ def test_fused_maxsim_matches_oracle(cuda, nbits, d, nq, padding):
     _assert_scores(got, ref, f"nbits={nbits} d={d} nq={nq} {padding}")
 
 
+@pytest.mark.parametrize("nbits,d", [(1, 128), (2, 128), (4, 128), (2, 64), (4, 64), (1, 32), (2, 96)])
+def test_fused_residual_offsets_alignment(cuda, nbits, d):
+    """A residuals view that starts nbits bytes into its buffer is aligned for one chunk
+    but not for a lane's whole run of chunks, so the fused kernel reads it chunk by chunk;
+    the aligned tensor takes one load per token. Both read the same bytes: bit-identical
+    scores, and both within tolerance of the oracle."""
+    import torch
+    from tilemaxsim_amd import flashmaxsim_score_residual
+    rng = np.random.default_rng(7 * nbits + d)
+    lens = rng.integers(0, 120, 300)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(offsets[-1])
+    C, codes, res, w = _index(rng, T, d, nbits, 129)
+    Q = rng.standard_normal((32, d)).astype(np.float32)
+    Q /= np.linalg.norm(Q, axis=1, keepdims=True)
+    Q = Q.astype(np.float16)
+    rb = res.shape[1]
+    buf = torch.zeros(T * rb + nbits, dtype=torch.uint8, device="cuda")
+    buf[nbits:] = _gpu(res.reshape(-1))
+    shifted = buf[nbits:].view(T, rb)
+    assert shifted.data_ptr() % nbits == 0 and shifted.data_ptr() % (2 * nbits) != 0
+    args = (_gpu(C), _gpu(w), nbits, _gpu(offsets))
+    got_a = flashmaxsim_score_residual(_gpu(Q), _gpu(codes), _gpu(res), *args, padding="mask").cpu().numpy()
+    got_s = flashmaxsim_score_residual(_gpu(Q), _gpu(codes), shifted, *args, padding="mask").cpu().numpy()
+    assert np.array_equal(got_a, got_s, equal_nan=True)
+    _assert_scores(got_a, ro.maxsim_residual(Q, codes, res, C, w, nbits, offsets), f"nbits={nbits} d={d}")
+
+
 def test_fused_candidates_match_packed_scoring(cuda):
     """PLAID's flow: pick candidate pids, decompress their tokens, score them packed.
     The fused kernel must give the same scores without the decompressed copy."""

@@ -83,6 +83,56 @@ __device__ __forceinline__ uint32_t load_res(const uint8_t* row, int chunk) {
   else return *(const uint32_t*)(row + 4 * chunk);
 }
 
+// The residual bytes of chunks c0 .. c0+KS-1 of one token (NBITS bytes per chunk, KS*NBITS
+// contiguous bytes), one u32 per chunk as load_res returns it. WIDE: one load of the whole
+// run, which needs KS*NBITS to be 1, 2, 4, 8 or 16 and the run aligned to its size (the
+// host checks the pointer; rows are 4*KS*NBITS bytes, so every run is then aligned).
+template <int NBITS, int KS, bool WIDE>
+__device__ __forceinline__ void load_res_run(const uint8_t* row, int c0, uint32_t (&rr)[KS]) {
+  constexpr int TB = NBITS * KS;
+  if constexpr (WIDE) {
+    const uint8_t* p = row + TB * (c0 / KS);
+    if constexpr (TB == 16) {
+      const uint4 v = *(const uint4*)p;
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int s = 0; s < KS; s++) rr[s] = w[s];  // NBITS = 4, KS = 4
+    } else if constexpr (TB == 8) {
+      const uint2 v = *(const uint2*)p;
+      const uint64_t x = ((uint64_t)v.y << 32) | v.x;
+#pragma unroll
+      for (int s = 0; s < KS; s++) rr[s] = (uint32_t)(x >> (8 * NBITS * s)) & (uint32_t)((1ull << (8 * NBITS)) - 1);
+    } else if constexpr (TB == 4) {
+      const uint32_t x = *(const uint32_t*)p;
+      if constexpr (NBITS == 4) {
+        rr[0] = x;  // KS = 1
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; s++) rr[s] = (x >> (8 * NBITS * s)) & ((1u << (8 * NBITS)) - 1u);
+      }
+    } else if constexpr (TB == 2) {
+      const uint32_t x = *(const uint16_t*)p;
+      if constexpr (NBITS == 2) {
+        rr[0] = x;  // KS = 1
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; s++) rr[s] = (x >> (8 * s)) & 0xffu;
+      }
+    } else {
+      static_assert(TB == 1, "WIDE needs a power-of-two run of at most 16 bytes");
+      rr[0] = *p;
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < KS; s++) rr[s] = load_res<NBITS>(row, c0 + s);
+  }
+}
+template <int NBITS, int KS>
+constexpr bool res_run_pow2() {
+  constexpr int TB = NBITS * KS;
+  return TB == 1 || TB == 2 || TB == 4 || TB == 8 || TB == 16;
+}
+
 // fp16 weights of the chunk's 8 dimensions from the LDS table.
 template <int NBITS>
 __device__ __forceinline__ u32x4 chunk_weights(const uint8_t* lut, uint32_t rw) {
@@ -122,26 +172,34 @@ template <int K>
 struct RingSlot {
   static constexpr int value = K;
 };
+#ifndef TMS_RES1_RING
+#define TMS_RES1_RING 3  // ring slots of the single-query fused kernel (3..8)
+#endif
+static_assert(TMS_RES1_RING >= 3 && TMS_RES1_RING <= 8, "the fused kernel's step loop is unrolled up to 8 times");
 
 // ---------------------------------------------------------------------------------
 // Fused MaxSim. One wave streams whole documents; a tile is 16 * NSUB tokens x d.
-// Centroid ids are read three tiles ahead and the centroid chunks and residual bytes
-// two tiles ahead of the tile being decoded and scored.
+// With a ring of NS tiles, centroid ids are read NS tiles ahead and the centroid chunks
+// and residual bytes NS - 1 tiles ahead of the tile being decoded and scored.
 // QLDS: the query fragments sit in LDS (shared by the workgroup's four waves) instead of
 // 8 * KS VGPRs per lane, which buys occupancy.
-template <int KS, int NBITS, int NSUB, bool QLDS>
+// Lane (r, g) owns chunks KS*g .. KS*g + KS-1 of token r, contiguous dimensions, so its
+// residual bytes are one contiguous run: with WIDE they arrive in one load per token
+// instead of one per chunk. Each vector-memory instruction costs about as much as a
+// centroid gather, so this is what the gather rate depends on.
+template <int KS, int NBITS, int NSUB, bool QLDS, bool WIDE>
 __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
   constexpr int TT = 16 * NSUB;
   __shared__ __attribute__((aligned(16))) uint8_t lut[4096];
   __shared__ u32x4 qsh[QLDS ? KS * 2 * 64 : 1];
   build_lut<NBITS>(lut, a.weights);
   if constexpr (QLDS) {
-    // fragment (s, h) of lane l: query token 32 blk0 + 16 h + l % 16, chunk 4 s + l / 16
+    // fragment (s, h) of lane l: query token 32 blk0 + 16 h + l % 16, chunk KS (l / 16) + s
     for (int f = threadIdx.x; f < KS * 2 * 64; f += kThreads) {
       const int l = f & 63, h = (f >> 6) & 1, s = f >> 7;
       const int tok = a.blk0 * 32 + 16 * h + (l & 15);
       const int64_t row = tok < a.nq ? tok : a.nq - 1;
-      const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + (l >> 4))) * 2);
+      const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (KS * (l >> 4) + s)) * 2);
       qsh[f] = tok < a.nq ? v : u32x4{0u, 0u, 0u, 0u};
     }
   }
@@ -167,7 +225,7 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
       const int64_t row = qvalid[h] ? tok : a.nq - 1;  // loaded unconditionally, zeroed below
 #pragma unroll
       for (int s = 0; s < KS; s++) {
-        const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2);
+        const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (KS * g + s)) * 2);
         qf[s][h] = qvalid[h] ? v : u32x4{0u, 0u, 0u, 0u};
       }
     }
@@ -267,10 +325,8 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
       const uint8_t* crow = a.centroids + code * a.d * 2;
       const uint8_t* rrow = a.residuals + row_of(c, sub) * a.rb;
 #pragma unroll
-      for (int s = 0; s < KS; s++) {
-        bd.cen[sub][s] = *(const u32x4*)(crow + 16 * (4 * s + g));
-        bd.res[sub][s] = load_res<NBITS>(rrow, 4 * s + g);
-      }
+      for (int s = 0; s < KS; s++) bd.cen[sub][s] = *(const u32x4*)(crow + 16 * (KS * g + s));
+      load_res_run<NBITS, KS, WIDE>(rrow, KS * g, bd.res[sub]);
     }
   };
 
@@ -319,40 +375,58 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
     if (c.t0 + TT >= c.len) finish(c.b, c.len);
   };
 
-  // A ring of three tiles. While tile i is scored, the bodies of tiles i+1 and i+2 and
-  // the ids of tile i+3 are in flight. Each step issues the ids of tile i+3 before the
-  // body of tile i+2, so waiting for the ids of tile i+2 (issued a step earlier, before
-  // the body of tile i+1) never waits for the later loads. One cursor walks ahead (and
-  // scores empty documents as it passes them); the ring keeps its positions. The step
-  // is unrolled three times, so every ring slot is a compile-time register.
-  Body bd[3];
-  int32_t ids[3][NSUB];
-  Cur cr[3];
+  // A ring of NS tiles. While tile i is scored, the bodies of tiles i+1 .. i+NS-1 and
+  // the ids of tile i+NS are in flight. Each step issues the ids of tile i+NS before
+  // the body of tile i+NS-1, so waiting for the ids of tile i+NS-1 (issued a step
+  // earlier, before the body of tile i+NS-2) never waits for the later loads. One
+  // cursor walks ahead (and scores empty documents as it passes them); the ring keeps
+  // its positions. The step is unrolled NS times, so every ring slot is a compile-time
+  // register.
+  constexpr int NS = TMS_RES1_RING;
+  Body bd[NS];
+  int32_t ids[NS][NSUB];
+  Cur cr[NS];
   Cur walk;
   seek(walk, b_begin);
   if (walk.b >= b_end) return;
 #pragma unroll
-  for (int k = 0; k < 3; k++) {
+  for (int k = 0; k < NS; k++) {
     cr[k] = walk;
     load_codes(ids[k], walk);
     advance(walk);
   }
-  load_body(ids[0], cr[0], bd[0]);
-  load_body(ids[1], cr[1], bd[1]);
+#pragma unroll
+  for (int k = 0; k < NS - 1; k++) load_body(ids[k], cr[k], bd[k]);
   auto step = [&](auto slot) -> bool {
-    constexpr int k = decltype(slot)::value;  // tile i sits in ring slot k
+    constexpr int k = decltype(slot)::value % NS;  // tile i sits in ring slot k
+    constexpr int kb = (k + NS - 1) % NS;          // the slot tile i-1 left: tile i+NS-1
     const Cur c = cr[k];
-    cr[k] = walk;                                            // tile i+3
+    cr[k] = walk;                                  // tile i+NS
     advance(walk);
     load_codes(ids[k], cr[k]);
-    load_body(ids[(k + 2) % 3], cr[(k + 2) % 3], bd[(k + 2) % 3]);  // tile i+2
-    compute(c, bd[k]);                                       // tile i
-    return cr[(k + 1) % 3].b >= b_end;                       // tile i+1 exists?
+    load_body(ids[kb], cr[kb], bd[kb]);            // tile i+NS-1
+    compute(c, bd[k]);                             // tile i
+    return cr[(k + 1) % NS].b >= b_end;            // tile i+1 exists?
   };
   while (true) {
     if (step(RingSlot<0>{})) return;
     if (step(RingSlot<1>{})) return;
     if (step(RingSlot<2>{})) return;
+    if constexpr (NS > 3) {
+      if (step(RingSlot<3>{})) return;
+    }
+    if constexpr (NS > 4) {
+      if (step(RingSlot<4>{})) return;
+    }
+    if constexpr (NS > 5) {
+      if (step(RingSlot<5>{})) return;
+    }
+    if constexpr (NS > 6) {
+      if (step(RingSlot<6>{})) return;
+    }
+    if constexpr (NS > 7) {
+      if (step(RingSlot<7>{})) return;
+    }
   }
 }
 
@@ -724,13 +798,26 @@ static int check_format(const char* fn, int64_t d, int nbits, int64_t ncent, con
 #ifndef TMS_RES_BATCHED_TOKENS
 #define TMS_RES_BATCHED_TOKENS 4096  // document tokens one batched workgroup walks (whole documents)
 #endif
-template <int KS>
-static int launch_fused_ks(const ResArgs& a, int nbits, int64_t grid, hipStream_t st) {
+// One residual load per token when the lane's run of KS*nbits bytes is a power of two and
+// the residuals pointer is aligned to it (rows are 4*KS*nbits bytes, so every run is).
+template <int KS, int NBITS>
+static void launch_fused_nbits(const ResArgs& a, int64_t grid, hipStream_t st) {
   constexpr int kNSub = 1;
   constexpr bool kQlds = TMS_RES_QLDS;
-  if (nbits == 1) hipLaunchKernelGGL((residual_maxsim_kernel<KS, 1, kNSub, kQlds>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  else if (nbits == 2) hipLaunchKernelGGL((residual_maxsim_kernel<KS, 2, kNSub, kQlds>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((residual_maxsim_kernel<KS, 4, kNSub, kQlds>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  constexpr int TB = NBITS * KS;
+  if constexpr (res_run_pow2<NBITS, KS>()) {
+    if (((uintptr_t)a.residuals % TB) == 0) {
+      hipLaunchKernelGGL((residual_maxsim_kernel<KS, NBITS, kNSub, kQlds, true>), dim3((unsigned)grid), dim3(256), 0, st, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((residual_maxsim_kernel<KS, NBITS, kNSub, kQlds, false>), dim3((unsigned)grid), dim3(256), 0, st, a);
+}
+template <int KS>
+static int launch_fused_ks(const ResArgs& a, int nbits, int64_t grid, hipStream_t st) {
+  if (nbits == 1) launch_fused_nbits<KS, 1>(a, grid, st);
+  else if (nbits == 2) launch_fused_nbits<KS, 2>(a, grid, st);
+  else launch_fused_nbits<KS, 4>(a, grid, st);
   return check_launch("residual_maxsim_kernel");
 }
 
