@@ -120,7 +120,10 @@ int tms_pq_score_lut(const float* lut, int64_t nq, int64_t M, int64_t K, const u
  * PQ MaxSim by codebook gather: each document token is rebuilt from the codebook in
  * registers (never in HBM) and scored on MFMA; same scores as tms_pq_score_lut up to
  * fp32 summation order. Replaces TileMaxSimPQ.score_batch (src/flash_pqsim_kernel.py:
- * 213-252) as a whole.
+ * 213-252) as a whole. Shapes: d = M * dsub in {32, 64, 96, 128}, dsub in {2, 4, 8, 16,
+ * 32}, M a multiple of 4, K <= 256, a codebook of at most 64 KiB, 16-byte aligned Q,
+ * codebook and codes, and nd * M < 2^31; other shapes return TMS_ERR_UNSUPPORTED (score
+ * them with tms_pq_build_lut + tms_pq_score_lut).
  */
 int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
                  const uint8_t* codes, int64_t B, int64_t nd, float* out, void* stream);
