@@ -241,3 +241,14 @@ def test_product_never_imports_the_oracle():
                 text = open(os.path.join(root, f)).read()
                 assert not re.search(r"^\s*(import|from)\s+oracle\b", text, flags=re.M), f
                 assert "maxsim_oracle" not in text and "c_oracle" not in text, f
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with status 2 and says why, before
+    importing torch or touching a device."""
+    import subprocess
+    import sys
+    res = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"], capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode == 2, (res.returncode, res.stderr)
+    assert "one GPU" in res.stderr and res.stdout == ""
