@@ -1,6 +1,6 @@
 """Benchmark of the fused MaxSim scoring path on one MI355X.
 
-Default workload (the one the headline metric is quoted on):
+Default workload (C2, the configuration the headline metric is quoted on):
 64 queries x 1,000,000 documents, Nq = 32, Nd = 180, d = 128, fp16 L2-normalised
 Gaussian embeddings (~46 GB resident in HBM). One step scores every query against
 every document with ``flash_maxsim_v2_multiquery`` (one HBM pass over the corpus per

@@ -1,6 +1,6 @@
 """GPU parity of the dense / masked / variable-length MaxSim kernels against the CPU oracle.
 
-Bar (BASELINE north star): |score - oracle| <= 1e-3 relative (fp32 accumulation), and
+Bar: |score - oracle| <= 1e-3 relative (fp32 accumulation), and
 identical top-100 rankings except for swaps among scores within that tolerance.
 The oracle is the float64 restatement of ``pytorch_maxsim_naive``
 (``src/flash_maxsim_kernel.py:280-288``) on the same fp16/bf16 input values.
@@ -136,7 +136,7 @@ def test_bf16_and_fp32_query(cuda):
 
 
 def test_c1_ranking_parity(cuda):
-    """1 query x 1000 docs x Nd=128, d=128, L2-normalised fp16.
+    """Workload C1, the CPU-runnable case: 1 query x 1000 docs x Nd=128, d=128, L2-normalised fp16.
     Top-100 must match the oracle except swaps among scores within tolerance."""
     from tilemaxsim_amd import flash_maxsim_v2_multiquery
     rng = _rng(0)

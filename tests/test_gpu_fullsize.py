@@ -1,4 +1,4 @@
-"""Parity at BASELINE's full sizes (C2-C5 with c2b/c3b, c6/c6b, top-k over C2's score matrix).
+"""Parity at the benchmark workloads' full sizes (C2-C5 with c2b/c3b, c6/c6b, top-k over C2's score matrix).
 
 Each test builds one configuration at its benchmark size on the GPU, scores it through
 the public entry points, and checks a seeded sample of documents, always including the

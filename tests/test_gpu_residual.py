@@ -3,8 +3,8 @@
 * tms_residual_decompress: fp16 outputs equal to the oracle's restatement of the codec
   (same half add, fp32 norm, fp32 division) up to 1 fp16 ulp; only the fp32 summation
   order of the norm differs, and it can move a rounding boundary;
-* tms_maxsim_residual: |score - oracle| <= 1e-3 relative + 1e-3 absolute, the BASELINE
-  bar; the oracle scores the decompressed fp16 tokens in float64.
+* tms_maxsim_residual: |score - oracle| <= 1e-3 relative + 1e-3 absolute, the scoring
+  bar of every path; the oracle scores the decompressed fp16 tokens in float64.
 """
 import numpy as np
 import pytest
