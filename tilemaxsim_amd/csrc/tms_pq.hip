@@ -73,44 +73,79 @@ struct LutArgs {
   int32_t docs_per_wave;  // <= 64
 };
 
-// LDS slice layout: [m][k][QG] fp32 for query tokens q0 .. q0+QG-1 (zero past nq).
-template <int QG>
-__global__ void __launch_bounds__(256) pq_lut_score_kernel(LutArgs a) {
-  extern __shared__ float lds[];
+// One lane per document token; a workgroup of 16 waves shares one slice of the table in
+// LDS: QG query tokens, [m][k][QG] fp32 (zero past nq), at most 128 KiB. Each lane loads
+// its token's M code bytes with one or a few wide loads, gathers its M rows of QG values
+// and adds them in ascending m, as the reference sums them (:154-167), then keeps a
+// running max per query token. A document's maxima are taken across the wave with DPP and
+// row swaps, and its partial score (the slice's query tokens) accumulates in lane
+// b - b_begin. Slices loop inside the kernel, so the codes are read once per slice.
+// CW: 4 = M is 16 and each token's codes are one 16-byte load; 1 = M % 4 == 0, 4-byte
+// loads; 0 = byte loads (any M).
+constexpr int kLutThreads = 1024;
+constexpr int kLutSliceFloats = 32768;  // 128 KiB of LDS
+
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+  return v;
+}
+
+template <int QG, int CW>
+__global__ void __launch_bounds__(kLutThreads) pq_lut_score_kernel(LutArgs a) {
+  __shared__ float lds[kLutSliceFloats];
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t b_begin = wave * a.docs_per_wave;
+  const int64_t wave = (int64_t)blockIdx.x * (kLutThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t b_begin = wave_uniform(wave * a.docs_per_wave);
   const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
-  const int64_t MK = (int64_t)a.M * a.K;
+  const int M = a.M, K = a.K, MK = a.M * a.K;
+  const int64_t nd = a.nd;
   const float NEG_INF = -__builtin_inff();
+
+  // Accumulate the rows of the code bytes in `word` (subspaces m0 .. m0+n-1) into s.
+  auto gather4 = [&](float (&s)[QG], uint32_t word, int m0, int n) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      if (i < n) {
+        const uint32_t code = min((word >> (8 * i)) & 0xffu, (uint32_t)(K - 1));
+        const float* row = lds + ((uint32_t)(m0 + i) * (uint32_t)K + code) * QG;
+#pragma unroll
+        for (int j = 0; j < QG; j++) s[j] += row[j];
+      }
+    }
+  };
 
   float partial = 0.f;  // lane j: running score of document b_begin + j
   for (int q0 = 0; q0 < a.nq; q0 += QG) {
     __syncthreads();
-    for (int64_t i = threadIdx.x; i < MK * QG; i += blockDim.x) {
-      const int qq = (int)(i % QG);
-      const int64_t mk = i / QG;
+    for (int i = threadIdx.x; i < MK * QG; i += kLutThreads) {  // reads run along mk
+      const int qq = i / MK, mk = i - qq * MK;
       const int q = q0 + qq;
-      lds[i] = (q < a.nq) ? a.lut[(int64_t)q * MK + mk] : 0.f;
+      lds[mk * QG + qq] = (q < a.nq) ? a.lut[(int64_t)q * MK + mk] : 0.f;
     }
     __syncthreads();
-    if (b_begin >= a.B) continue;
     for (int64_t b = b_begin; b < b_end; b++) {
       float mx[QG];
 #pragma unroll
       for (int j = 0; j < QG; j++) mx[j] = NEG_INF;
-      for (int64_t t0 = 0; t0 < a.nd; t0 += 64) {
-        int64_t t = t0 + lane;
-        if (t > a.nd - 1) t = a.nd - 1;  // duplicate of the last token: max unchanged
-        const uint8_t* cp = a.codes + (b * a.nd + t) * a.M;
+      for (int64_t t0 = 0; t0 < nd; t0 += 64) {
+        const int64_t t = (t0 + lane < nd) ? t0 + lane : nd - 1;  // duplicate of the last token: max unchanged
+        const uint8_t* cp = a.codes + (b * nd + t) * M;
         float s[QG];
 #pragma unroll
         for (int j = 0; j < QG; j++) s[j] = 0.f;
-        for (int m = 0; m < a.M; m++) {
-          const int code = min((int)cp[m], a.K - 1);
-          const float* row = lds + ((int64_t)m * a.K + code) * QG;
-#pragma unroll
-          for (int j = 0; j < QG; j++) s[j] += row[j];
+        if constexpr (CW == 4) {
+          const uint4 v = *(const uint4*)cp;
+          gather4(s, v.x, 0, 4);
+          gather4(s, v.y, 4, 4);
+          gather4(s, v.z, 8, 4);
+          gather4(s, v.w, 12, 4);
+        } else if constexpr (CW == 1) {
+          for (int m0 = 0; m0 < M; m0 += 4) gather4(s, *(const uint32_t*)(cp + m0), m0, 4);
+        } else {
+          for (int m = 0; m < M; m++) gather4(s, cp[m], m, 1);
         }
 #pragma unroll
         for (int j = 0; j < QG; j++) mx[j] = fmaxf(mx[j], s[j]);
@@ -118,12 +153,10 @@ __global__ void __launch_bounds__(256) pq_lut_score_kernel(LutArgs a) {
       float tot = 0.f;
 #pragma unroll
       for (int j = 0; j < QG; j++) {
-        float v = mx[j];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+        const float v = cross_row_max(row_max16(mx[j]));
         tot += (q0 + j < a.nq) ? v : 0.f;
       }
-      if (a.nd == 0) tot = NEG_INF;
+      if (nd == 0) tot = NEG_INF;
       if (lane == (int)(b - b_begin)) partial += tot;
     }
   }
@@ -417,13 +450,18 @@ static int fill_scores(float* out, int64_t n, float v, hipStream_t st);
 int run_pq_batched(const void* Q, int64_t nQ, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub,
                    int dtype, const uint8_t* codes, int64_t B, int64_t nd, float* out, hipStream_t st);
 
-template <int QG>
+template <int QG, int CW>
 static int launch_lut_score(const LutArgs& a, hipStream_t st) {
   const int64_t waves = (a.B + a.docs_per_wave - 1) / a.docs_per_wave;
-  const int64_t grid = (waves + 3) / 4;
-  const size_t lds = (size_t)a.M * a.K * QG * 4;
-  hipLaunchKernelGGL(pq_lut_score_kernel<QG>, dim3((unsigned)grid), dim3(256), lds, st, a);
+  const int64_t grid = (waves + kLutThreads / 64 - 1) / (kLutThreads / 64);
+  hipLaunchKernelGGL((pq_lut_score_kernel<QG, CW>), dim3((unsigned)grid), dim3(kLutThreads), 0, st, a);
   return check_launch("pq_lut_score_kernel");
+}
+template <int QG>
+static int launch_lut_cw(const LutArgs& a, const uint8_t* codes, hipStream_t st) {
+  if (a.M == 16 && ((uintptr_t)codes & 15) == 0) return launch_lut_score<QG, 4>(a, st);
+  if (a.M % 4 == 0 && ((uintptr_t)codes & 3) == 0) return launch_lut_score<QG, 1>(a, st);
+  return launch_lut_score<QG, 0>(a, st);
 }
 
 constexpr int kPqUT = TMS_PQ_UT;
@@ -488,13 +526,14 @@ static int score_lut(const float* lut, int64_t nq, int64_t M, int64_t K, const u
   a.nq = (int32_t)nq;
   a.M = (int32_t)M;
   a.K = (int32_t)K;
-  a.docs_per_wave = 64;
-  if (B < 256 * 4 * 64) a.docs_per_wave = (int32_t)((B + 1023) / 1024 > 0 ? (B + 1023) / 1024 : 1);
-  if (a.docs_per_wave > 64) a.docs_per_wave = 64;
+  // at most 64 documents per wave (one lane each); fewer when B is small, so that the
+  // grid still covers every CU
+  const int64_t per_wave = (B + 256 * 16 - 1) / (256 * 16);
+  a.docs_per_wave = (int32_t)(per_wave < 1 ? 1 : (per_wave > 64 ? 64 : per_wave));
   const int64_t mk = M * K;
-  if (mk * 4 * 4 <= 64 * 1024) return launch_lut_score<4>(a, st);
-  if (mk * 2 * 4 <= 64 * 1024) return launch_lut_score<2>(a, st);
-  return launch_lut_score<1>(a, st);
+  if (mk * 8 <= kLutSliceFloats) return launch_lut_cw<8>(a, codes, st);
+  if (mk * 4 <= kLutSliceFloats) return launch_lut_cw<4>(a, codes, st);
+  return launch_lut_cw<2>(a, codes, st);  // M * K <= 16384, checked by the caller
 }
 
 }  // namespace tms
