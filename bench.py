@@ -477,7 +477,30 @@ class PQ:
                "lds_peak_tbs": 78.6, "lds_frac": round(lds_tbs / 78.6, 4),
                "mfma_flops_per_launch": flops, "mfma_tflops": round(mfma_tf, 1)}
         out.update(gemm_ceiling(self.torch, mfma_tf))
+        out.update(self.table_gather_line())
         return out
+
+    def table_gather_line(self, calls=2):
+        """The reference's algorithm on the same data, after the timed steps: build the
+        (Nq, M, K) fp32 distance table and gather from it (TileMaxSimPQ.score_batch with
+        method="lut"), HIP events around each call."""
+        torch = self.torch
+        f = lambda: self.pq.score_batch(self.Q[0], self.codes, method="lut", validate=False)
+        f()
+        ts = []
+        for _ in range(calls):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            f()
+            e1.record()
+            ts.append((e0, e1))
+        torch.cuda.synchronize()
+        ms = float(np.mean([a.elapsed_time(b) for a, b in ts]))
+        code_bytes = self.B * self.Nd * self.M
+        return {"table_gather_ms": round(ms, 3), "table_gather_docs_per_s": round(self.B / (ms * 1e-3), 1),
+                "table_gather_code_gbs": round(code_bytes / (ms * 1e-3) / 1e9, 1),
+                "table_gather_note": "the reference's algorithm (fp32 distance table in LDS, gathered per code) on "
+                                     "the same query and codes, one call per query"}
 
     def pairs_per_step(self):
         return self.nQ * self.B
