@@ -252,3 +252,23 @@ def test_bench_refuses_more_than_one_gpu():
                          text=True, timeout=120)
     assert res.returncode == 2, (res.returncode, res.stderr)
     assert "one GPU" in res.stderr and res.stdout == ""
+
+
+def test_c_consumer_links_and_gets_error_statuses(tmp_path):
+    """tests/c_abi_consumer.c, built with gcc against include/tilemaxsim.h and
+    libtilemaxsim.so, calls entry points with invalid arguments from C and checks the
+    status codes and tms_last_error(); no call reaches the GPU."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    lib_dir = os.path.join(REPO, "tilemaxsim_amd")
+    exe = str(tmp_path / "c_abi_consumer")
+    build = subprocess.run([gcc, "-std=c11", "-Wall", "-Werror", "-I", os.path.join(REPO, "include"),
+                            os.path.join(REPO, "tests", "c_abi_consumer.c"), "-L", lib_dir, "-ltilemaxsim",
+                            f"-Wl,-rpath,{lib_dir}", "-o", exe], capture_output=True, text=True)
+    assert build.returncode == 0, build.stderr
+    run = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert run.returncode == 0, (run.returncode, run.stdout, run.stderr)
+    assert run.stdout.startswith("ok ")
