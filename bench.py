@@ -153,6 +153,38 @@ class Dense:
         line.update(gemm_ceiling(torch, tf))
         return line
 
+    def graph_line(self, torch, replays=200):
+        """C1 only, after the timed steps: the same step (score, then top-k) captured once
+        in a HIP graph (torch.cuda.CUDAGraph) and replayed, as a serving loop would for
+        each new query; HIP events around the replays. The eager step pays the Python
+        and launch cost of every call; a replay pays one graph launch."""
+        if self.name != "c1":
+            return None
+        ident = lambda f: f()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.step(ident)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step(ident)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / replays
+        ms = e0.elapsed_time(e1) / replays
+        return {"ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall_ms, 4), "replays": replays,
+                "value": round(self.pairs_per_step() / (ms * 1e-3), 1), "unit": "docs/s",
+                "note": "the step captured once in a HIP graph and replayed"}
+
     def config(self):
         return {"workload": f"{self.name}: {self.nQ} queries x {self.B:,} docs, Nq={self.Nq}, Nd={self.Nd}, d={self.d}, "
                             f"fp16 L2-normalised Gaussian, top-{self.k} per query",
@@ -703,6 +735,9 @@ def main():
     batched = wl.batched_line(torch) if hasattr(wl, "batched_line") else None
     if batched:  # c2: the same workload through the batched-query path
         out["batched_queries"] = batched
+    graph = wl.graph_line(torch) if hasattr(wl, "graph_line") else None
+    if graph:  # c1: the same step replayed from a HIP graph
+        out["graph_replay"] = graph
     print(json.dumps(out), flush=True)
 
 
