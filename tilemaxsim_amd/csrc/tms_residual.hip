@@ -437,22 +437,17 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
 // MFMA A-operand layout), the KS partial |v|^2 of each token meet in LDS, and the
 // normalised x = fp16(v * (1 / fp16(|v|))) goes to an LDS ring from which all eight
 // waves score the tile against the query blocks they hold, as the dense batched kernel
-// does. With NS ring slots, step i scores tile i behind one LDS-only barrier:
-//   issue the ids of tile i + 2 NS and the centroid chunks / residual bytes of tile
-//   i + 1 + NS (from ids issued NS - 1 steps earlier); normalise tile i+1 (decoded a step
-//   earlier, partial norms visible since the last barrier) into the ring; decode tile
-//   i+2 (its body issued NS - 1 steps earlier) and write its partial norms; barrier; read
-//   tile i+1's fragments; score tile i from the fragments read a step earlier.
+// does. Step i opens with one LDS-only barrier and then: reads tile i+1's fragments;
+// (decoding waves) issues the ids of tile i+7 and the centroid chunks / residual bytes of
+// tile i+5, normalises tile i+2 into the ring (its partial norms visible since the
+// barrier) and decodes tile i+3 (its partial norms to LDS); scores tile i. The decoding
+// work precedes the wave's own MFMAs, so it overlaps the MFMAs of the scoring-only wave
+// that shares its SIMD instead of stalling the barrier after them.
 constexpr int kResBatchedWaves = 8;
-#ifndef TMS_RES_RING
-#define TMS_RES_RING 3  // ring slots; loads run NS - 1 steps ahead of their use
-#endif
 
 template <int KS, int NBITS, int NB>
 __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_kernel(ResArgs a) {
-  constexpr int NS = TMS_RES_RING;  // ring slots: x tiles, partial norms, centroid bodies, ids
-  static_assert(NS >= 3 && NS <= 6 && NS != 5, "the step loop is unrolled lcm(NS, 2) <= 6 times");
-  constexpr int U = NS % 2 == 0 ? NS : 2 * NS;  // steps per loop iteration (slot indices are constants)
+  constexpr int NS = 3;  // slots of every pipeline buffer: x tiles, partial norms, bodies, ids
   __shared__ __attribute__((aligned(16))) uint8_t lut[4096];
   __shared__ u32x4 ring[NS][4][64];
   __shared__ f32x4 nrm[NS][16];  // partial |v|^2 of token r from decoding wave w, at [slot][r][w]
@@ -624,27 +619,36 @@ __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_ker
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
 
-    // prologue: tiles 0 and 1 decoded, tile 0 in the ring, the bodies of tiles 2 .. NS and
-    // the ids of tiles NS+1 .. 2 NS - 1 in flight (tile t always sits in slot t % NS)
-#pragma unroll
-    for (int t = 0; t < NS; t++) load_ids(ids[t]);
-    load_body(ids[0], bd[0]);
-    load_ids(ids[0]);  // tile NS
+    // Schedule, for tile t: ids loaded at step t-7, centroid chunk and residual bytes at
+    // t-5, decoded at t-3 (partial norms to LDS), normalised at t-2 (into the ring),
+    // fragments read at t-1, scored at t; tile t sits in slot t % 3 of every buffer. Step
+    // i opens with the barrier, and a decoding wave then normalises tile i+2 and decodes
+    // tile i+3 before issuing its MFMAs for tile i, so that work overlaps the MFMAs of the
+    // scoring-only wave on its SIMD.
+    // prologue: ends with tile 0's fragments read, tile 1 normalised, tile 2 decoded, the
+    // bodies of tiles 3 and 4 and the ids of tiles 5 and 6 in flight
+    load_ids(ids[0]);  // tiles 0, 1, 2
+    load_ids(ids[1]);
+    load_ids(ids[2]);
+    load_body(ids[0], bd[0]);  // tiles 0, 1, 2
     load_body(ids[1], bd[1]);
-    load_ids(ids[1]);  // tile NS + 1
-    decode(bd[0], 0);
-#pragma unroll
-    for (int t = 2; t <= NS; t++) {
-      load_body(ids[t % NS], bd[t % NS]);
-      if (t < NS) load_ids(ids[t]);  // tile t + NS
-    }
+    load_body(ids[2], bd[2]);
+    load_ids(ids[0]);  // tiles 3, 4
+    load_ids(ids[1]);
+    decode(bd[0], 0);  // tile 0
     sync();
     normalise(0);
-    decode(bd[1], 1);
+    load_body(ids[0], bd[0]);  // tile 3
+    load_ids(ids[2]);          // tile 5
+    decode(bd[1], 1);          // tile 1
     sync();
+    normalise(1);
     u32x4 frag[2][KS];
 #pragma unroll
-    for (int s = 0; s < KS; s++) frag[0][s] = ring[0][s][lane];
+    for (int s = 0; s < KS; s++) frag[0][s] = ring[0][s][lane];  // tile 0
+    load_body(ids[1], bd[1]);  // tile 4
+    load_ids(ids[0]);          // tile 6
+    decode(bd[2], 2);          // tile 2
 
     float rmax[NB][2];
 #pragma unroll
@@ -666,16 +670,16 @@ __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_ker
       }
     };
     auto step = [&](auto slot) -> bool {
-      constexpr int i = decltype(slot)::value;  // step index mod U
-      constexpr int s0 = i % NS, s1 = (i + 1) % NS, s2 = (i + 2) % NS;
+      constexpr int i = decltype(slot)::value;  // step index mod 6
+      constexpr int k0 = i % NS, k1 = (i + 1) % NS, k2 = (i + 2) % NS;
       constexpr int f = i & 1;
-      load_ids(ids[s0]);           // tile i + 2 NS
-      load_body(ids[s1], bd[s1]);  // tile i + 1 + NS
-      normalise(s1);               // tile i+1
-      decode(bd[s2], s2);          // tile i+2
       sync();
 #pragma unroll
-      for (int s = 0; s < KS; s++) frag[f ^ 1][s] = ring[s1][s][lane];  // tile i+1
+      for (int s = 0; s < KS; s++) frag[f ^ 1][s] = ring[k1][s][lane];  // tile i+1
+      load_ids(ids[k1]);           // tile i+7 (the slot of tile i+4, whose body is loaded)
+      load_body(ids[k2], bd[k2]);  // tile i+5 (the slot of tile i+2, decoded)
+      normalise(k2);               // tile i+2
+      decode(bd[k0], k0);          // tile i+3
       const u32x4(&t)[KS] = frag[f];
       f32x4 acc[NB][2];
 #pragma unroll
@@ -700,12 +704,10 @@ __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_ker
     while (true) {
       if (step(RingSlot<0>{})) break;
       if (step(RingSlot<1>{})) break;
-      if (step(RingSlot<2 % U>{})) break;
-      if (step(RingSlot<3 % U>{})) break;
-      if constexpr (U > 4) {
-        if (step(RingSlot<4>{})) break;
-        if (step(RingSlot<5>{})) break;
-      }
+      if (step(RingSlot<2>{})) break;
+      if (step(RingSlot<3>{})) break;
+      if (step(RingSlot<4>{})) break;
+      if (step(RingSlot<5>{})) break;
     }
   };
   if (wc.b < b_end) {
