@@ -74,7 +74,8 @@ struct LutArgs {
 };
 
 // One lane per document token; a workgroup of 16 waves shares one slice of the table in
-// LDS: QG query tokens, [m][k][QG] fp32 (zero past nq), at most 128 KiB. Each lane loads
+// LDS: QG query tokens, [m][k][QG] fp32 (zero past nq), at most 64 KiB, so two
+// workgroups (32 waves) share a CU and hide each other's gather latency. Each lane loads
 // its token's M code bytes with one or a few wide loads, gathers its M rows of QG values
 // and adds them in ascending m, as the reference sums them (:154-167), then keeps a
 // running max per query token. A document's maxima are taken across the wave with DPP and
@@ -82,8 +83,11 @@ struct LutArgs {
 // b - b_begin. Slices loop inside the kernel, so the codes are read once per slice.
 // CW: 4 = M is 16 and each token's codes are one 16-byte load; 1 = M % 4 == 0, 4-byte
 // loads; 0 = byte loads (any M).
+#ifndef TMS_LUT_SLICE_FLOATS
+#define TMS_LUT_SLICE_FLOATS 16384  // table slice in LDS: 64 KiB, two workgroups per CU
+#endif
 constexpr int kLutThreads = 1024;
-constexpr int kLutSliceFloats = 32768;  // 128 KiB of LDS
+constexpr int kLutSliceFloats = TMS_LUT_SLICE_FLOATS;
 
 __device__ __forceinline__ float row_max16(float v) {
   v = fmaxf(v, dpp_f32<0xB1>(v));   // quad_perm [1,0,3,2]
@@ -530,10 +534,11 @@ static int score_lut(const float* lut, int64_t nq, int64_t M, int64_t K, const u
   // grid still covers every CU
   const int64_t per_wave = (B + 256 * 16 - 1) / (256 * 16);
   a.docs_per_wave = (int32_t)(per_wave < 1 ? 1 : (per_wave > 64 ? 64 : per_wave));
-  const int64_t mk = M * K;
+  const int64_t mk = M * K;  // <= 16384, checked by the caller
   if (mk * 8 <= kLutSliceFloats) return launch_lut_cw<8>(a, codes, st);
   if (mk * 4 <= kLutSliceFloats) return launch_lut_cw<4>(a, codes, st);
-  return launch_lut_cw<2>(a, codes, st);  // M * K <= 16384, checked by the caller
+  if (mk * 2 <= kLutSliceFloats) return launch_lut_cw<2>(a, codes, st);
+  return launch_lut_cw<1>(a, codes, st);
 }
 
 }  // namespace tms
