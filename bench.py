@@ -618,6 +618,18 @@ class Copy:
         return None
 
 
+def _cpu_model():
+    """The host CPU's model name (Linux /proc/cpuinfo), else the architecture."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def _time_cpu(fn, docs_per_call, seconds, threads, sample):
     from threadpoolctl import threadpool_limits
     with threadpool_limits(limits=threads):
@@ -631,8 +643,8 @@ def _time_cpu(fn, docs_per_call, seconds, threads, sample):
             if el >= seconds:
                 break
     return {"value": docs_per_call * n / el, "unit": "docs/s (1 query)", "cores": threads, "kind": "port",
-            "sample": f"{sample} {n}x in {el:.1f} s; host {platform.processor() or platform.machine()}, "
-                      f"os.cpu_count()={os.cpu_count()}"}
+            "sample": f"{sample} {n}x in {el:.1f} s; host {_cpu_model()}, os.cpu_count()={os.cpu_count()}, "
+                      f"{threads} threads"}
 
 
 def _traffic(kernel, config):
