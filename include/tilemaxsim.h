@@ -31,6 +31,11 @@ extern "C" {
 
 #define TMS_DTYPE_F16 0
 #define TMS_DTYPE_BF16 1
+/* fp32 embeddings: taken by the dense entry points (tms_maxsim_*) and by
+ * tms_pq_build_lut. Each element is split into two bf16 terms (hi + lo) on the fly and
+ * every product is formed from three bf16 products, so its relative error is at most
+ * about 3 * 2^-16 (the reference computes fp32 inputs with TF32 tl.dot, about 2^-10). */
+#define TMS_DTYPE_F32 2
 
 /* Library version (major * 10000 + minor * 100 + patch). */
 int tms_version(void);

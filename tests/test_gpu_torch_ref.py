@@ -118,3 +118,19 @@ def test_batched_queries_vs_torch_naive(cuda):
         ref = _naive(Qs[q], D)
         torch.testing.assert_close(got[q], ref, rtol=RTOL, atol=ATOL)
         _check_topk(got[q], ref)
+
+
+def test_fp32_dense_vs_torch_naive(cuda):
+    """fp32 inputs, unnormalised as in the reference's precision experiment
+    (``src/cycle6_rerun_scaling.py:96-106``)."""
+    import torch
+    from tilemaxsim_amd import flash_maxsim_multi_doc, flash_maxsim_v2_multiquery
+    g = torch.Generator().manual_seed(77)
+    Q, D = torch.randn(32, 128, generator=g), torch.randn(500, 70, 128, generator=g)
+    ref = _naive(Q, D)
+    got = flash_maxsim_v2_multiquery(Q.cuda(), D.cuda()).cpu()
+    torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
+    _check_topk(got, ref)
+    offsets = torch.arange(0, 501 * 70, 70, dtype=torch.int64)
+    got_v = flash_maxsim_multi_doc(Q.cuda(), D.reshape(-1, 128).cuda(), offsets.cuda()).cpu()
+    torch.testing.assert_close(got_v, ref, rtol=RTOL, atol=ATOL)

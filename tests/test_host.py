@@ -161,7 +161,9 @@ def test_python_errors_before_device_checks():
     with pytest.raises(AssertionError):
         flash_maxsim_v2_multiquery(Q[:, :64], D)
     with pytest.raises(TypeError):
-        flash_maxsim_v2_multiquery(Q, D.float())
+        flash_maxsim_v2_multiquery(Q, D.double())
+    with pytest.raises(ValueError, match="GPU"):
+        flash_maxsim_v2_multiquery(Q, D.float())  # float32 documents are taken (on the GPU)
     with pytest.raises(ValueError, match="contiguous"):
         flash_maxsim_v2_multiquery(Q, D.transpose(0, 1))
     with pytest.raises(ValueError, match="GPU"):
@@ -186,6 +188,8 @@ def test_python_errors_before_device_checks():
     with pytest.raises(ValueError):
         TileMaxSimPQ(torch.zeros(16, 256, dtype=torch.float16))
     with pytest.raises(TypeError):
+        TileMaxSimPQ(torch.zeros(16, 256, 8, dtype=torch.float64))
+    with pytest.raises(ValueError, match="GPU"):
         TileMaxSimPQ(torch.zeros(16, 256, 8))
     with pytest.raises(ValueError, match="GPU"):
         TileMaxSimPQ(torch.zeros(16, 256, 8, dtype=torch.float16))

@@ -29,8 +29,8 @@ def same_device(**tensors: torch.Tensor) -> torch.device:
 
 
 def embedding_dtype(name: str, t: torch.Tensor) -> None:
-    if t.dtype not in (torch.float16, torch.bfloat16):
-        raise TypeError(f"{name} must be float16 or bfloat16 (got {t.dtype})")
+    if t.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"{name} must be float16, bfloat16 or float32 (got {t.dtype})")
 
 
 def contiguous(name: str, t: torch.Tensor) -> None:

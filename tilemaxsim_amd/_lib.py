@@ -20,6 +20,7 @@ TMS_ERR_HIP = 3
 
 TMS_DTYPE_F16 = 0
 TMS_DTYPE_BF16 = 1
+TMS_DTYPE_F32 = 2
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -102,7 +103,9 @@ def dtype_code(dt: torch.dtype) -> int:
         return TMS_DTYPE_F16
     if dt == torch.bfloat16:
         return TMS_DTYPE_BF16
-    raise TypeError(f"tilemaxsim_amd kernels take float16 or bfloat16 embeddings, got {dt}")
+    if dt == torch.float32:
+        return TMS_DTYPE_F32
+    raise TypeError(f"tilemaxsim_amd kernels take float16, bfloat16 or float32 embeddings, got {dt}")
 
 
 def stream_of(t: torch.Tensor) -> int:

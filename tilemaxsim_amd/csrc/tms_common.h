@@ -11,6 +11,40 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Eight consecutive elements of an embedding row as loaded from memory: 16 bytes for
+// fp16 / bf16, 32 bytes for fp32.
+template <int DT>
+struct Raw8 {
+  using T = u32x4;
+};
+template <>
+struct Raw8<TMS_DTYPE_F32> {
+  using T = u32x8;
+};
+
+// fp32 -> two bf16 terms: hi = bf16(x), lo = bf16(x - hi), both rounded to nearest even.
+// x - hi is exact in fp32, so |x - hi - lo| <= 2^-16 |x|; a product x*y is then
+// hi_x*hi_y + hi_x*lo_y + lo_x*hi_y up to about 3 * 2^-16 |x*y| (the lo*lo term and the
+// two roundings). Returns eight bf16 values packed like an MFMA operand fragment.
+__device__ __forceinline__ void split_bf16(u32x8 x, u32x4& hi, u32x4& lo) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    // elements copied out first: __builtin_bit_cast of a vector-element expression
+    // reads element 0 with this compiler
+    const uint32_t x0 = x[2 * i], x1 = x[2 * i + 1];
+    const f32x2 v = {__builtin_bit_cast(float, x0), __builtin_bit_cast(float, x1)};
+    const bf16x2 h = __builtin_convertvector(v, bf16x2);
+    const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+    const f32x2 hv = {__builtin_bit_cast(float, hb << 16), __builtin_bit_cast(float, hb & 0xffff0000u)};
+    const bf16x2 l = __builtin_convertvector(v - hv, bf16x2);
+    hi[i] = hb;
+    lo[i] = __builtin_bit_cast(uint32_t, l);
+  }
+}
 
 // One v_mfma_f32_16x16x32_{f16,bf16}: C(16x16 f32) += A(16x32) * B(32x16).
 // Lane l holds A[row l%16][k 8*(l/16) .. +8], B[k 8*(l/16) .. +8][col l%16] and

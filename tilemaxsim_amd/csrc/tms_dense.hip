@@ -78,11 +78,22 @@ struct DenseArgs {
   int64_t pad_len;         // varlen: score as if zero-padded to this many tokens (0 = off)
 };
 
-// 16-byte fragment of row `row`, chunk c (elements 8c .. 8c+7), zero outside [0, d).
-template <bool ALIGNED>
-__device__ __forceinline__ u32x4 load_chunk(const uint8_t* base, int64_t row, int c, int d, int nchunk) {
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if constexpr (ALIGNED) {
+// Elements 8c .. 8c+7 of row `row` (16 bytes; 32 for fp32), zero outside [0, d).
+template <int DT, bool ALIGNED>
+__device__ __forceinline__ typename Raw8<DT>::T load_chunk(const uint8_t* base, int64_t row, int c, int d, int nchunk) {
+  typename Raw8<DT>::T v = {};
+  if constexpr (DT == TMS_DTYPE_F32) {
+    const uint32_t* p = (const uint32_t*)base + row * d + 8 * (int64_t)c;
+    if constexpr (ALIGNED) {  // d % 8 == 0 and a 16-byte aligned base: two 16-byte loads
+      if (c < nchunk) {
+        const u32x4 a0 = *(const u32x4*)p, a1 = *(const u32x4*)(p + 4);
+        v = u32x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) v[j] = (8 * c + j < d) ? p[j] : 0u;
+    }
+  } else if constexpr (ALIGNED) {
     if (c < nchunk) v = *(const u32x4*)(base + (row * d + 8 * (int64_t)c) * 2);
   } else {
     const uint16_t* p = (const uint16_t*)base + row * d;
@@ -115,6 +126,11 @@ __global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
   constexpr bool QREG = KS_REG > 0;
   constexpr int KS = QREG ? KS_REG : 4;
   constexpr int TT = 16 * NSUB;
+  // fp32 inputs: every fragment is split into bf16 hi + lo terms and a product takes
+  // three bf16 MFMAs (hi*hi + hi*lo + lo*hi); F32 == false is the one-MFMA path.
+  constexpr bool F32 = DT == TMS_DTYPE_F32;
+  constexpr int MDT = F32 ? TMS_DTYPE_BF16 : DT;
+  using Raw = typename Raw8<DT>::T;
   extern __shared__ u32x4 qlds[];
 
   const int lane = threadIdx.x & 63;
@@ -135,7 +151,15 @@ __global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
     return (int64_t)qi * a.nq + tok;
   };
 
+  // fp16 / bf16: the fragment itself; fp32: its bf16 hi term here and lo term in qfl
+  // (LDS path: the lo terms follow the nfrag hi fragments).
   u32x4 qf[QREG ? NQB : 1][QREG ? KS : 1][2];
+  u32x4 qfl[QREG && F32 ? NQB : 1][QREG && F32 ? KS : 1][2];
+  auto to_frag = [&](const Raw& raw, u32x4& hi, u32x4& lo) {
+    if constexpr (F32) split_bf16(raw, hi, lo);
+    else hi = raw;
+  };
+  const int nfrag = NQB * a.nstep * 2 * 64;
   if constexpr (QREG) {
 #pragma unroll
     for (int j = 0; j < NQB; j++)
@@ -145,10 +169,10 @@ __global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
         for (int h = 0; h < 2; h++) {
           bool valid;
           int64_t row = q_row(j, h, r, valid);
-          qf[j][s][h] = valid ? load_chunk<true>(a.Q, row, 4 * s + g, a.d, a.nchunk) : u32x4{0u, 0u, 0u, 0u};
+          const Raw raw = valid ? load_chunk<DT, true>(a.Q, row, 4 * s + g, a.d, a.nchunk) : Raw{};
+          to_frag(raw, qf[j][s][h], qfl[F32 ? j : 0][F32 ? s : 0][h]);
         }
   } else {
-    const int nfrag = NQB * a.nstep * 2 * 64;
     for (int f = threadIdx.x; f < nfrag; f += blockDim.x) {
       int fl = f & 63, rest = f >> 6;
       int h = rest & 1;
@@ -156,7 +180,11 @@ __global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
       int S = rest % a.nstep, j = rest / a.nstep;
       bool valid;
       int64_t row = q_row(j, h, fl & 15, valid);
-      qlds[f] = valid ? load_chunk<ALIGNED>(a.Q, row, 4 * S + (fl >> 4), a.d, a.nchunk) : u32x4{0u, 0u, 0u, 0u};
+      const Raw raw = valid ? load_chunk<DT, ALIGNED>(a.Q, row, 4 * S + (fl >> 4), a.d, a.nchunk) : Raw{};
+      u32x4 hi, lo;
+      to_frag(raw, hi, lo);
+      qlds[f] = hi;
+      if constexpr (F32) qlds[nfrag + f] = lo;
     }
     __syncthreads();
   }
@@ -248,7 +276,7 @@ __global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
 
   // ---- tile buffers ------------------------------------------------------------
   struct Buf {
-    u32x4 f[NSUB][KS];
+    Raw f[NSUB][KS];
     uint32_t m[NSUB];  // masked mode: validity bits of this lane's 4 output rows
   };
   auto load_tile = [&](Buf& buf, const Cursor& c) {
@@ -261,11 +289,11 @@ __global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
       for (int s = 0; s < KS; s++) {
         const int S = c.kg * KS + s;
         if (!QREG && S >= a.nstep) {
-          buf.f[sub][s] = u32x4{0u, 0u, 0u, 0u};
-        } else if constexpr (FULL && ALIGNED) {
+          buf.f[sub][s] = Raw{};
+        } else if constexpr (FULL && ALIGNED && !F32) {
           buf.f[sub][s] = *(const u32x4*)(a.D + (row * a.d + 8 * (int64_t)(4 * S + g)) * 2);
         } else {
-          buf.f[sub][s] = load_chunk<ALIGNED>(a.D, row, 4 * S + g, a.d, a.nchunk);
+          buf.f[sub][s] = load_chunk<DT, ALIGNED>(a.D, row, 4 * S + g, a.d, a.nchunk);
         }
       }
       if constexpr (MODE == MODE_MASKED) {
@@ -342,12 +370,27 @@ __global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
 #pragma unroll
         for (int sub = 0; sub < NSUB; sub++) acc1[sub][0] = acc1[sub][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < KS; s++)
+        for (int s = 0; s < KS; s++) {
+          if constexpr (F32) {
 #pragma unroll
-          for (int h = 0; h < 2; h++)
+            for (int sub = 0; sub < NSUB; sub++) {
+              u32x4 dh, dl;
+              split_bf16(buf.f[sub][s], dh, dl);
 #pragma unroll
-            for (int sub = 0; sub < NSUB; sub++)
-              acc1[sub][h] = mfma16x16x32<DT>(buf.f[sub][s], qf[j][s][h], acc1[sub][h]);
+              for (int h = 0; h < 2; h++) {
+                acc1[sub][h] = mfma16x16x32<MDT>(dl, qf[j][s][h], acc1[sub][h]);
+                acc1[sub][h] = mfma16x16x32<MDT>(dh, qfl[j][s][h], acc1[sub][h]);
+                acc1[sub][h] = mfma16x16x32<MDT>(dh, qf[j][s][h], acc1[sub][h]);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+              for (int sub = 0; sub < NSUB; sub++)
+                acc1[sub][h] = mfma16x16x32<MDT>(buf.f[sub][s], qf[j][s][h], acc1[sub][h]);
+          }
+        }
 #pragma unroll
         for (int sub = 0; sub < NSUB; sub++)
 #pragma unroll
@@ -360,15 +403,30 @@ __global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
     for (int s = 0; s < KS; s++) {
       const int S = c.kg * KS + s;
       if (!QREG && S >= a.nstep) break;
+      u32x4 dh[NSUB], dl[F32 ? NSUB : 1];
+#pragma unroll
+      for (int sub = 0; sub < NSUB; sub++) {
+        if constexpr (F32) split_bf16(buf.f[sub][s], dh[sub], dl[sub]);
+        else dh[sub] = buf.f[sub][s];
+      }
 #pragma unroll
       for (int j = 0; j < NQB; j++)
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-          u32x4 qv;
-          if constexpr (QREG) qv = qf[j][s][h];
-          else qv = qlds[((j * a.nstep + S) * 2 + h) * 64 + lane];
+          const int qi = ((j * a.nstep + S) * 2 + h) * 64 + lane;
+          const u32x4 qv = qlds[qi];
+          if constexpr (F32) {
+            const u32x4 qlv = qlds[nfrag + qi];
 #pragma unroll
-          for (int sub = 0; sub < NSUB; sub++) acc[sub][j][h] = mfma16x16x32<DT>(buf.f[sub][s], qv, acc[sub][j][h]);
+            for (int sub = 0; sub < NSUB; sub++) {
+              acc[sub][j][h] = mfma16x16x32<MDT>(dl[sub], qv, acc[sub][j][h]);
+              acc[sub][j][h] = mfma16x16x32<MDT>(dh[sub], qlv, acc[sub][j][h]);
+              acc[sub][j][h] = mfma16x16x32<MDT>(dh[sub], qv, acc[sub][j][h]);
+            }
+          } else {
+#pragma unroll
+            for (int sub = 0; sub < NSUB; sub++) acc[sub][j][h] = mfma16x16x32<MDT>(dh[sub], qv, acc[sub][j][h]);
+          }
         }
     }
     if (c.kg == a.nkg - 1) {
@@ -445,9 +503,26 @@ constexpr int kMaxQldsBytes = 64 * 1024;
 #define TMS_DENSE_PFD 1  // tiles in flight ahead of the one being scored
 #endif
 
+// LDS bytes of the query fragments of one launch (fp32: hi and lo terms).
+static size_t qlds_bytes(int dtype, int nqb, int nstep) {
+  return (size_t)nqb * nstep * 2 * 64 * 16 * (dtype == TMS_DTYPE_F32 ? 2 : 1);
+}
+
 template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED>
 static int launch_one(const DenseArgs& a, int64_t grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((dense_maxsim_kernel<DT, MODE, NQB, KS_REG, FULL, ALIGNED, kNSub, TMS_DENSE_PFD>),
+  // fp32 tiles hold twice the bytes per token: one 16-token row block per tile keeps
+  // the bytes in flight per wave where the 16-bit path has them
+  constexpr int NS = DT == TMS_DTYPE_F32 ? 1 : kNSub;
+  if (lds > 64 * 1024) {
+    int dev = 0, cap = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cap, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      return fail(TMS_ERR_HIP, "dense_maxsim_kernel: cannot query the LDS limit");
+    if (lds > (size_t)cap)
+      return fail(TMS_ERR_UNSUPPORTED, "dense_maxsim_kernel: query fragments need %zu bytes of LDS, the device has %d",
+                  lds, cap);
+  }
+  hipLaunchKernelGGL((dense_maxsim_kernel<DT, MODE, NQB, KS_REG, FULL, ALIGNED, NS, TMS_DENSE_PFD>),
                      dim3((unsigned)grid), dim3(256), lds, st, a);
   return check_launch("dense_maxsim_kernel");
 }
@@ -463,7 +538,7 @@ static int launch_nqb(const DenseArgs& a, bool aligned, int64_t grid, hipStream_
       default: return launch_one<DT, MODE, NQB, 4, true, true>(a, grid, 0, st);
     }
   }
-  size_t lds = (size_t)NQB * a.nstep * 2 * 64 * 16;
+  size_t lds = qlds_bytes(DT, NQB, a.nstep);
   if (lds == 0) lds = 16;
   if (full) return launch_one<DT, MODE, NQB, 0, true, true>(a, grid, lds, st);
   if (aligned) return launch_one<DT, MODE, NQB, 0, false, true>(a, grid, lds, st);
@@ -491,7 +566,8 @@ static int run_dense(DenseArgs a, int64_t nQ, int mode, bool aligned, hipStream_
   const int64_t grid = (waves + 3) / 4;
   // Blocks per launch: two when Q fits in VGPRs or its LDS copy stays small.
   int maxq = 2;
-  if (!(aligned && a.d > 0 && a.d <= 128 && a.d % 32 == 0) && (int64_t)2 * a.nstep * 2 * 1024 > kMaxQldsBytes) maxq = 1;
+  if (!(aligned && a.d > 0 && a.d <= 128 && a.d % 32 == 0) && qlds_bytes(DT, 2, a.nstep) > (size_t)kMaxQldsBytes)
+    maxq = 1;
   for (int64_t blk0 = 0; blk0 < nblocks_total; blk0 += maxq) {
     a.blk0 = (int32_t)blk0;
     a.nblk = (int32_t)((nblocks_total - blk0 < maxq) ? nblocks_total - blk0 : maxq);
@@ -513,7 +589,8 @@ static int run_dense(DenseArgs a, int64_t nQ, int mode, bool aligned, hipStream_
 static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B,
                        int64_t nd, int64_t total_tokens, const int64_t* offsets, const uint8_t* mask, int mode,
                        int dtype, float* out, void* stream, int64_t pad_len = 0) {
-  if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16) return fail(TMS_ERR_UNSUPPORTED, "%s: unsupported dtype %d", fn, dtype);
+  if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16 && dtype != TMS_DTYPE_F32)
+    return fail(TMS_ERR_UNSUPPORTED, "%s: unsupported dtype %d", fn, dtype);
   if (pad_len < 0) return fail(TMS_ERR_INVALID, "%s: negative pad_len %lld", fn, (long long)pad_len);
   if (nQ < 0 || nq < 0 || d < 0 || B < 0 || nd < 0 || total_tokens < 0)
     return fail(TMS_ERR_INVALID, "%s: negative size (nQ=%lld nq=%lld d=%lld B=%lld nd=%lld T=%lld)", fn, (long long)nQ,
@@ -553,6 +630,7 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   a.pad_len = pad_len;
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
   const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
+  if (dtype == TMS_DTYPE_F32) return run_dense<TMS_DTYPE_F32>(a, nQ, mode, aligned, st);
   if (mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, dtype, out, st);
   if (mode == MODE_VARLEN && qreg && a.nbq <= 4 && nQ * a.nbq >= 4)  // one pass for up to 32 blocks
     return run_varlen_batched(Q, nQ, nq, d, D, total_tokens, offsets, 0, B, pad_len, dtype, out, st);

@@ -45,8 +45,19 @@ __device__ __forceinline__ float elem_to_f32(uint16_t bits) {
 // ------------------------------------------------------------------------------
 // distance table
 // ------------------------------------------------------------------------------
+// Element i of an fp16 / bf16 / fp32 array, as fp32 (exact).
 template <int DT>
-__global__ void __launch_bounds__(256) pq_build_lut_kernel(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ C,
+__device__ __forceinline__ float load_elem(const void* __restrict__ p, int64_t i) {
+  if constexpr (DT == TMS_DTYPE_F32) return ((const float*)p)[i];
+  else return elem_to_f32<DT>(((const uint16_t*)p)[i]);
+}
+
+// T[q, m, k] = sum_j Q[q, m*dsub + j] * C[m, k, j] in fp32, accumulated with fused
+// multiply-adds in j order (the reference's _build_distance_table_kernel,
+// src/flash_pqsim_kernel.py:31-67, rounds each product and sums them with tl.sum; for
+// fp16 / bf16 inputs the products are exact either way).
+template <int DT>
+__global__ void __launch_bounds__(256) pq_build_lut_kernel(const void* __restrict__ Q, const void* __restrict__ C,
                                                            float* __restrict__ lut, int64_t total, int M, int K,
                                                            int dsub) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -54,10 +65,10 @@ __global__ void __launch_bounds__(256) pq_build_lut_kernel(const uint16_t* __res
   const int k = (int)(i % K);
   const int m = (int)((i / K) % M);
   const int64_t q = i / ((int64_t)K * M);
-  const uint16_t* qp = Q + (q * M + m) * dsub;
-  const uint16_t* cp = C + ((int64_t)m * K + k) * dsub;
+  const int64_t qb = (q * M + m) * dsub;
+  const int64_t cb = ((int64_t)m * K + k) * dsub;
   float s = 0.f;
-  for (int j = 0; j < dsub; j++) s += elem_to_f32<DT>(qp[j]) * elem_to_f32<DT>(cp[j]);
+  for (int j = 0; j < dsub; j++) s = __builtin_fmaf(load_elem<DT>(Q, qb + j), load_elem<DT>(C, cb + j), s);
   lut[i] = s;
 }
 
@@ -443,8 +454,8 @@ static int build_lut(const void* Q, int64_t nq, const void* C, int64_t M, int64_
   const int64_t total = nq * M * K;
   if (total == 0) return TMS_OK;
   const int64_t grid = (total + 255) / 256;
-  hipLaunchKernelGGL(pq_build_lut_kernel<DT>, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)Q,
-                     (const uint16_t*)C, lut, total, (int)M, (int)K, (int)dsub);
+  hipLaunchKernelGGL(pq_build_lut_kernel<DT>, dim3((unsigned)grid), dim3(256), 0, st, Q, C, lut, total, (int)M,
+                     (int)K, (int)dsub);
   return check_launch("pq_build_lut_kernel");
 }
 
@@ -557,13 +568,15 @@ extern "C" {
 int tms_pq_build_lut(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
                      float* lut, void* stream) {
   const char* fn = "tms_pq_build_lut";
-  if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16) return fail(TMS_ERR_UNSUPPORTED, "%s: unsupported dtype %d", fn, dtype);
+  if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16 && dtype != TMS_DTYPE_F32)
+    return fail(TMS_ERR_UNSUPPORTED, "%s: unsupported dtype %d", fn, dtype);
   if (nq < 0 || M < 0 || K < 0 || dsub < 0) return fail(TMS_ERR_INVALID, "%s: negative size", fn);
   if (nq * M * K == 0) return TMS_OK;
   if (!Q || !codebook || !lut) return fail(TMS_ERR_INVALID, "%s: NULL pointer", fn);
   if (nq * M * K > ((int64_t)1 << 40)) return fail(TMS_ERR_UNSUPPORTED, "%s: table too large", fn);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == TMS_DTYPE_F16) return build_lut<TMS_DTYPE_F16>(Q, nq, codebook, M, K, dsub, lut, st);
+  if (dtype == TMS_DTYPE_F32) return build_lut<TMS_DTYPE_F32>(Q, nq, codebook, M, K, dsub, lut, st);
   return build_lut<TMS_DTYPE_BF16>(Q, nq, codebook, M, K, dsub, lut, st);
 }
 

@@ -22,7 +22,7 @@ def flash_maxsim_single(Q: torch.Tensor, D: torch.Tensor) -> torch.Tensor:
 
     Args:
         Q: (Nq, d) query token embeddings.
-        D: (Nd, d) document token embeddings, float16 or bfloat16.
+        D: (Nd, d) document token embeddings, float16, bfloat16 or float32.
 
     Returns:
         0-d float32 tensor (the reference returns ``out.sum()``).
@@ -58,7 +58,7 @@ def flash_maxsim_multi_doc(Q: torch.Tensor, D_flat: torch.Tensor, doc_offsets: t
 
     Args:
         Q: (Nq, d) query embeddings.
-        D_flat: (total_tokens, d) all document tokens, float16 or bfloat16, contiguous.
+        D_flat: (total_tokens, d) all document tokens, float16, bfloat16 or float32, contiguous.
         doc_offsets: (num_docs + 1,) integer start offsets (any device; moved to Q's
             device as int64).
         validate: check on the host that offsets are non-decreasing within
@@ -160,7 +160,7 @@ def maxsim_score(Q: torch.Tensor, D: torch.Tensor, D_mask: torch.Tensor | None =
     before the max, so padding never wins a max (a fully masked document scores -inf).
 
     Args:
-        Q: (Nq, d); D: (B, Nd, d) float16/bfloat16 contiguous; D_mask: (B, Nd) bool or
+        Q: (Nq, d); D: (B, Nd, d) float16/bfloat16/float32 contiguous; D_mask: (B, Nd) bool or
             integer (non-zero = real token), or None for no mask.
 
     Returns:

@@ -49,7 +49,9 @@ def flash_maxsim_v2_multiquery(Q: torch.Tensor, D: torch.Tensor) -> torch.Tensor
 
     Args:
         Q: (Nq, d) query token embeddings (cast to D's dtype on device).
-        D: (B, Nd, d) document token embeddings, float16 or bfloat16, contiguous.
+        D: (B, Nd, d) document token embeddings, float16, bfloat16 or float32,
+            contiguous (float32 is computed as bf16 hi + lo terms, relative error per
+            product below 1e-4; the reference computes float32 with TF32 products).
 
     Returns:
         (B,) float32 scores on Q's device. A document with Nd == 0 scores -inf.

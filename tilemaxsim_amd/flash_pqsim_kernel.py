@@ -14,17 +14,19 @@ import torch
 from . import _check, _lib
 
 
-def _mfma_shape_ok(M: int, K: int, dsub: int) -> bool:
+def _mfma_shape_ok(M: int, K: int, dsub: int, dtype: torch.dtype) -> bool:
     d = M * dsub
-    return (dsub in (2, 4, 8, 16, 32) and d % 32 == 0 and 0 < d <= 128 and M % 4 == 0
-            and 1 <= K <= 256 and d * K * 2 <= 64 * 1024)
+    return (dtype in (torch.float16, torch.bfloat16) and dsub in (2, 4, 8, 16, 32) and d % 32 == 0
+            and 0 < d <= 128 and M % 4 == 0 and 1 <= K <= 256 and d * K * 2 <= 64 * 1024)
 
 
 class TileMaxSimPQ:
     """High-level PQ MaxSim scorer (``src/flash_pqsim_kernel.py:176-280``).
 
     Args:
-        codebook: (M, K, dsub) PQ centroids, float16 or bfloat16, on the GPU.
+        codebook: (M, K, dsub) PQ centroids, float16, bfloat16 or float32, on the GPU.
+            A float32 codebook is scored by the table-gather kernel on an exact fp32
+            table (the MFMA kernel takes 16-bit centroids).
     """
 
     def __init__(self, codebook: torch.Tensor):
@@ -106,8 +108,8 @@ class TileMaxSimPQ:
             raise ValueError(f"method must be 'auto', 'mfma' or 'lut', got {method!r}")
         aligned = all(t.data_ptr() % 16 == 0 for t in (Q, self.codebook, codes))
         small_docs = Nd * M < 2**31  # the MFMA kernel addresses a document's codes with 32-bit offsets
-        use_mfma = method == "mfma" or (method == "auto" and _mfma_shape_ok(self.M, self.K, self.dsub) and aligned
-                                        and small_docs)
+        shape_ok = _mfma_shape_ok(self.M, self.K, self.dsub, self.codebook.dtype)
+        use_mfma = method == "mfma" or (method == "auto" and shape_ok and aligned and small_docs)
         lib = _lib.load()
         with torch.cuda.device(Q.device):
             stream = _lib.stream_of(Q)
@@ -147,7 +149,7 @@ class TileMaxSimPQ:
         if B == 0 or nQ == 0:
             return scores
         aligned = all(t.data_ptr() % 16 == 0 for t in (Qs, self.codebook, codes))
-        if not (_mfma_shape_ok(self.M, self.K, self.dsub) and aligned and Nd * M < 2**31):
+        if not (_mfma_shape_ok(self.M, self.K, self.dsub, self.codebook.dtype) and aligned and Nd * M < 2**31):
             for q in range(nQ):
                 scores[q] = self.score_batch(Qs[q], codes, validate=False)
             return scores
