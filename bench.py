@@ -47,23 +47,30 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "copy"])
+    p.add_argument("--config", default="c2",
+                   choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "prec", "copy"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
+    p.add_argument("--dtype", default="fp16", choices=["fp16", "bf16", "fp32"],
+                   help="embedding dtype for --config c1, c2, c4 and prec")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
 
 
 # ----------------------------------------------------------------------------- data
-def normalized_fp16(torch, shape, gen, chunk_rows=1 << 21):
-    """Gaussian -> L2-normalise each token in fp32 -> fp16, generated in chunks on the GPU."""
-    out = torch.empty(shape, dtype=torch.float16, device="cuda")
+def normalized_fp16(torch, shape, gen, chunk_rows=1 << 21, dtype=None, normalize=True):
+    """Gaussian -> L2-normalise each token in fp32 -> fp16 (or ``dtype``), generated in
+    chunks on the GPU. ``normalize=False`` keeps the raw Gaussian values."""
+    out = torch.empty(shape, dtype=dtype or torch.float16, device="cuda")
     flat = out.view(-1, shape[-1])
     for s in range(0, flat.shape[0], chunk_rows):
         e = min(flat.shape[0], s + chunk_rows)
         x = torch.randn(e - s, shape[-1], device="cuda", generator=gen)
-        flat[s:e] = torch.nn.functional.normalize(x, dim=-1).half()
+        flat[s:e] = torch.nn.functional.normalize(x, dim=-1) if normalize else x
     return out
+
+
+DTYPES = {"fp16": ("float16", 2), "bf16": ("bfloat16", 2), "fp32": ("float32", 4)}
 
 
 def topk_rows(scores, k):
@@ -100,15 +107,18 @@ class KernelTimer:
 class Dense:
     kernel = "dense_maxsim_kernel"
 
-    def __init__(self, torch, n_queries, B, Nd, d, Nq=32, name="c2", topk=100):
+    def __init__(self, torch, n_queries, B, Nd, d, Nq=32, name="c2", topk=100, dtype="fp16", normalize=True):
         self.torch, self.nQ, self.B, self.Nd, self.d, self.Nq, self.k = torch, n_queries, B, Nd, d, Nq, topk
-        self.name = name
-        # fixed-length documents with d in {32, 64, 96, 128} run the streaming kernel
-        self.kernel = "stream_maxsim_kernel" if d <= 128 and d % 32 == 0 else "dense_maxsim_kernel"
+        self.name, self.dtype, self.normalize = name, dtype, normalize
+        tname, self.esize = DTYPES[dtype]
+        # fixed-length fp16 / bf16 documents with d in {32, 64, 96, 128} run the streaming kernel
+        self.kernel = ("stream_maxsim_kernel" if d <= 128 and d % 32 == 0 and dtype != "fp32"
+                       else "dense_maxsim_kernel")
         gen = torch.Generator(device="cuda").manual_seed(1234)
-        log(f"[bench] generating {B} docs x {Nd} x {d} fp16 ({B * Nd * d * 2 / 1e9:.2f} GB)")
-        self.D = normalized_fp16(torch, (B, Nd, d), gen)
-        self.Q = normalized_fp16(torch, (n_queries, Nq, d), gen)
+        log(f"[bench] generating {B} docs x {Nd} x {d} {dtype} ({B * Nd * d * self.esize / 1e9:.2f} GB)")
+        tdt = getattr(torch, tname)
+        self.D = normalized_fp16(torch, (B, Nd, d), gen, dtype=tdt, normalize=normalize)
+        self.Q = normalized_fp16(torch, (n_queries, Nq, d), gen, dtype=tdt, normalize=normalize)
         self.scores = torch.empty(n_queries, B, dtype=torch.float32, device="cuda")
 
     def step(self, timer):
@@ -119,7 +129,7 @@ class Dense:
         return topk_rows(self.scores, min(self.k, self.B))
 
     def bytes_per_launch(self):
-        return self.Nq * self.d * 2 + self.B * self.Nd * self.d * 2 + self.B * 4
+        return (self.Nq * self.d + self.B * self.Nd * self.d) * self.esize + self.B * 4
 
     def pairs_per_step(self):
         return self.nQ * self.B
@@ -128,7 +138,7 @@ class Dense:
         """C2 only, after the timed steps: the same step (every query against every
         document, then the top-k) with all queries in one flash_maxsim_batched_queries
         call per step; HIP events around each call and around each whole step."""
-        if self.name != "c2":
+        if self.name != "c2" or self.dtype == "fp32":  # fp32 has no shared-tile kernel
             return None
         from tilemaxsim_amd import flash_maxsim_batched_queries
         calls, whole = [], []
@@ -186,16 +196,21 @@ class Dense:
                 "note": "the step captured once in a HIP graph and replayed"}
 
     def config(self):
-        return {"workload": f"{self.name}: {self.nQ} queries x {self.B:,} docs, Nq={self.Nq}, Nd={self.Nd}, d={self.d}, "
-                            f"fp16 L2-normalised Gaussian, top-{self.k} per query",
-                "queries": self.nQ, "docs": self.B, "Nq": self.Nq, "Nd": self.Nd, "d": self.d, "top_k": self.k,
-                "kernel": "flash_maxsim_v2_multiquery (one HBM pass per query)"}
+        values = "L2-normalised Gaussian" if self.normalize else "unnormalised Gaussian"
+        cfg = {"workload": f"{self.name}: {self.nQ} queries x {self.B:,} docs, Nq={self.Nq}, Nd={self.Nd}, d={self.d}, "
+                           f"{self.dtype} {values}, top-{self.k} per query",
+               "queries": self.nQ, "docs": self.B, "Nq": self.Nq, "Nd": self.Nd, "d": self.d, "top_k": self.k,
+               "dtype": self.dtype, "kernel": "flash_maxsim_v2_multiquery (one HBM pass per query)"}
+        if self.name == "prec":
+            cfg["reference_shape"] = ("the reference's precision experiment: src/cycle6_rerun_scaling.py:96-115, "
+                                      "src/run_all_experiments.py:287-347")
+        return cfg
 
     def cpu_baseline(self, seconds, threads):
         from oracle import maxsim_oracle as orc
         n = min(self.B, 4000)
-        Q = self.Q[0].cpu().numpy()
-        D = self.D[:n].cpu().numpy()
+        Q = self.Q[0].float().cpu().numpy()
+        D = self.D[:n].float().cpu().numpy()
         return _time_cpu(lambda: orc.maxsim_naive(Q, D, chunk=500), n, seconds, threads,
                          f"{n} docs of this corpus x query 0, numpy fp32 materialise-then-reduce "
                          "(restates pytorch_maxsim_naive), repeated")
@@ -663,6 +678,9 @@ def main():
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); documents shard across GPUs "
               "with no communication besides a top-k merge, which is not part of this build", file=sys.stderr)
         sys.exit(2)
+    if args.dtype != "fp16" and args.config not in ("c1", "c2", "c4", "prec"):
+        print(f"bench.py: --dtype applies to --config c1, c2, c4 and prec (got {args.config})", file=sys.stderr)
+        sys.exit(2)
     import torch
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
@@ -671,9 +689,12 @@ def main():
     import tilemaxsim_amd  # noqa: F401  (fails loudly if libtilemaxsim.so is missing)
 
     if args.config == "c1":
-        wl = Dense(torch, 1, 1000, 128, 128, name="c1")
+        wl = Dense(torch, 1, 1000, 128, 128, name="c1", dtype=args.dtype)
     elif args.config == "c2":
-        wl = Dense(torch, 64, 1_000_000, 180, 128, name="c2")
+        wl = Dense(torch, 64, 1_000_000, 180, 128, name="c2", dtype=args.dtype)
+    elif args.config == "prec":
+        # the reference's precision experiment: 1 query, B = 10K, Nd = 128, d = 128, raw randn
+        wl = Dense(torch, 1, 10_000, 128, 128, name="prec", dtype=args.dtype, normalize=False)
     elif args.config == "c2b":
         wl = DenseBatched(torch, 64, 1_000_000, 180, 128, name="c2b")
     elif args.config == "c3":
@@ -681,7 +702,7 @@ def main():
     elif args.config == "c3b":
         wl = VarlenBatched(torch, 32, 2_000_000, 32, 300, 128)
     elif args.config == "c4":
-        wl = Dense(torch, 16, 200_000, 128, args.d, name=f"c4_d{args.d}")
+        wl = Dense(torch, 16, 200_000, 128, args.d, name=f"c4_d{args.d}", dtype=args.dtype)
     elif args.config == "c5":
         wl = PQ(torch, 32, 5_000_000, 128)
     elif args.config == "c5b":
@@ -712,7 +733,8 @@ def main():
 
     nbytes = wl.bytes_per_launch()
     achieved = nbytes / (k_mean * 1e-3) / 1e9
-    traffic, traffic_src = _traffic(wl.kernel, args.config if args.config != "c4" else f"c4_d{args.d}")
+    tconf = args.config if args.config != "c4" else f"c4_d{args.d}"
+    traffic, traffic_src = _traffic(wl.kernel, tconf if args.dtype == "fp16" else f"{tconf}_{args.dtype}")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": wl.kernel, "bytes_per_launch": nbytes, "launch_ms_mean": round(k_mean, 5),
@@ -739,7 +761,7 @@ def main():
     out = {
         "metric": METRIC, "value": round(pairs / (ms_step * 1e-3), 1), "unit": "docs/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": getattr(wl, "dtype", "fp16"),
         "data": "synthetic (seeded; no dataset)", "config": wl.config(),
         "hbm_gbs": round(achieved, 1), "hbm_pct_of_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
         "roofline": roofline, "cpu_baseline": cpu,

@@ -256,6 +256,10 @@ def test_bench_refuses_more_than_one_gpu():
                          text=True, timeout=120)
     assert res.returncode == 2, (res.returncode, res.stderr)
     assert "one GPU" in res.stderr and res.stdout == ""
+    # --dtype only applies to the dense fixed-length configs
+    res = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--config", "c5", "--dtype", "fp32"],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 2 and "--dtype" in res.stderr, (res.returncode, res.stderr)
 
 
 def test_c_consumer_links_and_gets_error_statuses(tmp_path):
