@@ -12,8 +12,10 @@ through the batched-query kernel), c4
 (d-tiled, ``--d 256|512|768``), c5 (PQ/ADC, 5M documents of uint8 codes), c5b (c5
 through the batched-query kernel), c6 (C3's
 corpus as a ColBERTv2 residual-compressed index, fused decode + MaxSim per query), c6b
-(the same index, all queries through the batched residual kernel), copy (counter
-calibration).
+(the same index, all queries through the batched residual kernel), prec (the
+reference's precision experiment: 1 query x 10K raw-Gaussian documents, Nd = 128,
+d = 128), copy (counter calibration). ``--dtype fp16|bf16|fp32`` sets the embedding
+dtype of c1, c2, c4 and prec.
 
 Prints ONE JSON line on stdout. ``value`` is (query, document) pairs scored per second
 over the whole step; ``roofline`` is the dominant kernel's algorithmic bandwidth from
@@ -209,8 +211,11 @@ class Dense:
     def cpu_baseline(self, seconds, threads):
         from oracle import maxsim_oracle as orc
         n = min(self.B, 4000)
-        Q = self.Q[0].float().cpu().numpy()
-        D = self.D[:n].float().cpu().numpy()
+        Q, D = self.Q[0], self.D[:n]
+        if self.dtype == "bf16":  # numpy has no bfloat16: cast once, outside the timed calls
+            Q, D = Q.float(), D.float()
+        # fp16 stays fp16: the timed port casts each chunk to fp32, as the reference's .float() does
+        Q, D = Q.cpu().numpy(), D.cpu().numpy()
         return _time_cpu(lambda: orc.maxsim_naive(Q, D, chunk=500), n, seconds, threads,
                          f"{n} docs of this corpus x query 0, numpy fp32 materialise-then-reduce "
                          "(restates pytorch_maxsim_naive), repeated")
