@@ -21,6 +21,9 @@
 //    no -inf masking is needed and nothing outside the document is fetched.
 //  * The per-(query token, row) running max lives in the MFMA accumulator layout; the
 //    cross-lane max and the sum over query tokens happen once per document.
+//  * fp32 embeddings: a lane's 8-element chunk is 32 bytes (two 16-byte loads), split
+//    into bf16 hi and lo terms before the MFMAs, and each product is formed from three
+//    bf16 MFMAs (split_bf16 in tms_common.h); tiles are one 16-token block.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
