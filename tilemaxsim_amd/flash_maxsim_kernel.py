@@ -96,7 +96,7 @@ def flash_maxsim_multi_doc(Q: torch.Tensor, D_flat: torch.Tensor, doc_offsets: t
     if num_docs == 0:
         return scores
     lib = _lib.load()
-    with torch.cuda.device(Q.device):
+    with _lib.on_device(Q.device):
         _lib.check(lib.tms_maxsim_varlen(Q.data_ptr(), Nq, d, D_flat.data_ptr(), T, offsets.data_ptr(), num_docs,
                                          _lib.dtype_code(D_flat.dtype), scores.data_ptr(), _lib.stream_of(Q)))
     return scores
@@ -133,7 +133,7 @@ def _varlen_batched(fn: str, Qs: torch.Tensor, D_flat: torch.Tensor, doc_offsets
     if B == 0 or nQ == 0:
         return out
     lib = _lib.load()
-    with torch.cuda.device(Qs.device):
+    with _lib.on_device(Qs.device):
         _lib.check(lib.tms_maxsim_varlen_batched(Qs.data_ptr(), nQ, Nq, d, D_flat.data_ptr(), T, offsets.data_ptr(), B,
                                                  pad_len, _lib.dtype_code(D_flat.dtype), out.data_ptr(),
                                                  _lib.stream_of(Qs)))
@@ -193,7 +193,7 @@ def maxsim_score(Q: torch.Tensor, D: torch.Tensor, D_mask: torch.Tensor | None =
     if B == 0:
         return scores
     lib = _lib.load()
-    with torch.cuda.device(Q.device):
+    with _lib.on_device(Q.device):
         _lib.check(lib.tms_maxsim_masked(Q.data_ptr(), Q.shape[0], d, D.data_ptr(), mask.data_ptr(), B, Nd,
                                          _lib.dtype_code(D.dtype), scores.data_ptr(), _lib.stream_of(Q)))
     return scores

@@ -32,7 +32,7 @@ def _dense(Q: torch.Tensor, D: torch.Tensor, fn: str) -> torch.Tensor:
     if B == 0:
         return scores
     lib = _lib.load()
-    with torch.cuda.device(Q.device):
+    with _lib.on_device(Q.device):
         _lib.check(lib.tms_maxsim_dense(Q.data_ptr(), Nq, d, D.data_ptr(), B, Nd, _lib.dtype_code(D.dtype),
                                         scores.data_ptr(), _lib.stream_of(Q)))
     return scores
@@ -91,7 +91,7 @@ def flash_maxsim_batched_queries(Qs: torch.Tensor, D: torch.Tensor) -> torch.Ten
     if B == 0 or nQ == 0:
         return out
     lib = _lib.load()
-    with torch.cuda.device(Qs.device):
+    with _lib.on_device(Qs.device):
         _lib.check(lib.tms_maxsim_dense_batched(Qs.data_ptr(), nQ, Nq, d, D.data_ptr(), B, Nd,
                                                 _lib.dtype_code(D.dtype), out.data_ptr(), _lib.stream_of(Qs)))
     return out

@@ -72,7 +72,7 @@ class TileMaxSimPQ:
         if table.numel() == 0:
             return table
         lib = _lib.load()
-        with torch.cuda.device(Q.device):
+        with _lib.on_device(Q.device):
             _lib.check(lib.tms_pq_build_lut(Q.data_ptr(), Nq, self.codebook.data_ptr(), self.M, self.K, self.dsub,
                                             _lib.dtype_code(self.codebook.dtype), table.data_ptr(),
                                             _lib.stream_of(Q)))
@@ -111,7 +111,7 @@ class TileMaxSimPQ:
         shape_ok = _mfma_shape_ok(self.M, self.K, self.dsub, self.codebook.dtype)
         use_mfma = method == "mfma" or (method == "auto" and shape_ok and aligned and small_docs)
         lib = _lib.load()
-        with torch.cuda.device(Q.device):
+        with _lib.on_device(Q.device):
             stream = _lib.stream_of(Q)
             if use_mfma:
                 _lib.check(lib.tms_pq_score(Q.data_ptr(), Nq, self.codebook.data_ptr(), self.M, self.K, self.dsub,
@@ -154,7 +154,7 @@ class TileMaxSimPQ:
                 scores[q] = self.score_batch(Qs[q], codes, validate=False)
             return scores
         lib = _lib.load()
-        with torch.cuda.device(Qs.device):
+        with _lib.on_device(Qs.device):
             _lib.check(lib.tms_pq_score_batched(Qs.data_ptr(), nQ, Nq, self.codebook.data_ptr(), self.M, self.K,
                                                 self.dsub, _lib.dtype_code(self.codebook.dtype), codes.data_ptr(), B,
                                                 Nd, scores.data_ptr(), _lib.stream_of(Qs)))

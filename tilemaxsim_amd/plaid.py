@@ -72,7 +72,7 @@ def flashmaxsim_score_packed(Q: torch.Tensor, D_packed: torch.Tensor, D_lengths:
     if B == 0:
         return scores
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.check(lib.tms_maxsim_varlen_padded(Q2.data_ptr(), Q2.shape[0], d, D_packed.data_ptr(), T,
                                                 offsets.data_ptr(), B, pad_len, _lib.TMS_DTYPE_F16,
                                                 scores.data_ptr(), _lib.stream_of(Q2)))

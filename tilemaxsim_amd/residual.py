@@ -69,7 +69,7 @@ def decompress_residual(codes: torch.Tensor, residuals: torch.Tensor, centroids:
     if T == 0:
         return out
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.check(lib.tms_residual_decompress(codes.data_ptr(), residuals.data_ptr(), T, centroids.data_ptr(),
                                                centroids.shape[0], d, bucket_weights.data_ptr(), nbits,
                                                out.data_ptr(), _lib.stream_of(codes)))
@@ -151,7 +151,7 @@ def flashmaxsim_score_residual(Q: torch.Tensor, codes: torch.Tensor, residuals: 
     if B == 0:
         return scores
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.check(lib.tms_maxsim_residual(Q2.data_ptr(), Q2.shape[0], d, centroids.data_ptr(), centroids.shape[0],
                                            bucket_weights.data_ptr(), nbits, codes.data_ptr(), residuals.data_ptr(),
                                            T, offsets.data_ptr(), ndocs,
@@ -191,7 +191,7 @@ def flashmaxsim_score_residual_batched(Qs: torch.Tensor, codes: torch.Tensor, re
     if B == 0 or nQ == 0:
         return scores
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         _lib.check(lib.tms_maxsim_residual_batched(Qs.data_ptr(), nQ, Nq, d, centroids.data_ptr(), centroids.shape[0],
                                                    bucket_weights.data_ptr(), nbits, codes.data_ptr(),
                                                    residuals.data_ptr(), T, offsets.data_ptr(), ndocs,

@@ -7,12 +7,19 @@ Order: values descending; equal values by ascending index (deterministic, where
 """
 from __future__ import annotations
 
+import functools
+
 import torch
 
 from . import _check, _lib
 from .flash_maxsim_v2 import flash_maxsim_batched_queries, flash_maxsim_v2_multiquery
 
 MAX_K = 1024
+
+
+@functools.lru_cache(maxsize=256)
+def _workspace_bytes(rows: int, n: int, k: int) -> int:
+    return int(_lib.load().tms_topk_workspace_size(rows, n, k))
 
 
 def topk(scores: torch.Tensor, k: int):
@@ -40,14 +47,19 @@ def topk(scores: torch.Tensor, k: int):
     idx = torch.empty(rows, k, dtype=torch.int64, device=s2.device)
     if rows > 0 and k > 0:
         lib = _lib.load()
-        ws_bytes = int(lib.tms_topk_workspace_size(rows, n, k))
+        per_call = min(rows, 65535)  # grid-y limit per call
+        ws_bytes = _workspace_bytes(per_call, n, k)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=s2.device)
-        with torch.cuda.device(s2.device):
+        with _lib.on_device(s2.device):
             stream = _lib.stream_of(s2)
-            for r0 in range(0, rows, 65535):  # grid-y limit per call
-                r1 = min(rows, r0 + 65535)
-                _lib.check(lib.tms_topk(s2[r0:r1].data_ptr(), r1 - r0, n, k, ws.data_ptr(), ws_bytes,
-                                        vals[r0:r1].data_ptr(), idx[r0:r1].data_ptr(), stream))
+            if rows == per_call:
+                _lib.check(lib.tms_topk(s2.data_ptr(), rows, n, k, ws.data_ptr(), ws_bytes, vals.data_ptr(),
+                                        idx.data_ptr(), stream))
+            else:
+                for r0 in range(0, rows, per_call):
+                    r1 = min(rows, r0 + per_call)
+                    _lib.check(lib.tms_topk(s2[r0:r1].data_ptr(), r1 - r0, n, k, ws.data_ptr(), ws_bytes,
+                                            vals[r0:r1].data_ptr(), idx[r0:r1].data_ptr(), stream))
     if scores.dim() == 1:
         return vals[0], idx[0]
     return vals, idx
