@@ -106,8 +106,8 @@ int tms_maxsim_varlen_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d,
                               float* out, void* stream);
 
 /*
- * PQ distance table lut[q, m, k] = sum_j Q[q, m*dsub + j] * codebook[m, k, j] (fp32).
- * Replaces TileMaxSimPQ.build_distance_table (src/flash_pqsim_kernel.py:190-211) and
+ * PQ distance table lut[q, m, k] = sum_j Q[q, m*dsub + j] * codebook[m, k, j] (fp32;
+ * fp16, bf16 or fp32 Q and codebook of one dtype). Replaces TileMaxSimPQ.build_distance_table (src/flash_pqsim_kernel.py:190-211) and
  * _build_distance_table_kernel (:31-67).
  */
 int tms_pq_build_lut(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
@@ -127,8 +127,8 @@ int tms_pq_score_lut(const float* lut, int64_t nq, int64_t M, int64_t K, const u
  * fp32 summation order. Replaces TileMaxSimPQ.score_batch (src/flash_pqsim_kernel.py:
  * 213-252) as a whole. Shapes: d = M * dsub in {32, 64, 96, 128}, dsub in {2, 4, 8, 16,
  * 32}, M a multiple of 4, K <= 256, a codebook of at most 64 KiB, 16-byte aligned Q,
- * codebook and codes, and nd * M < 2^31; other shapes return TMS_ERR_UNSUPPORTED (score
- * them with tms_pq_build_lut + tms_pq_score_lut).
+ * codebook and codes, nd * M < 2^31, and an fp16 or bf16 codebook; other shapes and
+ * fp32 return TMS_ERR_UNSUPPORTED (score them with tms_pq_build_lut + tms_pq_score_lut).
  */
 int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
                  const uint8_t* codes, int64_t B, int64_t nd, float* out, void* stream);
