@@ -501,6 +501,12 @@ static int fill(float* out, int64_t n, float v, hipStream_t st) {
 #define TMS_DENSE_TOKENS_PER_WAVE 192  // document tokens one wave streams (rounded to whole documents)
 #endif
 constexpr int kNSub = TMS_DENSE_NSUB;
+#ifndef TMS_DENSE_F32_NSUB
+#define TMS_DENSE_F32_NSUB 1  // 16-token row blocks per tile for fp32 documents, Q in VGPRs
+#endif
+#ifndef TMS_DENSE_F32_LDS_NSUB
+#define TMS_DENSE_F32_LDS_NSUB 2  // the same with Q in LDS
+#endif
 constexpr int kMaxQldsBytes = 64 * 1024;
 #ifndef TMS_DENSE_PFD
 #define TMS_DENSE_PFD 1  // tiles in flight ahead of the one being scored
@@ -513,9 +519,12 @@ static size_t qlds_bytes(int dtype, int nqb, int nstep) {
 
 template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED>
 static int launch_one(const DenseArgs& a, int64_t grid, size_t lds, hipStream_t st) {
-  // fp32 tiles hold twice the bytes per token: one 16-token row block per tile keeps
-  // the bytes in flight per wave where the 16-bit path has them
-  constexpr int NS = DT == TMS_DTYPE_F32 ? 1 : kNSub;
+  // fp32 tiles hold twice the bytes per token: with Q in VGPRs, one 16-token row block
+  // per tile keeps the bytes in flight per wave where the 16-bit path has them; with Q
+  // in LDS (d > 128: its lo terms take up to 128 KiB, one or two workgroups per CU) two
+  // blocks per tile keep more bytes in flight per wave (measured: +20 % at d = 768,
+  // +12 % at d = 1000, within 4 % either way at d = 200 .. 512)
+  constexpr int NS = DT == TMS_DTYPE_F32 ? (KS_REG > 0 ? TMS_DENSE_F32_NSUB : TMS_DENSE_F32_LDS_NSUB) : kNSub;
   if (lds > 64 * 1024) {
     int dev = 0, cap = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
