@@ -54,6 +54,14 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     # NULL output with work to do
     rc, msg = _c_call("tms_maxsim_dense", 16, 32, 128, 16, 10, 5, 0, None, None)
     assert rc == 1 and "out" in msg
+    # fp32 (TMS_DTYPE_F32 = 2) passes the dense dtype check and stops at the same NULL output
+    rc, msg = _c_call("tms_maxsim_dense", 16, 32, 128, 16, 10, 5, 2, None, None)
+    assert rc == 1 and "out" in msg
+    # the MFMA PQ scorer takes 16-bit codebooks only: fp32 is refused before any HIP call
+    rc, msg = _c_call("tms_pq_score", 16, 32, 16, 16, 256, 8, 2, 16, 10, 5, 16, None)
+    assert rc == 2 and "dtype" in msg
+    rc, msg = _c_call("tms_pq_score_batched", 16, 2, 32, 16, 16, 256, 8, 2, 16, 10, 5, 16, None)
+    assert rc == 2 and "dtype" in msg
     # empty batch: nothing to do, success, no HIP call
     rc, _ = _c_call("tms_maxsim_dense", None, 32, 128, None, 0, 5, 0, None, None)
     assert rc == 0
