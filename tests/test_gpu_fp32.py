@@ -125,12 +125,13 @@ def test_fp32_misaligned_pointer_and_mixed_dtypes(cuda):
 
 
 @pytest.mark.gpu
-def test_fp32_masked_varlen_and_batched(cuda):
+@pytest.mark.parametrize("d", [128, 768])  # Q in VGPRs; Q in LDS above 80 KiB (8-wave workgroups)
+def test_fp32_masked_varlen_and_batched(cuda, d):
     import torch
     from tilemaxsim_amd import (flash_maxsim_batched_queries, flash_maxsim_multi_doc,
                                 flash_maxsim_multi_doc_batched, maxsim_score)
-    rng = _rng(9)
-    B, Nmax, d = 120, 90, 128
+    rng = _rng(9 + d)
+    B, Nmax = 120, 90
     lens = rng.integers(0, Nmax + 1, B)
     lens[:3] = 0
     Q = _randn(rng, (32, d), True)

@@ -124,8 +124,8 @@ struct Cursor {
 
 // KS_REG > 0: Q fragments in VGPRs, d == 32 * KS_REG (single k-group).
 // KS_REG == 0: Q fragments in LDS, k-groups of 4 steps (128 dims), any d.
-template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, int NSUB, int PFD>
-__global__ void __launch_bounds__(256, 1) dense_maxsim_kernel(DenseArgs a) {
+template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, int NSUB, int PFD, int NT>
+__global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
   constexpr bool QREG = KS_REG > 0;
   constexpr int KS = QREG ? KS_REG : 4;
   constexpr int TT = 16 * NSUB;
@@ -517,14 +517,15 @@ static size_t qlds_bytes(int dtype, int nqb, int nstep) {
   return (size_t)nqb * nstep * 2 * 64 * 16 * (dtype == TMS_DTYPE_F32 ? 2 : 1);
 }
 
-template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED>
-static int launch_one(const DenseArgs& a, int64_t grid, size_t lds, hipStream_t st) {
+template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED, int NT>
+static int launch_nt(const DenseArgs& a, int64_t waves, size_t lds, hipStream_t st) {
   // fp32 tiles hold twice the bytes per token: with Q in VGPRs, one 16-token row block
   // per tile keeps the bytes in flight per wave where the 16-bit path has them; with Q
   // in LDS (d > 128: its lo terms take up to 128 KiB, one or two workgroups per CU) two
   // blocks per tile keep more bytes in flight per wave (measured: +20 % at d = 768,
   // +12 % at d = 1000, within 4 % either way at d = 200 .. 512)
   constexpr int NS = DT == TMS_DTYPE_F32 ? (KS_REG > 0 ? TMS_DENSE_F32_NSUB : TMS_DENSE_F32_LDS_NSUB) : kNSub;
+  const int64_t grid = (waves + NT / 64 - 1) / (NT / 64);
   if (lds > 64 * 1024) {
     int dev = 0, cap = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -534,27 +535,39 @@ static int launch_one(const DenseArgs& a, int64_t grid, size_t lds, hipStream_t 
       return fail(TMS_ERR_UNSUPPORTED, "dense_maxsim_kernel: query fragments need %zu bytes of LDS, the device has %d",
                   lds, cap);
   }
-  hipLaunchKernelGGL((dense_maxsim_kernel<DT, MODE, NQB, KS_REG, FULL, ALIGNED, NS, TMS_DENSE_PFD>),
-                     dim3((unsigned)grid), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((dense_maxsim_kernel<DT, MODE, NQB, KS_REG, FULL, ALIGNED, NS, TMS_DENSE_PFD, NT>),
+                     dim3((unsigned)grid), dim3(NT), lds, st, a);
   return check_launch("dense_maxsim_kernel");
 }
 
+// fp32 with Q in LDS above 80 KiB (d >= 768: the query's hi and lo terms leave room for
+// one workgroup per CU): 8-wave workgroups, so the CU still holds two waves per SIMD
+// (d = 768: 5.2 -> 5.8 TB/s, d = 1000: 4.5 -> 5.1 TB/s). Below that, 4-wave
+// workgroups (8-wave ones measured 5 % slower at d = 200 and 512).
+template <int DT, int MODE, int NQB, int KS_REG, bool FULL, bool ALIGNED>
+static int launch_one(const DenseArgs& a, int64_t waves, size_t lds, hipStream_t st) {
+  if constexpr (DT == TMS_DTYPE_F32 && KS_REG == 0) {
+    if (lds > 80 * 1024) return launch_nt<DT, MODE, NQB, KS_REG, FULL, ALIGNED, 512>(a, waves, lds, st);
+  }
+  return launch_nt<DT, MODE, NQB, KS_REG, FULL, ALIGNED, 256>(a, waves, lds, st);
+}
+
 template <int DT, int MODE, int NQB>
-static int launch_nqb(const DenseArgs& a, bool aligned, int64_t grid, hipStream_t st) {
+static int launch_nqb(const DenseArgs& a, bool aligned, int64_t waves, hipStream_t st) {
   const bool full = aligned && (a.d % 32 == 0);
   if (aligned && a.d > 0 && a.d <= 128 && a.d % 32 == 0) {
     switch (a.d / 32) {
-      case 1: return launch_one<DT, MODE, NQB, 1, true, true>(a, grid, 0, st);
-      case 2: return launch_one<DT, MODE, NQB, 2, true, true>(a, grid, 0, st);
-      case 3: return launch_one<DT, MODE, NQB, 3, true, true>(a, grid, 0, st);
-      default: return launch_one<DT, MODE, NQB, 4, true, true>(a, grid, 0, st);
+      case 1: return launch_one<DT, MODE, NQB, 1, true, true>(a, waves, 0, st);
+      case 2: return launch_one<DT, MODE, NQB, 2, true, true>(a, waves, 0, st);
+      case 3: return launch_one<DT, MODE, NQB, 3, true, true>(a, waves, 0, st);
+      default: return launch_one<DT, MODE, NQB, 4, true, true>(a, waves, 0, st);
     }
   }
   size_t lds = qlds_bytes(DT, NQB, a.nstep);
   if (lds == 0) lds = 16;
-  if (full) return launch_one<DT, MODE, NQB, 0, true, true>(a, grid, lds, st);
-  if (aligned) return launch_one<DT, MODE, NQB, 0, false, true>(a, grid, lds, st);
-  return launch_one<DT, MODE, NQB, 0, false, false>(a, grid, lds, st);
+  if (full) return launch_one<DT, MODE, NQB, 0, true, true>(a, waves, lds, st);
+  if (aligned) return launch_one<DT, MODE, NQB, 0, false, true>(a, waves, lds, st);
+  return launch_one<DT, MODE, NQB, 0, false, false>(a, waves, lds, st);
 }
 
 // Documents per wave: short waves (about TMS_DENSE_TOKENS_PER_WAVE tokens, i.e. one
@@ -575,7 +588,6 @@ template <int DT>
 static int run_dense(DenseArgs a, int64_t nQ, int mode, bool aligned, hipStream_t st) {
   const int64_t nblocks_total = nQ * (int64_t)a.nbq;
   const int64_t waves = (a.B + a.docs_per_wave - 1) / a.docs_per_wave;
-  const int64_t grid = (waves + 3) / 4;
   // Blocks per launch: two when Q fits in VGPRs or its LDS copy stays small.
   int maxq = 2;
   if (!(aligned && a.d > 0 && a.d <= 128 && a.d % 32 == 0) && qlds_bytes(DT, 2, a.nstep) > (size_t)kMaxQldsBytes)
@@ -585,13 +597,13 @@ static int run_dense(DenseArgs a, int64_t nQ, int mode, bool aligned, hipStream_
     a.nblk = (int32_t)((nblocks_total - blk0 < maxq) ? nblocks_total - blk0 : maxq);
     int rc;
     if (a.nblk == 2) {
-      if (mode == MODE_FIXED) rc = launch_nqb<DT, MODE_FIXED, 2>(a, aligned, grid, st);
-      else if (mode == MODE_VARLEN) rc = launch_nqb<DT, MODE_VARLEN, 2>(a, aligned, grid, st);
-      else rc = launch_nqb<DT, MODE_MASKED, 2>(a, aligned, grid, st);
+      if (mode == MODE_FIXED) rc = launch_nqb<DT, MODE_FIXED, 2>(a, aligned, waves, st);
+      else if (mode == MODE_VARLEN) rc = launch_nqb<DT, MODE_VARLEN, 2>(a, aligned, waves, st);
+      else rc = launch_nqb<DT, MODE_MASKED, 2>(a, aligned, waves, st);
     } else {
-      if (mode == MODE_FIXED) rc = launch_nqb<DT, MODE_FIXED, 1>(a, aligned, grid, st);
-      else if (mode == MODE_VARLEN) rc = launch_nqb<DT, MODE_VARLEN, 1>(a, aligned, grid, st);
-      else rc = launch_nqb<DT, MODE_MASKED, 1>(a, aligned, grid, st);
+      if (mode == MODE_FIXED) rc = launch_nqb<DT, MODE_FIXED, 1>(a, aligned, waves, st);
+      else if (mode == MODE_VARLEN) rc = launch_nqb<DT, MODE_VARLEN, 1>(a, aligned, waves, st);
+      else rc = launch_nqb<DT, MODE_MASKED, 1>(a, aligned, waves, st);
     }
     if (rc != TMS_OK) return rc;
   }
