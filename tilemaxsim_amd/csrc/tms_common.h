@@ -58,6 +58,12 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
   }
 }
 
+// Stores the quiet-NaN score of an invalid document as an integer. Device code is built
+// with -fno-honor-nans, under which a NaN that passes through any float operation
+// (an add, a select, a max) is undefined, so the marker never enters float arithmetic:
+// kernels carry "invalid" as an integer flag and this is the document's final write.
+__device__ __forceinline__ void store_nan_score(float* p) { *(uint32_t*)p = 0x7fc00000u; }
+
 // A value the whole wave shares, moved to scalar registers (so control flow that depends
 // on it is uniform to the compiler).
 __device__ __forceinline__ int64_t wave_uniform(int64_t x) {

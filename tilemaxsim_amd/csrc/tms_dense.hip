@@ -229,6 +229,19 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
     for (int j = 0; j < NQB; j++) blk[j] = v;  // every block in range holds a real token
     write_doc(b, blk);
   };
+  // A document with invalid offsets scores NaN for every query of the launch, written
+  // as an integer (every launch over it writes the same bits, with no float arithmetic).
+  auto write_bad = [&](int64_t b) {
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < NQB; j++) {
+        if (j >= my_nblk) break;
+        const int jb = my_blk0 + j;
+        const int qi = jb / a.nbq;
+        if (j == my_nblk - 1 || (jb + 1) / a.nbq != qi) store_nan_score(a.out + (int64_t)qi * a.B + b);
+      }
+    }
+  };
 
   // ---- document cursor -------------------------------------------------------
   auto doc_info = [&](int64_t b, int64_t& base, bool& bad) -> int64_t {
@@ -263,7 +276,8 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
         return;
       }
       // an empty document zero-padded to pad_len > 0 tokens has every max equal to 0
-      write_empty(b, bad ? __builtin_nanf("") : (a.pad_len > 0 ? 0.f : NEG_INF));
+      if (bad) write_bad(b);
+      else write_empty(b, a.pad_len > 0 ? 0.f : NEG_INF);
     }
     c.b = b_end;
   };

@@ -293,7 +293,11 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
         c.t0 = 0;
         return;
       }
-      write(b, len < 0 ? __builtin_bit_cast(float, 0x7fc00000u) : (a.pad_len > 0 ? 0.f : NEG_INF));
+      if (len < 0) {  // invalid pid or offsets: NaN, written as an integer by every launch
+        if (lane == 0) store_nan_score(a.out + b);
+      } else {
+        write(b, a.pad_len > 0 ? 0.f : NEG_INF);
+      }
     }
     c.b = b_end;
   };
@@ -529,8 +533,8 @@ __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_ker
         c.t0 = 0;
         return;
       }
-      if (record) {
-        const float v = len < 0 ? __builtin_bit_cast(float, 0x7fc00000u) : (a.pad_len > 0 ? 0.f : NEG_INF);
+      if (record) {  // invalid pid or offsets (len < 0): the final store writes NaN for the lane
+        const float v = a.pad_len > 0 ? 0.f : NEG_INF;
 #pragma unroll
         for (int j = 0; j < NB; j++) pend[j] = lane == (int)(b - b_begin) ? v : pend[j];
       }
@@ -726,7 +730,9 @@ __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_ker
       const int qi = jb / a.nbq;
       s += pend[j];
       if (j == my_nblk - 1 || (jb + 1) / a.nbq != qi) {  // the query's last block
-        a.out[(int64_t)qi * a.B + b] = s;
+        float* o = a.out + (int64_t)qi * a.B + b;
+        if (dlen < 0) store_nan_score(o);  // invalid pid or offsets
+        else *o = s;
         s = 0.f;
       }
     }

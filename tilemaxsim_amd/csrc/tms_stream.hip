@@ -376,8 +376,8 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
         c.t0 = 0;
         return;
       }
-      if (record) {
-        const float v = len < 0 ? __builtin_bit_cast(float, 0x7fc00000u) : (a.pad_len > 0 ? 0.f : NEG_INF);
+      if (record) {  // invalid offsets (len < 0): the final store writes NaN for the lane
+        const float v = a.pad_len > 0 ? 0.f : NEG_INF;
 #pragma unroll
         for (int j = 0; j < NB; j++) pend[j] = lane == (int)(b - b_begin) ? v : pend[j];
       }
@@ -513,7 +513,9 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
       const int qi = jb / a.nbq;
       s += pend[j];
       if (j == my_nblk - 1 || (jb + 1) / a.nbq != qi) {  // the query's last block
-        a.out[(int64_t)qi * a.B + b] = s;
+        float* o = a.out + (int64_t)qi * a.B + b;
+        if (dlen < 0) store_nan_score(o);  // invalid offsets
+        else *o = s;
         s = 0.f;
       }
     }
