@@ -238,8 +238,12 @@ def pq_decompress_score(Q: np.ndarray, codebook: np.ndarray, codes: np.ndarray, 
 def topk(scores: np.ndarray, k: int):
     """Top-k (values descending, int64 indices) of a 1-D score vector, as the
     reference's callers take with ``torch.topk`` (``src/cycle3_experiments.py:215``).
-    Ties are broken by the lower index."""
+    Ties are broken by the lower index; -0.0 and +0.0 are equal (a tie), and every NaN,
+    whatever its sign bit, ranks above +inf, as ``torch.topk`` orders NaN."""
     s = np.asarray(scores)
     k = min(k, s.shape[0])
-    order = np.lexsort((np.arange(s.shape[0]), -s.astype(np.float64)))[:k]
+    s64 = s.astype(np.float64)
+    nan = np.isnan(s64)
+    # lexsort: last key first -- NaN first, then value descending, then index ascending
+    order = np.lexsort((np.arange(s.shape[0]), -np.where(nan, 0.0, s64), ~nan))[:k]
     return s[order], order.astype(np.int64)

@@ -71,6 +71,41 @@ def test_topk_rows_ties_nan_inf(cuda):
         _check_row(v[r], i[r], rows[r], 100)
 
 
+def test_topk_signed_zeros_and_sign_bit_nan(cuda):
+    """Keys are canonicalised: -0.0 ties with +0.0 by index, also at the k-th position,
+    and a NaN with its sign bit set ranks above +inf like any NaN; the values keep the
+    input's bits."""
+    import torch
+    from tilemaxsim_amd import topk
+    rng = np.random.default_rng(5)
+    n, k = 20000, 100
+    rows = np.abs(rng.standard_normal((4, n))).astype(np.float32) + 1.0
+    # row 0: 60 values above zero, then zeros of both signs straddle the k-th position
+    rows[0, :] = -1.0 - np.abs(rng.standard_normal(n)).astype(np.float32)
+    rows[0, rng.choice(n, 60, replace=False)] = 5.0
+    zpos = rng.choice(np.flatnonzero(rows[0] < 0), 80, replace=False)
+    rows[0, zpos] = np.where(np.arange(80) % 2 == 0, np.float32(-0.0), np.float32(0.0))
+    # row 1: sign-bit NaN, +NaN and +inf
+    neg_nan = np.array([0xFFC00000], dtype=np.uint32).view(np.float32)[0]
+    rows[1, 777] = neg_nan
+    rows[1, 10] = np.inf
+    rows[1, 15000] = np.nan
+    # row 2: the same across several chunks (the multi-level path), zeros at the boundary
+    rows[2, :] = -3.0
+    rows[2, rng.choice(n, 99, replace=False)] = 2.0
+    rows[2, 4096 * 3 + 5] = -0.0
+    rows[2, 4096 * 1 + 9] = 0.0
+    rows[3, 4096 * 2] = -neg_nan  # +NaN with a payload-free bit pattern
+    rows[3, 1] = neg_nan
+    v, i = topk(torch.from_numpy(rows).cuda(), k)
+    v, i = v.cpu().numpy(), i.cpu().numpy()
+    for r in range(4):
+        _check_row(v[r], i[r], rows[r], k)
+    assert i[1, 0] == 777 and i[1, 1] == 15000 and i[1, 2] == 10
+    assert v[1].view(np.uint32)[0] == 0xFFC00000  # the input's own NaN bits
+    assert i[2, 99] == 4096 * 1 + 9  # +0.0 at index 4105 before -0.0 at 12293
+
+
 def test_maxsim_topk_end_to_end(cuda):
     import torch
     from tilemaxsim_amd import maxsim_topk

@@ -247,6 +247,18 @@ def test_topk_matches_brute_force_and_sort(n, k):
     assert rest.size == 0 or rest.max() <= v.min()  # nothing left out beats what was kept
 
 
+def test_topk_signed_zero_and_nan():
+    """-0.0 ties with +0.0 (by index), and a NaN of either sign ranks above +inf."""
+    neg_nan = np.array([0xFFC00000], dtype=np.uint32).view(np.float32)[0]
+    x = np.array([1.0, -0.0, 0.0, -0.0, np.inf, neg_nan, -1.0, np.nan], dtype=np.float32)
+    v, i = orc.topk(x, 8)
+    assert i.tolist() == [5, 7, 4, 0, 1, 2, 3, 6]
+    assert np.signbit(v[4]) and not np.signbit(v[5]) and np.signbit(v[6])  # values keep their bits
+    # brute force over the same rule (NaN -> above +inf; -0.0 == 0.0)
+    key = [(0 if np.isnan(t) else 1, -float(t) if not np.isnan(t) else 0.0, j) for j, t in enumerate(x)]
+    assert [j for *_, j in sorted(key)] == i.tolist()
+
+
 def test_planted_topk_mistakes_are_caught():
     x = np.array([2.0, 5.0, 5.0, 1.0, 5.0, 3.0], dtype=np.float32)
     bv, bi = _brute_topk(x, 4)

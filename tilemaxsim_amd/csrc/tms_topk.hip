@@ -23,13 +23,14 @@ constexpr int kChunk = 4096;  // keys sorted per workgroup (32 KiB of LDS)
 constexpr int kTopkThreads = 256;
 constexpr int kMaxK = kChunk / 4;
 
+// Order-preserving image of a float's bits. -0.0 is taken as +0.0 (they compare equal,
+// so they tie and go by index) and every NaN as the positive quiet NaN, so that a NaN
+// with its sign bit set (x86's default NaN, or a negated one) still ranks above +inf.
 __device__ __forceinline__ uint32_t order_key(float f) {
-  const uint32_t b = __builtin_bit_cast(uint32_t, f);
+  uint32_t b = __builtin_bit_cast(uint32_t, f);
+  b = (b == 0x80000000u) ? 0u : b;
+  b = ((b & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : b;
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-__device__ __forceinline__ float key_value(uint32_t k) {
-  const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-  return __builtin_bit_cast(float, b);
 }
 
 // FIRST: input is fp32 scores (row stride in_stride), indices are positions in the row.
@@ -38,8 +39,10 @@ __device__ __forceinline__ float key_value(uint32_t k) {
 constexpr int kPerThread = kChunk / kTopkThreads;  // 16 keys per thread
 static_assert(kTopkThreads == 256, "one histogram bin per thread; wave 0 scans four bins per lane");
 
+// The values written by the LAST level are read back from the scores (vals, row stride
+// val_stride) at the selected indices, so they keep the input's bits (-0.0, NaN payloads).
 template <bool FIRST, bool LAST>
-__global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* __restrict__ vals,
+__global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* __restrict__ vals, int64_t val_stride,
                                                                   const uint64_t* __restrict__ keys_in, int64_t n_in,
                                                                   int64_t in_stride, uint64_t* __restrict__ keys_out,
                                                                   int64_t out_stride, float* __restrict__ out_vals,
@@ -58,7 +61,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
     key[e] = 0;  // below every real element
     if (p < n_in) {
       if constexpr (FIRST) {
-        key[e] = ((uint64_t)order_key(vals[row * in_stride + p]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)p);
+        key[e] = ((uint64_t)order_key(vals[row * val_stride + p]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)p);
       } else {
         key[e] = keys_in[row * in_stride + p];
       }
@@ -152,9 +155,10 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
       }
     }
     for (int i = tid; i < k; i += kTopkThreads) {
-      const uint64_t kv = sel[i];
-      out_vals[row * k + i] = key_value((uint32_t)(kv >> 32));
-      out_idx[row * k + i] = (int64_t)(0xffffffffu - (uint32_t)kv);
+      const int64_t idx = (int64_t)(0xffffffffu - (uint32_t)sel[i]);
+      // a selected key is always a real element (k <= n); the clamp only bounds the read
+      out_vals[row * k + i] = vals[row * val_stride + (idx < val_stride ? idx : val_stride - 1)];
+      out_idx[row * k + i] = idx;
     }
   }
 }
@@ -182,6 +186,11 @@ static int64_t workspace_bytes(int64_t nrows, int64_t n, int k) {
   return (a + b) * nrows * (int64_t)sizeof(uint64_t);
 }
 
+static int topk_checks(const char* fn, const float* scores, int64_t nrows, int64_t n, int64_t k,
+                       const float* out_values, const int64_t* out_indices);
+static int topk_run(const float* scores, int64_t nrows, int64_t n, int64_t k, void* workspace, float* out_values,
+                    int64_t* out_indices, hipStream_t st);
+
 }  // namespace tms
 
 using namespace tms;
@@ -196,6 +205,21 @@ int64_t tms_topk_workspace_size(int64_t nrows, int64_t n, int64_t k) {
 int tms_topk(const float* scores, int64_t nrows, int64_t n, int64_t k, void* workspace, int64_t workspace_bytes_,
              float* out_values, int64_t* out_indices, void* stream) {
   const char* fn = "tms_topk";
+  int rc = topk_checks(fn, scores, nrows, n, k, out_values, out_indices);
+  if (rc != TMS_OK || nrows == 0 || k == 0) return rc;
+  const int64_t need = workspace_bytes(nrows, n, (int)k);
+  if (need > 0 && (!workspace || workspace_bytes_ < need))
+    return fail(TMS_ERR_INVALID, "%s: workspace of %lld bytes needed, got %lld", fn, (long long)need,
+                (long long)workspace_bytes_);
+  return topk_run(scores, nrows, n, k, workspace, out_values, out_indices, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace tms {
+
+static int topk_checks(const char* fn, const float* scores, int64_t nrows, int64_t n, int64_t k,
+                       const float* out_values, const int64_t* out_indices) {
   if (nrows < 0 || n < 0 || k < 0) return fail(TMS_ERR_INVALID, "%s: negative size", fn);
   if (k > n) return fail(TMS_ERR_INVALID, "%s: k=%lld exceeds the row length %lld", fn, (long long)k, (long long)n);
   if (k > kMaxK) return fail(TMS_ERR_UNSUPPORTED, "%s: k=%lld > %d is not supported", fn, (long long)k, kMaxK);
@@ -203,11 +227,12 @@ int tms_topk(const float* scores, int64_t nrows, int64_t n, int64_t k, void* wor
   if (nrows > 65535) return fail(TMS_ERR_UNSUPPORTED, "%s: more than 65535 rows per call", fn);
   if (nrows == 0 || k == 0) return TMS_OK;
   if (!scores || !out_values || !out_indices) return fail(TMS_ERR_INVALID, "%s: NULL pointer", fn);
-  const int64_t need = workspace_bytes(nrows, n, (int)k);
-  if (need > 0 && (!workspace || workspace_bytes_ < need))
-    return fail(TMS_ERR_INVALID, "%s: workspace of %lld bytes needed, got %lld", fn, (long long)need,
-                (long long)workspace_bytes_);
-  hipStream_t st = (hipStream_t)stream;
+  return TMS_OK;
+}
+
+// The levels of one call; `workspace` holds workspace_bytes(nrows, n, k) bytes.
+static int topk_run(const float* scores, int64_t nrows, int64_t n, int64_t k, void* workspace, float* out_values,
+                    int64_t* out_indices, hipStream_t st) {
   int64_t sizes[64];
   const int64_t lv = level_sizes(n, (int)k, sizes, 64);
   int64_t amax = 0;
@@ -218,13 +243,13 @@ int tms_topk(const float* scores, int64_t nrows, int64_t n, int64_t k, void* wor
 
   const dim3 block(kTopkThreads);
   if (lv == 0) {
-    hipLaunchKernelGGL((topk_level_kernel<true, true>), dim3(1, (unsigned)nrows), block, 0, st, scores, nullptr, n, n,
-                       nullptr, 0, out_values, out_indices, (int)k);
+    hipLaunchKernelGGL((topk_level_kernel<true, true>), dim3(1, (unsigned)nrows), block, 0, st, scores, n, nullptr, n,
+                       n, nullptr, 0, out_values, out_indices, (int)k);
     return check_launch("topk_level_kernel");
   }
   // level 0: scores -> keys
   hipLaunchKernelGGL((topk_level_kernel<true, false>), dim3((unsigned)ceil_div(n, kChunk), (unsigned)nrows), block, 0,
-                     st, scores, nullptr, n, n, bufs[0], strides[0], nullptr, nullptr, (int)k);
+                     st, scores, n, nullptr, n, n, bufs[0], strides[0], nullptr, nullptr, (int)k);
   int rc = check_launch("topk_level_kernel");
   if (rc) return rc;
   for (int64_t i = 1; i <= lv; i++) {
@@ -232,12 +257,12 @@ int tms_topk(const float* scores, int64_t nrows, int64_t n, int64_t k, void* wor
     const uint64_t* in = bufs[(i - 1) % 2];
     const int64_t in_stride = strides[(i - 1) % 2];
     if (i == lv) {
-      hipLaunchKernelGGL((topk_level_kernel<false, true>), dim3(1, (unsigned)nrows), block, 0, st, nullptr, in, n_in,
-                         in_stride, nullptr, 0, out_values, out_indices, (int)k);
+      hipLaunchKernelGGL((topk_level_kernel<false, true>), dim3(1, (unsigned)nrows), block, 0, st, scores, n, in,
+                         n_in, in_stride, nullptr, 0, out_values, out_indices, (int)k);
     } else {
       hipLaunchKernelGGL((topk_level_kernel<false, false>), dim3((unsigned)ceil_div(n_in, kChunk), (unsigned)nrows),
-                         block, 0, st, nullptr, in, n_in, in_stride, bufs[i % 2], strides[i % 2], nullptr, nullptr,
-                         (int)k);
+                         block, 0, st, scores, n, in, n_in, in_stride, bufs[i % 2], strides[i % 2], nullptr,
+                         nullptr, (int)k);
     }
     rc = check_launch("topk_level_kernel");
     if (rc) return rc;
@@ -245,4 +270,4 @@ int tms_topk(const float* scores, int64_t nrows, int64_t n, int64_t k, void* wor
   return TMS_OK;
 }
 
-}  // extern "C"
+}  // namespace tms
