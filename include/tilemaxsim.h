@@ -160,6 +160,23 @@ int tms_topk(const float* scores, int64_t nrows, int64_t n, int64_t k, void* wor
 int64_t tms_topk_workspace_size(int64_t nrows, int64_t n, int64_t k);
 
 /*
+ * tms_topk without a workspace argument: allocates nothing and takes no caller memory
+ * beyond its inputs and outputs. No counterpart in the reference; it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The intermediate keys live in a fixed 32 MiB device
+ * array of the library (TMS_TOPK_SCRATCH_BYTES; one copy per GPU, held until the process
+ * ends), whose address is looked up on the first call on each device: the calling
+ * thread's current device must be the one that holds the pointers and the stream. Sizes
+ * whose tms_topk_workspace_size() exceeds that return TMS_ERR_UNSUPPORTED (split the rows
+ * over several calls). Every call on one GPU shares its array: calls that overlap on
+ * one GPU (different streams, or host threads, with no ordering between them) race, and
+ * must be serialised by the caller. Results equal tms_topk's bit for bit.
+ */
+#define TMS_TOPK_SCRATCH_BYTES (32LL << 20)
+int tms_topk_noalloc(const float* scores, int64_t nrows, int64_t n, int64_t k, float* out_values,
+                     int64_t* out_indices, void* stream);
+
+/*
  * Residual-compressed documents: the ColBERTv2 codec (ResidualCodec in
  * colbert/indexing/codecs/residual.py) of colbert-ai 0.2.22, the ColBERT release the
  * reference's PLAID drop-in is written against (src/plaid_integration_benchmark.py:23).

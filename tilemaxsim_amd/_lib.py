@@ -40,6 +40,7 @@ SIGNATURES = {
     "tms_pq_score": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tms_topk": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p],
     "tms_topk_workspace_size": [_i64, _i64, _i64],
+    "tms_topk_noalloc": [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p],
     "tms_residual_decompress": [_c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _int, _c_void_p,
                                 _c_void_p],
     "tms_maxsim_residual": [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p, _int, _c_void_p, _c_void_p, _i64,
