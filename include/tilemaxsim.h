@@ -36,6 +36,14 @@ extern "C" {
  * every product is formed from three bf16 products, so its relative error is at most
  * about 3 * 2^-16 (the reference computes fp32 inputs with TF32 tl.dot, about 2^-10). */
 #define TMS_DTYPE_F32 2
+/* OR-ed into the dtype of a dense entry point (tms_maxsim_*), of tms_pq_build_lut or of
+ * tms_pq_score: Q is fp32 while the documents / codebook are the fp16 or bf16 `dtype`.
+ * The query is not rounded to 16 bits: each element is split into hi + lo terms of the
+ * document type (fp16: after a per-token power-of-two scale, which the max commutes
+ * with) and a product takes two MFMAs, relative error about 2^-17 (bf16) or 2^-21
+ * (fp16) per element; the reference computes fp32 x 16-bit products with TF32 tl.dot
+ * (2^-11). Redundant with TMS_DTYPE_F32 documents, whose queries are fp32 already. */
+#define TMS_QUERY_F32 0x100
 
 /* Library version (major * 10000 + minor * 100 + patch). */
 int tms_version(void);

@@ -66,8 +66,8 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     rc, _ = _c_call("tms_maxsim_dense", None, 32, 128, None, 0, 5, 0, None, None)
     assert rc == 0
     # d beyond the supported width
-    rc, msg = _c_call("tms_maxsim_dense", 16, 32, 4096, 16, 10, 5, 0, 16, None)
-    assert rc == 2 and "1024" in msg
+    rc, msg = _c_call("tms_maxsim_dense", 16, 32, 70000, 16, 10, 5, 0, 16, None)
+    assert rc == 2 and "65536" in msg
     # varlen without offsets
     rc, msg = _c_call("tms_maxsim_varlen", 16, 32, 128, 16, 100, None, 10, 0, 16, None)
     assert rc == 1 and "offsets" in msg

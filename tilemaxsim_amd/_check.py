@@ -7,6 +7,8 @@ from __future__ import annotations
 
 import torch
 
+from . import _lib
+
 
 def tensor(name: str, t) -> None:
     if not isinstance(t, torch.Tensor):
@@ -45,3 +47,25 @@ def query_like(Q: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     if Q.dtype != dtype:
         Q = Q.to(dtype)
     return Q.contiguous()
+
+
+def query_for(Q: torch.Tensor, dtype: torch.dtype) -> tuple[torch.Tensor, int]:
+    """The query as the kernels take it against documents (or a codebook) of ``dtype``,
+    and the C dtype code to pass with it.
+
+    A query of the documents' dtype is used as it is. Against fp32 documents any float
+    query becomes fp32. Against fp16 / bf16 documents a query of another float dtype
+    becomes fp32 (exactly, for a 16-bit query) and the code carries ``TMS_QUERY_F32``:
+    the kernels then split each element into two 16-bit terms instead of rounding it to
+    the documents' type, as the reference computes such a pair in fp32 / TF32
+    (``src/flash_maxsim_v2.py:99,111,117``).
+    """
+    if not Q.is_floating_point():
+        raise TypeError(f"Q must be a floating-point tensor (got {Q.dtype})")
+    code = _lib.dtype_code(dtype)
+    if Q.dtype == dtype:
+        return Q.contiguous(), code
+    Qf = Q.to(torch.float32).contiguous()
+    if dtype == torch.float32:
+        return Qf, code
+    return Qf, code | _lib.TMS_QUERY_F32

@@ -21,6 +21,7 @@ TMS_ERR_HIP = 3
 TMS_DTYPE_F16 = 0
 TMS_DTYPE_BF16 = 1
 TMS_DTYPE_F32 = 2
+TMS_QUERY_F32 = 0x100  # OR-ed into a 16-bit dtype: Q is fp32 (split into two 16-bit terms, not rounded)
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64

@@ -46,6 +46,46 @@ __device__ __forceinline__ void split_bf16(u32x8 x, u32x4& hi, u32x4& lo) {
   }
 }
 
+// fp32 query elements -> two fp16 terms of x * scale: hi = fp16(xs), lo = fp16(xs - hi),
+// both rounded to nearest even (xs - hi is exact in fp32). `scale` is the token's power
+// of two from pow2_scale, which puts its largest |x| in [2^14, 2^15): hi never overflows,
+// and |xs - hi - lo| <= 2^-22 |xs| + 2^-25 (the last term is fp16's subnormal spacing,
+// 2^-39 of the token's largest element). Scaling by a power of two is exact, and a
+// positive per-token factor commutes with the max over document tokens, so the running
+// max is taken on scaled dot products and multiplied by 1 / scale before the sum.
+__device__ __forceinline__ void split_f16(u32x8 x, float scale, u32x4& hi, u32x4& lo) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t x0 = x[2 * i], x1 = x[2 * i + 1];
+    const float a = __builtin_bit_cast(float, x0) * scale, b = __builtin_bit_cast(float, x1) * scale;
+    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    const _Float16 la = (_Float16)(a - (float)ha), lb = (_Float16)(b - (float)hb);
+    hi[i] = (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+    lo[i] = (uint32_t)__builtin_bit_cast(uint16_t, la) | ((uint32_t)__builtin_bit_cast(uint16_t, lb) << 16);
+  }
+}
+
+// The power of two 2^s that maps amax = f * 2^e (f in [0.5, 1)) into [2^14, 2^15):
+// s = 15 - e, clamped to [-126, 126] so that 2^s and 2^-s (returned in inv) are normal.
+__device__ __forceinline__ float pow2_scale(float amax, float& inv) {
+  const int be = (int)((__builtin_bit_cast(uint32_t, amax) >> 23) & 0xffu);  // 0 for 0 and subnormals
+  int s = 15 - (be - 126);
+  s = s < -126 ? -126 : (s > 126 ? 126 : s);
+  inv = __builtin_bit_cast(float, (uint32_t)(127 - s) << 23);
+  return __builtin_bit_cast(float, (uint32_t)(127 + s) << 23);
+}
+
+// Largest |x| over eight fp32 elements.
+__device__ __forceinline__ float absmax8(u32x8 x) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t xi = x[i];
+    m = fmaxf(m, __builtin_bit_cast(float, xi & 0x7fffffffu));
+  }
+  return m;
+}
+
 // One v_mfma_f32_16x16x32_{f16,bf16}: C(16x16 f32) += A(16x32) * B(32x16).
 // Lane l holds A[row l%16][k 8*(l/16) .. +8], B[k 8*(l/16) .. +8][col l%16] and
 // C[row 4*(l/16)+i][col l%16] for i = 0..3 (layout checked on the hardware).

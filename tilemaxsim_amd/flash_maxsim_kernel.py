@@ -85,7 +85,7 @@ def flash_maxsim_multi_doc(Q: torch.Tensor, D_flat: torch.Tensor, doc_offsets: t
     _check.on_gpu("Q", Q)
     _check.on_gpu("D_flat", D_flat)
     _check.same_device(Q=Q, D_flat=D_flat)
-    Q = _check.query_like(Q, D_flat.dtype)
+    Q, code = _check.query_for(Q, D_flat.dtype)
     offsets = doc_offsets.to(device=Q.device, dtype=torch.int64).contiguous()
     num_docs = offsets.shape[0] - 1
     if validate and num_docs > 0:
@@ -98,7 +98,7 @@ def flash_maxsim_multi_doc(Q: torch.Tensor, D_flat: torch.Tensor, doc_offsets: t
     lib = _lib.load()
     with _lib.on_device(Q.device):
         _lib.check(lib.tms_maxsim_varlen(Q.data_ptr(), Nq, d, D_flat.data_ptr(), T, offsets.data_ptr(), num_docs,
-                                         _lib.dtype_code(D_flat.dtype), scores.data_ptr(), _lib.stream_of(Q)))
+                                         code, scores.data_ptr(), _lib.stream_of(Q)))
     return scores
 
 
@@ -121,7 +121,7 @@ def _varlen_batched(fn: str, Qs: torch.Tensor, D_flat: torch.Tensor, doc_offsets
     _check.on_gpu("Qs", Qs)
     _check.on_gpu("D_flat", D_flat)
     _check.same_device(Qs=Qs, D_flat=D_flat)
-    Qs = _check.query_like(Qs, D_flat.dtype)
+    Qs, code = _check.query_for(Qs, D_flat.dtype)
     offsets = doc_offsets.to(device=Qs.device, dtype=torch.int64).contiguous()
     B = offsets.shape[0] - 1
     if (validate or zero_pad) and B > 0:
@@ -135,7 +135,7 @@ def _varlen_batched(fn: str, Qs: torch.Tensor, D_flat: torch.Tensor, doc_offsets
     lib = _lib.load()
     with _lib.on_device(Qs.device):
         _lib.check(lib.tms_maxsim_varlen_batched(Qs.data_ptr(), nQ, Nq, d, D_flat.data_ptr(), T, offsets.data_ptr(), B,
-                                                 pad_len, _lib.dtype_code(D_flat.dtype), out.data_ptr(),
+                                                 pad_len, code, out.data_ptr(),
                                                  _lib.stream_of(Qs)))
     return out
 
@@ -183,7 +183,7 @@ def maxsim_score(Q: torch.Tensor, D: torch.Tensor, D_mask: torch.Tensor | None =
     _check.on_gpu("D", D)
     _check.on_gpu("D_mask", D_mask)
     _check.same_device(Q=Q, D=D, D_mask=D_mask)
-    Q = _check.query_like(Q, D.dtype)
+    Q, code = _check.query_for(Q, D.dtype)
     mask = D_mask
     if mask.dtype != torch.uint8:
         mask = mask != 0
@@ -195,5 +195,5 @@ def maxsim_score(Q: torch.Tensor, D: torch.Tensor, D_mask: torch.Tensor | None =
     lib = _lib.load()
     with _lib.on_device(Q.device):
         _lib.check(lib.tms_maxsim_masked(Q.data_ptr(), Q.shape[0], d, D.data_ptr(), mask.data_ptr(), B, Nd,
-                                         _lib.dtype_code(D.dtype), scores.data_ptr(), _lib.stream_of(Q)))
+                                         code, scores.data_ptr(), _lib.stream_of(Q)))
     return scores

@@ -27,14 +27,14 @@ def _dense(Q: torch.Tensor, D: torch.Tensor, fn: str) -> torch.Tensor:
     _check.on_gpu("Q", Q)
     _check.on_gpu("D", D)
     _check.same_device(Q=Q, D=D)
-    Q = _check.query_like(Q, D.dtype)
+    Q, code = _check.query_for(Q, D.dtype)
     scores = torch.empty(B, dtype=torch.float32, device=Q.device)
     if B == 0:
         return scores
     lib = _lib.load()
     with _lib.on_device(Q.device):
-        _lib.check(lib.tms_maxsim_dense(Q.data_ptr(), Nq, d, D.data_ptr(), B, Nd, _lib.dtype_code(D.dtype),
-                                        scores.data_ptr(), _lib.stream_of(Q)))
+        _lib.check(lib.tms_maxsim_dense(Q.data_ptr(), Nq, d, D.data_ptr(), B, Nd, code, scores.data_ptr(),
+                                        _lib.stream_of(Q)))
     return scores
 
 
@@ -48,7 +48,9 @@ def flash_maxsim_v2_multiquery(Q: torch.Tensor, D: torch.Tensor) -> torch.Tensor
     and combines blocks with float atomics), and the result is deterministic.
 
     Args:
-        Q: (Nq, d) query token embeddings (cast to D's dtype on device).
+        Q: (Nq, d) query token embeddings. A query of another float dtype than D is
+            scored at fp32 precision (split into two 16-bit terms against fp16 / bf16
+            documents, never rounded to D's dtype).
         D: (B, Nd, d) document token embeddings, float16, bfloat16 or float32,
             contiguous (float32 is computed as bf16 hi + lo terms, relative error per
             product below 1e-4; the reference computes float32 with TF32 products).
@@ -86,12 +88,12 @@ def flash_maxsim_batched_queries(Qs: torch.Tensor, D: torch.Tensor) -> torch.Ten
     _check.on_gpu("Qs", Qs)
     _check.on_gpu("D", D)
     _check.same_device(Qs=Qs, D=D)
-    Qs = _check.query_like(Qs, D.dtype)
+    Qs, code = _check.query_for(Qs, D.dtype)
     out = torch.empty(nQ, B, dtype=torch.float32, device=Qs.device)
     if B == 0 or nQ == 0:
         return out
     lib = _lib.load()
     with _lib.on_device(Qs.device):
-        _lib.check(lib.tms_maxsim_dense_batched(Qs.data_ptr(), nQ, Nq, d, D.data_ptr(), B, Nd,
-                                                _lib.dtype_code(D.dtype), out.data_ptr(), _lib.stream_of(Qs)))
+        _lib.check(lib.tms_maxsim_dense_batched(Qs.data_ptr(), nQ, Nq, d, D.data_ptr(), B, Nd, code, out.data_ptr(),
+                                                _lib.stream_of(Qs)))
     return out
