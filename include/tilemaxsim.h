@@ -44,6 +44,11 @@ extern "C" {
  * (fp16) per element; the reference computes fp32 x 16-bit products with TF32 tl.dot
  * (2^-11). Redundant with TMS_DTYPE_F32 documents, whose queries are fp32 already. */
 #define TMS_QUERY_F32 0x100
+/* OR-ed into the dtype of tms_pq_score / tms_pq_score_batched: `codes` points to int16
+ * (TMS_CODES_I16) or int32 (TMS_CODES_I32) codes, read at that width, instead of uint8.
+ * Codes at or beyond K (or negative) are invalid input and are clamped into the table. */
+#define TMS_CODES_I16 0x200
+#define TMS_CODES_I32 0x400
 
 /* Library version (major * 10000 + minor * 100 + patch). */
 int tms_version(void);
@@ -115,7 +120,9 @@ int tms_maxsim_varlen_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t d,
 
 /*
  * PQ distance table lut[q, m, k] = sum_j Q[q, m*dsub + j] * codebook[m, k, j] (fp32;
- * fp16, bf16 or fp32 Q and codebook of one dtype). Replaces TileMaxSimPQ.build_distance_table (src/flash_pqsim_kernel.py:190-211) and
+ * fp16, bf16 or fp32 Q and codebook of one dtype, or with TMS_QUERY_F32 an fp32 Q
+ * against an fp16 / bf16 codebook, used unrounded). Replaces
+ * TileMaxSimPQ.build_distance_table (src/flash_pqsim_kernel.py:190-211) and
  * _build_distance_table_kernel (:31-67).
  */
 int tms_pq_build_lut(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
@@ -130,24 +137,40 @@ int tms_pq_score_lut(const float* lut, int64_t nq, int64_t M, int64_t K, const u
                      float* out, void* stream);
 
 /*
+ * tms_pq_score_lut for codes of code_bytes = 1, 2 or 4 bytes (uint8, int16, int32), read
+ * at their own width, and any K (the reference scores int32 codes with no K limit,
+ * src/flash_pqsim_kernel.py:219,233,161-165). Tables of M * K <= 16384 entries per query
+ * token are gathered from LDS slices of query tokens; larger ones from slices tiled over
+ * m as well, with per-token partial sums in registers (documents of up to 4096 tokens);
+ * tables with K > 16384, or longer documents, straight from memory. Codes at or beyond
+ * K are clamped into the table.
+ */
+int tms_pq_score_lut_ex(const float* lut, int64_t nq, int64_t M, int64_t K, const void* codes, int code_bytes,
+                        int64_t B, int64_t nd, float* out, void* stream);
+
+/*
  * PQ MaxSim by codebook gather: each document token is rebuilt from the codebook in
  * registers (never in HBM) and scored on MFMA; same scores as tms_pq_score_lut up to
  * fp32 summation order. Replaces TileMaxSimPQ.score_batch (src/flash_pqsim_kernel.py:
  * 213-252) as a whole. Shapes: d = M * dsub in {32, 64, 96, 128}, dsub in {2, 4, 8, 16,
- * 32}, M a multiple of 4, K <= 256, a codebook of at most 64 KiB, 16-byte aligned Q,
- * codebook and codes, nd * M < 2^31, and an fp16 or bf16 codebook; other shapes and
- * fp32 return TMS_ERR_UNSUPPORTED (score them with tms_pq_build_lut + tms_pq_score_lut).
+ * 32}, M a multiple of 4, a codebook of d * K 16-bit elements that fits the device's LDS
+ * (K <= 640 at d = 128 on gfx950's 160 KiB), 16-byte aligned Q, codebook and codes,
+ * nd * M * code bytes < 2^31, and an fp16 or bf16 codebook. dtype flags: TMS_QUERY_F32
+ * (fp32 Q, uint8 codes), TMS_CODES_I16 / TMS_CODES_I32. Other shapes and fp32 codebooks
+ * return TMS_ERR_UNSUPPORTED before any HIP call (score them with tms_pq_build_lut +
+ * tms_pq_score_lut_ex).
  */
 int tms_pq_score(const void* Q, int64_t nq, const void* codebook, int64_t M, int64_t K, int64_t dsub, int dtype,
                  const uint8_t* codes, int64_t B, int64_t nd, float* out, void* stream);
 
 /*
  * Batched-query PQ scoring: nQ queries of nq tokens (Qs is (nQ, nq, M*dsub)) against the
- * same uint8 codes; out is (nQ, B), row-major. Shapes as tms_pq_score (its MFMA path);
- * with at most 128 tokens per query, each 16-token tile is decoded once per pass (codes
- * gathered through the codebook in LDS) and shared by up to 32 query blocks of 32
- * tokens. Replaces nQ calls of TileMaxSimPQ.score_batch (src/flash_pqsim_kernel.py:213-252)
- * over the same codes.
+ * same codes; out is (nQ, B), row-major. Shapes and dtype flags as tms_pq_score; with
+ * uint8 codes, a query of the codebook's type, a codebook of at most 64 KiB and at most
+ * 128 tokens per query, each 16-token tile is decoded once per pass (codes gathered
+ * through the codebook in LDS) and shared by up to 32 query blocks of 32 tokens; other
+ * inputs are scored one query at a time. Replaces nQ calls of TileMaxSimPQ.score_batch
+ * (src/flash_pqsim_kernel.py:213-252) over the same codes.
  */
 int tms_pq_score_batched(const void* Qs, int64_t nQ, int64_t nq, const void* codebook, int64_t M, int64_t K,
                          int64_t dsub, int dtype, const uint8_t* codes, int64_t B, int64_t nd, float* out,

@@ -18,8 +18,9 @@ int main(void) {
   /* k larger than the row */
   if (tms_topk(out, 1, 4, 5, NULL, 0, out, NULL, NULL) != TMS_ERR_INVALID) return 5;
   if (tms_topk_workspace_size(1, 4096, 100) != 0) return 6;
-  /* PQ codes cannot index K > 256 */
-  if (tms_pq_score_lut((const float*)out, 32, 16, 300, NULL, 1, 1, out, NULL) != TMS_ERR_UNSUPPORTED) return 7;
+  /* PQ codes of 3 bytes (1, 2 and 4 are taken) */
+  if (tms_pq_score_lut_ex((const float*)out, 32, 16, 300, (const void*)out, 3, 1, 1, out, NULL) != TMS_ERR_INVALID)
+    return 7;
   /* residual format: nbits 3 */
   if (tms_residual_decompress(NULL, NULL, 1, (const void*)out, 1, 128, (const void*)out, 3, out, NULL) !=
       TMS_ERR_UNSUPPORTED)

@@ -45,6 +45,7 @@ def _c_call(name, *args):
 
 
 def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
+    from tilemaxsim_amd import _lib
     # negative sizes
     rc, msg = _c_call("tms_maxsim_dense", None, -1, 128, None, 10, 5, 0, None, None)
     assert rc == 1 and "negative" in msg
@@ -81,13 +82,19 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert rc == 1 and "pad_len" in msg
     rc, _ = _c_call("tms_maxsim_varlen_batched", 16, 0, 32, 128, 16, 100, 16, 10, 0, 0, None, None)
     assert rc == 0  # no queries
-    # PQ: K beyond uint8 codes, unsupported MFMA shape
-    rc, msg = _c_call("tms_pq_score", 16, 32, 16, 16, 300, 8, 0, 16, 10, 5, 16, None)
-    assert rc == 2 and "256" in msg
+    # PQ: unsupported MFMA shape; fp32 queries with int32 codes (no MFMA form); dtype flags
     rc, msg = _c_call("tms_pq_score", 16, 32, 16, 16, 256, 3, 0, 16, 10, 5, 16, None)
     assert rc == 2 and "tms_pq_score_lut" in msg
-    rc, msg = _c_call("tms_pq_score_lut", 16, 32, 1000, 256, 16, 10, 5, 16, None)
-    assert rc == 2 and "LDS" in msg
+    q32_i32 = _lib.TMS_DTYPE_F16 | _lib.TMS_QUERY_F32 | _lib.TMS_CODES_I32
+    rc, msg = _c_call("tms_pq_score", 16, 32, 16, 16, 256, 8, q32_i32, 16, 10, 5, 16, None)
+    assert rc == 2 and "uint8" in msg
+    rc, msg = _c_call("tms_pq_score", 16, 32, 16, 16, 256, 8, 2 | _lib.TMS_CODES_I16, 16, 10, 5, 16, None)
+    assert rc == 2 and "dtype 2" in msg  # fp32 codebooks take the table path, whatever the code width
+    # tms_pq_score_lut_ex(lut, nq, M, K, codes, code_bytes, B, nd, out, stream)
+    rc, msg = _c_call("tms_pq_score_lut_ex", 16, 32, 16, 256, 16, 3, 10, 5, 16, None)
+    assert rc == 1 and "code_bytes" in msg
+    rc, msg = _c_call("tms_pq_score_lut_ex", 16, 32, 1 << 16, 1 << 16, 16, 4, 10, 5, 16, None)
+    assert rc == 2 and "2^31" in msg
     # tms_pq_score_batched(Qs, nQ, nq, codebook, M, K, dsub, dtype, codes, B, nd, out, stream)
     rc, msg = _c_call("tms_pq_score_batched", 16, -2, 32, 16, 16, 256, 8, 0, 16, 10, 5, 16, None)
     assert rc == 1 and "negative" in msg

@@ -22,6 +22,8 @@ TMS_DTYPE_F16 = 0
 TMS_DTYPE_BF16 = 1
 TMS_DTYPE_F32 = 2
 TMS_QUERY_F32 = 0x100  # OR-ed into a 16-bit dtype: Q is fp32 (split into two 16-bit terms, not rounded)
+TMS_CODES_I16 = 0x200  # OR-ed into a PQ dtype: int16 codes
+TMS_CODES_I32 = 0x400  # OR-ed into a PQ dtype: int32 codes
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -38,6 +40,7 @@ SIGNATURES = {
     "tms_maxsim_dense_batched": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _int, _c_void_p, _c_void_p],
     "tms_pq_build_lut": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _c_void_p],
     "tms_pq_score_lut": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
+    "tms_pq_score_lut_ex": [_c_void_p, _i64, _i64, _i64, _c_void_p, _int, _i64, _i64, _c_void_p, _c_void_p],
     "tms_pq_score": [_c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _int, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "tms_topk": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p],
     "tms_topk_workspace_size": [_i64, _i64, _i64],

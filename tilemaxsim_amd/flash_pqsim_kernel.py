@@ -3,9 +3,10 @@
 
 ``build_distance_table`` runs ``tms_pq_build_lut``. ``score_batch`` runs the
 codebook-gather MFMA kernel (``tms_pq_score``) whenever the shape allows it and the
-reference's table-gather algorithm (``tms_pq_build_lut`` + ``tms_pq_score_lut``)
-otherwise; ``method=`` forces either one. Codes are read as uint8 in place (the
-reference makes an int32 copy of them first).
+reference's table-gather algorithm (``tms_pq_build_lut`` + ``tms_pq_score_lut_ex``)
+otherwise; ``method=`` forces either one. uint8, int16 and int32 codes are read in place
+at their own width (the reference makes an int32 copy of them first), and any K is
+accepted, as in the reference.
 """
 from __future__ import annotations
 
@@ -14,19 +15,20 @@ import torch
 from . import _check, _lib
 
 
-def _mfma_shape_ok(M: int, K: int, dsub: int, dtype: torch.dtype) -> bool:
-    d = M * dsub
-    return (dtype in (torch.float16, torch.bfloat16) and dsub in (2, 4, 8, 16, 32) and d % 32 == 0
-            and 0 < d <= 128 and M % 4 == 0 and 1 <= K <= 256 and d * K * 2 <= 64 * 1024)
+# Code element types read at their own width; other integer codes are converted to int32
+# (the reference converts every code tensor to int32, src/flash_pqsim_kernel.py:233).
+_CODE_FLAGS = {torch.uint8: 0, torch.int16: _lib.TMS_CODES_I16, torch.int32: _lib.TMS_CODES_I32}
+_CODE_BYTES = {torch.uint8: 1, torch.int16: 2, torch.int32: 4}
 
 
 class TileMaxSimPQ:
     """High-level PQ MaxSim scorer (``src/flash_pqsim_kernel.py:176-280``).
 
     Args:
-        codebook: (M, K, dsub) PQ centroids, float16, bfloat16 or float32, on the GPU.
-            A float32 codebook is scored by the table-gather kernel on an exact fp32
-            table (the MFMA kernel takes 16-bit centroids).
+        codebook: (M, K, dsub) PQ centroids, float16, bfloat16 or float32, on the GPU;
+            any K. A float32 codebook, or one too large for the LDS (d * K 16-bit
+            elements above 160 KiB), is scored by the table-gather kernel on an exact
+            fp32 table (the MFMA kernel takes 16-bit centroids).
     """
 
     def __init__(self, codebook: torch.Tensor):
@@ -38,17 +40,17 @@ class TileMaxSimPQ:
         self.codebook = codebook.contiguous()
         self.M, self.K, self.dsub = codebook.shape
         self.d = self.M * self.dsub
-        if self.K > 256:
-            raise NotImplementedError(f"K={self.K} > 256 centroids does not fit uint8 codes")
 
-    def _query(self, Q: torch.Tensor) -> torch.Tensor:
+    def _query(self, Q: torch.Tensor):
+        """The query as the kernels take it, and its dtype code (an fp32 query against a
+        16-bit codebook keeps its precision: ``TMS_QUERY_F32``)."""
         _check.tensor("Q", Q)
         if Q.dim() != 2:
             raise ValueError(f"Q must be (Nq, d), got shape {tuple(Q.shape)}")
         assert Q.shape[1] == self.d, f"Q width {Q.shape[1]} != M*dsub = {self.d}"
         _check.on_gpu("Q", Q)
         _check.same_device(Q=Q, codebook=self.codebook)
-        return _check.query_like(Q, self.codebook.dtype)
+        return _check.query_for(Q, self.codebook.dtype)
 
     def _codes(self, codes: torch.Tensor, validate: bool) -> torch.Tensor:
         if codes.dtype.is_floating_point or codes.dtype == torch.bool:
@@ -59,14 +61,11 @@ class TileMaxSimPQ:
             lo, hi = int(codes.min()), int(codes.max())
             if lo < 0 or hi >= self.K:
                 raise ValueError(f"codes must lie in [0, K={self.K}), found [{lo}, {hi}]")
-        if codes.dtype != torch.uint8:
-            codes = codes.to(torch.uint8)
+        if codes.dtype not in _CODE_FLAGS:
+            codes = codes.to(torch.int32)
         return codes.contiguous()
 
-    def build_distance_table(self, Q: torch.Tensor) -> torch.Tensor:
-        """Query-centroid table ``T[q, m, k] = Q[q, m*dsub:(m+1)*dsub] . C[m, k]`` in fp32
-        (``src/flash_pqsim_kernel.py:190-211``). Returns (Nq, M, K) float32."""
-        Q = self._query(Q)
+    def _table(self, Q: torch.Tensor, qcode: int) -> torch.Tensor:
         Nq = Q.shape[0]
         table = torch.empty(Nq, self.M, self.K, dtype=torch.float32, device=Q.device)
         if table.numel() == 0:
@@ -74,9 +73,15 @@ class TileMaxSimPQ:
         lib = _lib.load()
         with _lib.on_device(Q.device):
             _lib.check(lib.tms_pq_build_lut(Q.data_ptr(), Nq, self.codebook.data_ptr(), self.M, self.K, self.dsub,
-                                            _lib.dtype_code(self.codebook.dtype), table.data_ptr(),
-                                            _lib.stream_of(Q)))
+                                            qcode, table.data_ptr(), _lib.stream_of(Q)))
         return table
+
+    def build_distance_table(self, Q: torch.Tensor) -> torch.Tensor:
+        """Query-centroid table ``T[q, m, k] = Q[q, m*dsub:(m+1)*dsub] . C[m, k]`` in fp32
+        (``src/flash_pqsim_kernel.py:190-211``). Returns (Nq, M, K) float32. The query is
+        used in its own precision (an fp32 query is not rounded to the codebook's type)."""
+        Q, qcode = self._query(Q)
+        return self._table(Q, qcode)
 
     def score_batch(self, Q: torch.Tensor, codes: torch.Tensor, method: str = "auto",
                     validate: bool = True) -> torch.Tensor:
@@ -84,11 +89,14 @@ class TileMaxSimPQ:
         (``src/flash_pqsim_kernel.py:213-252``).
 
         Args:
-            Q: (Nq, d) query embeddings.
-            codes: (B, Nd, M) PQ codes (uint8, or any integer dtype with values < K).
-            method: "auto" (MFMA kernel when the shape allows it), "mfma" or "lut".
+            Q: (Nq, d) query embeddings (an fp32 query against a 16-bit codebook is scored
+                at fp32 precision, never rounded to the codebook's type).
+            codes: (B, Nd, M) PQ codes: uint8, int16 or int32 (read in place at their
+                width), or any other integer dtype (converted to int32), values < K.
+            method: "auto" (MFMA kernel when the shape allows it, else the table path),
+                "mfma" or "lut".
             validate: check that codes lie in [0, K) (one device-to-host copy; skipped
-                for uint8 codes when K == 256, where every byte is valid).
+                for uint8 codes when K >= 256, where every byte is valid).
 
         Returns:
             (B,) float32 MaxSim scores; a document with Nd == 0 scores -inf.
@@ -98,38 +106,39 @@ class TileMaxSimPQ:
             raise ValueError(f"codes must be (B, Nd, M), got shape {tuple(codes.shape)}")
         B, Nd, M = codes.shape
         assert M == self.M, f"codes have M={M} subspaces, codebook has {self.M}"
-        Q = self._query(Q)
+        if method not in ("auto", "mfma", "lut"):
+            raise ValueError(f"method must be 'auto', 'mfma' or 'lut', got {method!r}")
+        Q, qcode = self._query(Q)
         codes = self._codes(codes, validate)
         Nq = Q.shape[0]
         scores = torch.empty(B, dtype=torch.float32, device=Q.device)
         if B == 0:
             return scores
-        if method not in ("auto", "mfma", "lut"):
-            raise ValueError(f"method must be 'auto', 'mfma' or 'lut', got {method!r}")
-        aligned = all(t.data_ptr() % 16 == 0 for t in (Q, self.codebook, codes))
-        small_docs = Nd * M < 2**31  # the MFMA kernel addresses a document's codes with 32-bit offsets
-        shape_ok = _mfma_shape_ok(self.M, self.K, self.dsub, self.codebook.dtype)
-        use_mfma = method == "mfma" or (method == "auto" and shape_ok and aligned and small_docs)
         lib = _lib.load()
         with _lib.on_device(Q.device):
             stream = _lib.stream_of(Q)
-            if use_mfma:
-                _lib.check(lib.tms_pq_score(Q.data_ptr(), Nq, self.codebook.data_ptr(), self.M, self.K, self.dsub,
-                                            _lib.dtype_code(self.codebook.dtype), codes.data_ptr(), B, Nd,
-                                            scores.data_ptr(), stream))
-            else:
-                table = self.build_distance_table(Q)
-                _lib.check(lib.tms_pq_score_lut(table.data_ptr(), Nq, self.M, self.K, codes.data_ptr(), B, Nd,
-                                                scores.data_ptr(), stream))
+            if method != "lut":
+                # the C entry point refuses shapes the MFMA kernel does not take before any
+                # device work; "auto" then scores through the table
+                status = lib.tms_pq_score(Q.data_ptr(), Nq, self.codebook.data_ptr(), self.M, self.K, self.dsub,
+                                          qcode | _CODE_FLAGS[codes.dtype], codes.data_ptr(), B, Nd,
+                                          scores.data_ptr(), stream)
+                if status == _lib.TMS_OK or method == "mfma" or status != _lib.TMS_ERR_UNSUPPORTED:
+                    _lib.check(status)
+                    return scores
+            table = self._table(Q, qcode)
+            _lib.check(lib.tms_pq_score_lut_ex(table.data_ptr(), Nq, self.M, self.K, codes.data_ptr(),
+                                               _CODE_BYTES[codes.dtype], B, Nd, scores.data_ptr(), stream))
         return scores
 
     def score_batch_queries(self, Qs: torch.Tensor, codes: torch.Tensor, validate: bool = True) -> torch.Tensor:
         """Score ``nQ`` queries against the same PQ codes: ``Qs`` (nQ, Nq, d) -> (nQ, B).
 
         Equivalent to stacking :meth:`score_batch` over the queries. On the MFMA shapes
-        each 16-token tile of codes is decoded once per pass through the codebook in LDS
-        and shared by up to 32 query blocks of 32 tokens (``tms_pq_score_batched``);
-        other shapes score query by query. No reference counterpart.
+        (uint8 codes, a query of the codebook's type) each 16-token tile of codes is
+        decoded once per pass through the codebook in LDS and shared by up to 32 query
+        blocks of 32 tokens (``tms_pq_score_batched``); other inputs score query by query.
+        No reference counterpart.
         """
         _check.tensor("Qs", Qs)
         _check.tensor("codes", codes)
@@ -142,22 +151,22 @@ class TileMaxSimPQ:
         assert Qs.shape[2] == self.d, f"Q width {Qs.shape[2]} != M*dsub = {self.d}"
         _check.on_gpu("Qs", Qs)
         _check.same_device(Qs=Qs, codebook=self.codebook)
-        Qs = _check.query_like(Qs, self.codebook.dtype)
+        Qs, qcode = _check.query_for(Qs, self.codebook.dtype)
         codes = self._codes(codes, validate)
         nQ, Nq = Qs.shape[0], Qs.shape[1]
         scores = torch.empty(nQ, B, dtype=torch.float32, device=Qs.device)
         if B == 0 or nQ == 0:
             return scores
-        aligned = all(t.data_ptr() % 16 == 0 for t in (Qs, self.codebook, codes))
-        if not (_mfma_shape_ok(self.M, self.K, self.dsub, self.codebook.dtype) and aligned and Nd * M < 2**31):
-            for q in range(nQ):
-                scores[q] = self.score_batch(Qs[q], codes, validate=False)
-            return scores
         lib = _lib.load()
         with _lib.on_device(Qs.device):
-            _lib.check(lib.tms_pq_score_batched(Qs.data_ptr(), nQ, Nq, self.codebook.data_ptr(), self.M, self.K,
-                                                self.dsub, _lib.dtype_code(self.codebook.dtype), codes.data_ptr(), B,
-                                                Nd, scores.data_ptr(), _lib.stream_of(Qs)))
+            status = lib.tms_pq_score_batched(Qs.data_ptr(), nQ, Nq, self.codebook.data_ptr(), self.M, self.K,
+                                              self.dsub, qcode | _CODE_FLAGS[codes.dtype], codes.data_ptr(), B, Nd,
+                                              scores.data_ptr(), _lib.stream_of(Qs))
+        if status == _lib.TMS_ERR_UNSUPPORTED:  # shapes without an MFMA path: the table, query by query
+            for q in range(nQ):
+                scores[q] = self.score_batch(Qs[q], codes, method="lut", validate=False)
+            return scores
+        _lib.check(status)
         return scores
 
     def score_single(self, Q: torch.Tensor, codes: torch.Tensor, method: str = "auto") -> torch.Tensor:
