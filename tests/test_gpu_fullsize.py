@@ -1,10 +1,19 @@
-"""Parity at the benchmark workloads' full sizes (C2-C5 with c2b/c3b, c6/c6b, top-k over C2's score matrix).
+"""Parity at the benchmark workloads' full sizes (C2-C5 with c2b/c3b/c5b, c6/c6b, top-k
+over C2's score matrix).
 
-Each test builds one configuration at its benchmark size on the GPU, scores it through
-the public entry points, and checks a seeded sample of documents, always including the
-first and the last (the largest offsets into multi-GB buffers), against the float64
-oracle on copies of exactly those documents. Top-k is checked bit for bit on the whole
-(64, 1M) score matrix. Tolerance: 1e-3 relative + 1e-3 absolute.
+Every score of C2 (64 queries x 1M docs), C3 (32 queries x 2M varlen docs), C4 (16
+queries x 200K docs at d = 256, 512 and 768) and C5 (32 queries x 5M PQ docs) is
+compared with an independent fp32 restatement of the reference's materialise-then-reduce
+oracle (``pytorch_maxsim_naive``, ``src/flash_maxsim_kernel.py:280-288``; for PQ the
+decompress-then-score ``pytorch_pqsim_baseline``, ``src/flash_pqsim_kernel.py:283-313``),
+run chunked on the same GPU with plain fp32 GEMMs (TF32 off): S = D_chunk @ Q^T, max over
+each document's tokens, sum over query tokens. Bar: |delta| <= 1e-3 relative + 1e-3
+absolute on every document, and each query's top-100 identical to the restatement's
+except for swaps among documents whose scores lie within that tolerance of each other
+(the north star's ranking criterion; the reference's consumer is ``torch.topk``,
+``src/cycle3_experiments.py:215``). Each test prints its largest relative error.
+A seeded sample of documents, always the first and the last (the largest offsets into
+multi-GB buffers), is also checked against the float64 oracle.
 """
 import numpy as np
 import pytest
@@ -38,89 +47,200 @@ def _release(torch):
     torch.cuda.empty_cache()
 
 
+def _fp32_no_tf32(torch):
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+
+
+def _ref_fixed(torch, Qs, D, chunk_tokens=1 << 19):
+    """fp32 MaxSim of every query in Qs (nQ, Nq, d) against D (B, Nd, d): (nQ, B)."""
+    _fp32_no_tf32(torch)
+    nQ, Nq, d = Qs.shape
+    B, Nd, _ = D.shape
+    QT = Qs.reshape(nQ * Nq, d).float().t().contiguous()
+    out = torch.empty(nQ, B, dtype=torch.float32, device="cuda")
+    step = max(1, chunk_tokens // Nd)
+    for b0 in range(0, B, step):
+        b1 = min(B, b0 + step)
+        S = torch.mm(D[b0:b1].reshape(-1, d).float(), QT)  # ((b1-b0) Nd, nQ Nq)
+        out[:, b0:b1] = S.view(b1 - b0, Nd, nQ, Nq).amax(dim=1).sum(dim=-1).t()
+    return out
+
+
+def _ref_varlen(torch, Qs, D_flat, offs, chunk_docs=2048):
+    """fp32 MaxSim of every query in Qs against documents D_flat[offs[b]:offs[b+1]]
+    (every document non-empty): each document's rows of S are gathered into a
+    (docs, longest, queries) block, short documents repeating their last row, which
+    leaves the max unchanged."""
+    _fp32_no_tf32(torch)
+    nQ, Nq, d = Qs.shape
+    B = offs.numel() - 1
+    QT = Qs.reshape(nQ * Nq, d).float().t().contiguous()
+    offs_h = offs.cpu()
+    lens = offs[1:] - offs[:-1]
+    assert int(lens.min()) > 0
+    L = int(lens.max())
+    ar = torch.arange(L, device="cuda")
+    out = torch.empty(nQ, B, dtype=torch.float32, device="cuda")
+    for b0 in range(0, B, chunk_docs):
+        b1 = min(B, b0 + chunk_docs)
+        t0, t1 = int(offs_h[b0]), int(offs_h[b1])
+        S = torch.mm(D_flat[t0:t1].float(), QT)
+        rows = (offs[b0:b1, None] - t0) + torch.minimum(ar[None, :], lens[b0:b1, None] - 1)
+        m = S.index_select(0, rows.reshape(-1)).view(b1 - b0, L, nQ * Nq).amax(dim=1)
+        out[:, b0:b1] = m.view(b1 - b0, nQ, Nq).sum(dim=-1).t()
+    return out
+
+
+def _ref_pq(torch, Qs, codebook, codes, chunk_docs=4096):
+    """fp32 decompress-then-score: tokens rebuilt from the codebook in fp32, then MaxSim."""
+    _fp32_no_tf32(torch)
+    nQ, Nq, d = Qs.shape
+    B, Nd, M = codes.shape
+    cbf = codebook.float()
+    QT = Qs.reshape(nQ * Nq, d).float().t().contiguous()
+    msel = torch.arange(M, device="cuda")
+    out = torch.empty(nQ, B, dtype=torch.float32, device="cuda")
+    for b0 in range(0, B, chunk_docs):
+        b1 = min(B, b0 + chunk_docs)
+        Dc = cbf[msel, codes[b0:b1].long()]  # (nb, Nd, M, dsub)
+        S = torch.mm(Dc.reshape(-1, d), QT)
+        out[:, b0:b1] = S.view(b1 - b0, Nd, nQ, Nq).amax(dim=1).sum(dim=-1).t()
+    return out
+
+
+def _check_all(torch, got, ref, what):
+    """Every score within RTOL/ATOL of the fp32 restatement; prints the largest errors."""
+    err = (got - ref).abs()
+    lim = RTOL * ref.abs() + ATOL
+    rel = (err / ref.abs().clamp_min(1e-30)).max().item()
+    print(f"{what}: {got.numel()} scores, max |delta| {err.max().item():.3e}, max relative {rel:.3e}", flush=True)
+    bad = int((err > lim).sum().item())
+    assert bad == 0, f"{what}: {bad} scores outside the bar (worst |delta| {err.max().item():.3e})"
+
+
+def _check_top100(torch, got, ref, what, k=100):
+    """Per query: the HIP top-k of our scores against torch.topk of the restatement's;
+    identical except swaps among documents within the tolerance of each other."""
+    from tilemaxsim_amd import topk
+    gi = topk(got, k)[1]
+    rv, ri = torch.topk(ref, k, dim=1)
+    kth = rv[:, k - 1:k]
+    tol = RTOL * kth.abs() + ATOL
+    rg = torch.gather(ref, 1, gi)  # the restatement's scores of our picks, in our order
+    assert bool((rg >= kth - tol).all()), f"{what}: a pick below the 100th score by more than the tolerance"
+    assert bool((rg[:, 1:] <= rg[:, :-1] + tol).all()), f"{what}: order differs beyond the tolerance"
+    same = int((gi == ri).sum().item())
+    nset = sum(len(set(gi[q].tolist()) ^ set(ri[q].tolist())) for q in range(gi.shape[0]))
+    print(f"{what}: top-{k} of {gi.shape[0]} queries, {same} of {gi.numel()} positions identical, "
+          f"{nset // 2} set swaps (all within tolerance)", flush=True)
+
+
 def test_c2_dense_and_batched_fullsize(cuda):
-    """C2: 1M docs x Nd=180 x d=128 (46 GB); one query through the stream kernel and
-    four through the batched-query kernel."""
+    """C2: 64 queries x 1M docs x Nd=180 x d=128 (46 GB); every query through the stream
+    kernel (one HBM pass each, as the bench step) and all 64 through the batched kernel."""
     import torch
     from tilemaxsim_amd import flash_maxsim_batched_queries, flash_maxsim_v2_multiquery
     D = _normal_fp16(torch, (1_000_000, 180, 128), 11)
-    Qs = _normal_fp16(torch, (4, 32, 128), 12)
-    single = flash_maxsim_v2_multiquery(Qs[0], D)
+    Qs = _normal_fp16(torch, (64, 32, 128), 12)
+    single = torch.stack([flash_maxsim_v2_multiquery(Qs[q], D) for q in range(64)])
     batched = flash_maxsim_batched_queries(Qs, D)
+    ref = _ref_fixed(torch, Qs, D)
+    _check_all(torch, single, ref, "C2 per-query stream kernel")
+    _check_all(torch, batched, ref, "C2 batched kernel")
+    _check_top100(torch, single, ref, "C2 per-query")
+    _check_top100(torch, batched, ref, "C2 batched")
     idx = _sample(1_000_000, 60, 1)
     Dcpu = D[torch.from_numpy(idx).cuda()].cpu().numpy()
-    Qcpu = Qs.cpu().numpy()
-    for q in range(4):
-        ref = orc.maxsim_f64(Qcpu[q], Dcpu)
-        np.testing.assert_allclose(batched[q].cpu().numpy()[idx], ref, rtol=RTOL, atol=ATOL)
-        if q == 0:
-            np.testing.assert_allclose(single.cpu().numpy()[idx], ref, rtol=RTOL, atol=ATOL)
-    del D, single, batched
+    for q in (0, 63):
+        np.testing.assert_allclose(single[q].cpu().numpy()[idx], orc.maxsim_f64(Qs[q].cpu().numpy(), Dcpu),
+                                   rtol=RTOL, atol=ATOL)
+    del D, single, batched, ref
     _release(torch)
 
 
 def test_c3_varlen_fullsize(cuda):
-    """C3: 2M docs, Nd ~ U[32, 300] (332M tokens, 85 GB), int64 offsets; one query through
-    the varlen kernel and 32 through the batched kernel (c3b)."""
+    """C3: 32 queries x 2M docs, Nd ~ U[32, 300] (332M tokens, 85 GB), int64 offsets;
+    every query through the varlen kernel and all 32 through the batched kernel (c3b)."""
     import torch
     from tilemaxsim_amd import flash_maxsim_multi_doc, flash_maxsim_multi_doc_batched
     rng = np.random.default_rng(77)
     lens = rng.integers(32, 301, size=2_000_000)
     offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
     D = _normal_fp16(torch, (int(offs[-1]), 128), 21)
-    Q = _normal_fp16(torch, (32, 128), 22)
-    got = flash_maxsim_multi_doc(Q, D, torch.from_numpy(offs).cuda()).cpu().numpy()
+    Qs = _normal_fp16(torch, (32, 32, 128), 22)
+    offs_t = torch.from_numpy(offs).cuda()
+    single = torch.stack([flash_maxsim_multi_doc(Qs[q], D, offs_t, validate=False) for q in range(32)])
+    batched = flash_maxsim_multi_doc_batched(Qs, D, offs_t, validate=False)
+    ref = _ref_varlen(torch, Qs, D, offs_t)
+    _check_all(torch, single, ref, "C3 per-query varlen kernel")
+    _check_all(torch, batched, ref, "C3 batched kernel")
+    _check_top100(torch, single, ref, "C3 per-query")
+    _check_top100(torch, batched, ref, "C3 batched")
     idx = _sample(2_000_000, 60, 2)
     rows = np.concatenate([np.arange(offs[b], offs[b + 1]) for b in idx])
     sub = D[torch.from_numpy(rows).cuda()].cpu().numpy()
     sub_offs = np.concatenate([[0], np.cumsum(lens[idx])]).astype(np.int64)
-    ref = orc.maxsim_varlen(Q.cpu().numpy(), sub, sub_offs, f64=True)
-    np.testing.assert_allclose(got[idx], ref, rtol=RTOL, atol=ATOL)
-    # c3b: 32 queries through the batched kernel, three of them checked on the sample
-    Qs = _normal_fp16(torch, (32, 32, 128), 23)
-    gotb = flash_maxsim_multi_doc_batched(Qs, D, torch.from_numpy(offs).cuda(), validate=False).cpu().numpy()
-    for q in (0, 13, 31):
-        refq = orc.maxsim_varlen(Qs[q].cpu().numpy(), sub, sub_offs, f64=True)
-        np.testing.assert_allclose(gotb[q][idx], refq, rtol=RTOL, atol=ATOL)
-    del D
+    for q in (0, 31):
+        np.testing.assert_allclose(single[q].cpu().numpy()[idx],
+                                   orc.maxsim_varlen(Qs[q].cpu().numpy(), sub, sub_offs, f64=True),
+                                   rtol=RTOL, atol=ATOL)
+    del D, single, batched, ref
     _release(torch)
 
 
-def test_c4_dtiled_fullsize(cuda):
-    """C4 at its largest width: 200K docs x Nd=128 x d=768 (39 GB), Q in LDS."""
+@pytest.mark.parametrize("d", [256, 512, 768])
+def test_c4_dtiled_fullsize(cuda, d):
+    """C4: 16 queries x 200K docs x Nd=128 at d = 256, 512, 768 (13-39 GB), Q in LDS."""
     import torch
     from tilemaxsim_amd import flash_maxsim_v2_multiquery
-    D = _normal_fp16(torch, (200_000, 128, 768), 31)
-    Q = _normal_fp16(torch, (32, 768), 32)
-    got = flash_maxsim_v2_multiquery(Q, D).cpu().numpy()
+    D = _normal_fp16(torch, (200_000, 128, d), 30 + d)
+    Qs = _normal_fp16(torch, (16, 32, d), 31 + d)
+    got = torch.stack([flash_maxsim_v2_multiquery(Qs[q], D) for q in range(16)])
+    ref = _ref_fixed(torch, Qs, D)
+    _check_all(torch, got, ref, f"C4 d={d}")
+    _check_top100(torch, got, ref, f"C4 d={d}")
     idx = _sample(200_000, 40, 3)
-    ref = orc.maxsim_f64(Q.cpu().numpy(), D[torch.from_numpy(idx).cuda()].cpu().numpy())
-    np.testing.assert_allclose(got[idx], ref, rtol=RTOL, atol=ATOL)
-    del D
+    np.testing.assert_allclose(got[0].cpu().numpy()[idx],
+                               orc.maxsim_f64(Qs[0].cpu().numpy(), D[torch.from_numpy(idx).cuda()].cpu().numpy()),
+                               rtol=RTOL, atol=ATOL)
+    del D, got, ref
     _release(torch)
 
 
 def test_c5_pq_fullsize(cuda):
-    """C5: 5M docs x Nd=128 x M=16 uint8 codes (10.24 GB), both PQ algorithms on a
-    sample; the MFMA kernel on everything."""
+    """C5: 32 queries x 5M docs x Nd=128 x M=16 uint8 codes (10.24 GB): every query
+    through the MFMA kernel and all 32 through the batched kernel (c5b), against fp32
+    decompress-then-score; the table-gather kernel on two queries."""
     import torch
     from tilemaxsim_amd import TileMaxSimPQ
     g = torch.Generator(device="cuda").manual_seed(41)
     codes = torch.randint(0, 256, (5_000_000, 128, 16), dtype=torch.uint8, device="cuda", generator=g)
     cb = torch.randn(16, 256, 8, device="cuda", generator=g).half()
-    Q = _normal_fp16(torch, (32, 128), 42)
-    got = TileMaxSimPQ(cb).score_batch(Q, codes, validate=False).cpu().numpy()
+    Qs = _normal_fp16(torch, (32, 32, 128), 42)
+    pq = TileMaxSimPQ(cb)
+    single = torch.stack([pq.score_batch(Qs[q], codes, validate=False) for q in range(32)])
+    batched = pq.score_batch_queries(Qs, codes, validate=False)
+    ref = _ref_pq(torch, Qs, cb, codes)
+    _check_all(torch, single, ref, "C5 per-query MFMA kernel")
+    _check_all(torch, batched, ref, "C5 batched kernel")
+    _check_top100(torch, single, ref, "C5 per-query")
+    _check_top100(torch, batched, ref, "C5 batched")
+    lut = torch.stack([pq.score_batch(Qs[q], codes, method="lut", validate=False) for q in (0, 31)])
+    _check_all(torch, lut, ref[[0, 31]], "C5 table-gather kernel (queries 0 and 31)")
     idx = _sample(5_000_000, 60, 4)
-    ref = orc.pq_decompress_score(Q.cpu().numpy(), cb.cpu().numpy(), codes[torch.from_numpy(idx).cuda()].cpu().numpy(),
-                                  f64=True)
-    np.testing.assert_allclose(got[idx], ref, rtol=RTOL, atol=ATOL)
-    del codes
+    np.testing.assert_allclose(single[0].cpu().numpy()[idx],
+                               orc.pq_decompress_score(Qs[0].cpu().numpy(), cb.cpu().numpy(),
+                                                       codes[torch.from_numpy(idx).cuda()].cpu().numpy(), f64=True),
+                               rtol=RTOL, atol=ATOL)
+    del codes, single, batched, ref
     _release(torch)
 
 
 def test_c6_residual_fullsize(cuda):
     """c6: C3's corpus as a ColBERTv2 index (nbits=2, 262,144 centroids, 12 GB), one query
-    through the fused kernel; c6b: 32 queries through the batched kernel."""
+    through the fused kernel; c6b: 32 queries through the batched kernel. A seeded sample
+    against the float64 codec oracle."""
     import torch
     from tilemaxsim_amd import flashmaxsim_score_residual, flashmaxsim_score_residual_batched
     rng = np.random.default_rng(77)
