@@ -14,13 +14,16 @@ through the batched-query kernel), c6 (C3's
 corpus as a ColBERTv2 residual-compressed index, fused decode + MaxSim per query), c6b
 (the same index, all queries through the batched residual kernel), prec (the
 reference's precision experiment: 1 query x 10K raw-Gaussian documents, Nd = 128,
-d = 128), copy (counter calibration). ``--dtype fp16|bf16|fp32`` sets the embedding
-dtype of c1, c2, c4 and prec.
+d = 128), copy (counter calibration), readprobe (a read-only streaming kernel over a
+C2-sized 46 GB buffer: the read rate any streaming kernel reaches on this part).
+``--dtype fp16|bf16|fp32`` sets the embedding dtype of c1, c2, c4 and prec.
 
 Prints ONE JSON line on stdout. ``value`` is (query, document) pairs scored per second
 over the whole step; ``roofline`` is the dominant kernel's algorithmic bandwidth from
-HIP events around each of its launches; ``cpu_baseline`` times the numpy restatement
-of the reference PyTorch path on this host's cores over a bounded sample.
+HIP events around each of its launches; ``cpu_baseline`` times the reference's PyTorch
+scoring path (restated in ``oracle/torch_ref.py``, fp32 on the CPU with
+``torch.set_num_threads(os.cpu_count())``) on this host over a bounded sample, with the
+numpy restatement beside it.
 """
 from __future__ import annotations
 
@@ -50,7 +53,8 @@ def parse():
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--config", default="c2",
-                   choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "prec", "copy"])
+                   choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "prec", "copy",
+                            "readprobe"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--dtype", default="fp16", choices=["fp16", "bf16", "fp32"],
                    help="embedding dtype for --config c1, c2, c4 and prec")
@@ -208,17 +212,22 @@ class Dense:
                                       "src/run_all_experiments.py:287-347")
         return cfg
 
-    def cpu_baseline(self, seconds, threads):
+    def cpu_baseline(self, seconds):
         from oracle import maxsim_oracle as orc
+        from oracle import torch_ref as tr
         n = min(self.B, 4000)
+        Qt, Dt = self.Q[0].cpu(), self.D[:n].cpu()
+        # torch: the reference's own formulation; each chunk is cast .float() in the timed calls
+        base = _time_torch_cpu(lambda: tr.maxsim_naive(Qt, Dt, chunk=500), n, seconds,
+                               f"{n} docs of this corpus x query 0, torch fp32 einsum -> max -> sum "
+                               "(pytorch_maxsim_naive), 500-doc chunks, repeated")
         Q, D = self.Q[0], self.D[:n]
         if self.dtype == "bf16":  # numpy has no bfloat16: cast once, outside the timed calls
             Q, D = Q.float(), D.float()
-        # fp16 stays fp16: the timed port casts each chunk to fp32, as the reference's .float() does
         Q, D = Q.cpu().numpy(), D.cpu().numpy()
-        return _time_cpu(lambda: orc.maxsim_naive(Q, D, chunk=500), n, seconds, threads,
-                         f"{n} docs of this corpus x query 0, numpy fp32 materialise-then-reduce "
-                         "(restates pytorch_maxsim_naive), repeated")
+        base["numpy_port"] = _time_cpu(lambda: orc.maxsim_naive(Q, D, chunk=500), n, seconds / 2,
+                                       f"{n} docs x query 0, numpy fp32 materialise-then-reduce, repeated")
+        return base
 
 
 def gemm_ceiling(torch, achieved_tflops):
@@ -309,14 +318,21 @@ class Varlen(Dense):
                 "queries": self.nQ, "docs": self.B, "tokens": self.T, "Nq": self.Nq, "d": self.d, "top_k": self.k,
                 "kernel": "flash_maxsim_multi_doc (offsets, no padding)"}
 
-    def cpu_baseline(self, seconds, threads):
+    def cpu_baseline(self, seconds):
         from oracle import maxsim_oracle as orc
+        from oracle import torch_ref as tr
         n = 4000
-        offs = self.offsets[: n + 1].cpu().numpy()
-        Q = self.Q[0].cpu().numpy()
-        Dflat = self.D[: int(offs[-1])].cpu().numpy()
-        return _time_cpu(lambda: orc.maxsim_varlen(Q, Dflat, offs), n, seconds, threads,
-                         f"first {n} docs x query 0, numpy fp32 per-token sims + segmented max, repeated")
+        offs_t = self.offsets[: n + 1].cpu()
+        Qt, Dt = self.Q[0].cpu(), self.D[: int(offs_t[-1])].cpu()
+        base = _time_torch_cpu(lambda: tr.maxsim_varlen_masked(Qt, Dt, offs_t, chunk=500), n, seconds,
+                               f"first {n} docs x query 0, torch fp32: 500-doc chunks padded to their longest, "
+                               "einsum -> masked_fill(-inf) -> max -> sum (pytorch_maxsim_score), repeated")
+        offs = offs_t.numpy()
+        Q, Dflat = Qt.numpy(), Dt.numpy()
+        base["numpy_port"] = _time_cpu(lambda: orc.maxsim_varlen(Q, Dflat, offs), n, seconds / 2,
+                                       f"first {n} docs x query 0, numpy fp32 per-token sims + segmented max, "
+                                       "repeated")
+        return base
 
 
 class VarlenBatched(Varlen):
@@ -424,7 +440,7 @@ class Residual(Varlen):
                 "kernel": "flashmaxsim_score_residual (decode in registers + MFMA)",
                 "roofline_bytes": "compressed index bytes (codes + residuals + offsets) + centroid table per launch"}
 
-    def cpu_baseline(self, seconds, threads):
+    def cpu_baseline(self, seconds):
         from oracle import residual_oracle as ro
         n = 2000
         offs = self.offsets[: n + 1].cpu().numpy()
@@ -432,7 +448,7 @@ class Residual(Varlen):
         Q = self.Q[0].cpu().numpy()
         codes, res = self.codes[:t].cpu().numpy(), self.res[:t].cpu().numpy()
         C, w = self.centroids.cpu().numpy(), self.weights.cpu().numpy()
-        return _time_cpu(lambda: ro.maxsim_residual_f32(Q, codes, res, C, w, self.nbits, offs), n, seconds, threads,
+        return _time_cpu(lambda: ro.maxsim_residual_f32(Q, codes, res, C, w, self.nbits, offs), n, seconds,
                          f"first {n} docs x query 0, numpy decompress (restated codec) then fp32 varlen MaxSim, "
                          "repeated")
 
@@ -565,14 +581,18 @@ class PQ:
                 "kernel": "TileMaxSimPQ.score_batch (codebook gather in LDS + MFMA)",
                 "roofline_bytes": "code bytes B*Nd*M per launch"}
 
-    def cpu_baseline(self, seconds, threads):
+    def cpu_baseline(self, seconds):
         from oracle import maxsim_oracle as orc
+        from oracle import torch_ref as tr
         n = 2000
-        Q = self.Q[0].cpu().numpy()
-        C = self.codebook.cpu().numpy()
-        codes = self.codes[:n].cpu().numpy()
-        return _time_cpu(lambda: orc.pq_decompress_score(Q, C, codes, chunk=500), n, seconds, threads,
-                         f"{n} docs x query 0, numpy decompress-then-score (restates pytorch_pqsim_baseline), repeated")
+        Qt, Ct, codes_t = self.Q[0].cpu(), self.codebook.cpu(), self.codes[:n].cpu()
+        base = _time_torch_cpu(lambda: tr.pq_decompress_score(Qt, Ct, codes_t, chunk=500), n, seconds,
+                               f"{n} docs x query 0, torch fp32 decompress per subspace then einsum -> max -> sum "
+                               "(pytorch_pqsim_baseline), 500-doc chunks, repeated")
+        Q, C, codes = Qt.numpy(), Ct.numpy(), codes_t.numpy()
+        base["numpy_port"] = _time_cpu(lambda: orc.pq_decompress_score(Q, C, codes, chunk=500), n, seconds / 2,
+                                       f"{n} docs x query 0, numpy decompress-then-score, repeated")
+        return base
 
 
 class PQBatched(PQ):
@@ -634,7 +654,40 @@ class Copy:
     def config(self):
         return {"workload": f"copy: {self.n} bytes device to device (rocprof counter calibration)"}
 
-    def cpu_baseline(self, seconds, threads):
+    def cpu_baseline(self, seconds):
+        return None
+
+
+class ReadProbe:
+    """A read-only streaming kernel (tms_read_probe: 8 KiB per wave-iteration, persistent
+    XCD-grouped grid) over a C2-sized 46.08 GB buffer: the rate at which this part
+    delivers a document stream to any kernel, against which the scoring kernels'
+    fractions of the 8 TB/s spec are read."""
+    kernel = "read_probe_kernel"
+
+    def __init__(self, torch, nbytes=46_080_000_000):
+        from tilemaxsim_amd import _lib
+        self.torch, self.n, self.lib = torch, nbytes, _lib.load()
+        self.buf = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+        self.sink = torch.empty(_lib.TMS_READ_PROBE_SINK_WORDS, dtype=torch.int32, device="cuda")
+        self.check = _lib.check
+
+    def step(self, timer):
+        stream = self.torch.cuda.current_stream().cuda_stream
+        timer(lambda: self.check(self.lib.tms_read_probe(self.buf.data_ptr(), self.n, self.sink.data_ptr(),
+                                                         self.sink.numel(), stream)))
+
+    def bytes_per_launch(self):
+        return self.n
+
+    def pairs_per_step(self):
+        return 0
+
+    def config(self):
+        return {"workload": f"readprobe: {self.n} bytes read once per launch (C2's corpus size), no writes "
+                            "beyond one word per thread"}
+
+    def cpu_baseline(self, seconds):
         return None
 
 
@@ -650,8 +703,35 @@ def _cpu_model():
     return platform.processor() or platform.machine()
 
 
-def _time_cpu(fn, docs_per_call, seconds, threads, sample):
+def _time_torch_cpu(fn, docs_per_call, seconds, sample):
+    """Times a torch CPU function on every host core (torch.set_num_threads(os.cpu_count()))."""
+    import torch
+    threads = os.cpu_count() or 1
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        fn()  # warm-up
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        used = torch.get_num_threads()
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": docs_per_call * n / el, "unit": "docs/s (1 query)", "cores": used, "kind": "port",
+            "impl": f"torch {torch.__version__} (CPU, fp32)", "torch_num_threads": used,
+            "os_cpu_count": os.cpu_count(), "cpu_model": _cpu_model(),
+            "sample": f"{sample} {n}x in {el:.1f} s"}
+
+
+def _time_cpu(fn, docs_per_call, seconds, sample):
+    """Times a numpy function with its BLAS on every host core."""
     from threadpoolctl import threadpool_limits
+    threads = os.cpu_count() or 1
     with threadpool_limits(limits=threads):
         fn()  # warm-up
         n = 0
@@ -716,6 +796,8 @@ def main():
         wl = Residual(torch, 32, 2_000_000, 32, 300)
     elif args.config == "c6b":
         wl = ResidualBatched(torch, 32, 2_000_000, 32, 300)
+    elif args.config == "readprobe":
+        wl = ReadProbe(torch)
     else:
         wl = Copy(torch)
     torch.cuda.synchronize()
@@ -754,9 +836,8 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        threads = max(1, min(16, os.cpu_count() or 1))
-        log(f"[bench] CPU baseline on {threads} threads, ~{args.cpu_seconds:.0f} s")
-        cpu = wl.cpu_baseline(args.cpu_seconds, threads)
+        log(f"[bench] CPU baseline on {os.cpu_count()} threads, ~{1.5 * args.cpu_seconds:.0f} s")
+        cpu = wl.cpu_baseline(args.cpu_seconds)
     if hasattr(wl, "extra_roofline"):
         roofline.update(wl.extra_roofline(k_mean))
     if hasattr(wl, "unfused_ms"):  # after the timed steps (c6: needs a decompressed copy of the corpus)

@@ -261,6 +261,16 @@ int tms_maxsim_residual_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t 
                                 const uint8_t* residuals, int64_t total_tokens, const int64_t* offsets, int64_t ndocs,
                                 const int64_t* pids, int64_t B, int64_t pad_len, float* out, void* stream);
 
+/*
+ * Measurement helper, not part of the scoring path and with no counterpart in the
+ * reference: reads `bytes` (a multiple of 8 KiB) of `buf` once with a read-only
+ * streaming kernel and writes one XOR word per thread to `sink`
+ * (TMS_READ_PROBE_SINK_WORDS words). `bench.py --config readprobe` times it over a
+ * C2-sized buffer: the read rate any streaming kernel on this part can reach.
+ */
+#define TMS_READ_PROBE_SINK_WORDS 524288
+int tms_read_probe(const void* buf, int64_t bytes, uint32_t* sink, int64_t sink_words, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

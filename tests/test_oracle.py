@@ -330,3 +330,25 @@ def test_packed_zero_padding_pins():
     full = orc.maxsim_varlen(Q, flat, offsets, f64=True)
     assert got[1] == pytest.approx(full[1], rel=1e-13) and got[3] == pytest.approx(full[3], rel=1e-13)
     assert got[2] == 0.0
+
+
+# ---------------------------------------------------------------- torch restatement
+def test_torch_restatement_matches_numpy_oracle():
+    """oracle/torch_ref.py (the CPU baseline bench.py times) against the pinned numpy
+    oracle: dense, variable-length (padded and masked) and PQ decompress-then-score."""
+    import torch
+    from oracle import torch_ref as tr
+    rng = _rng(314)
+    Q = rng.standard_normal((32, 64)).astype(np.float16)
+    D = rng.standard_normal((70, 23, 64)).astype(np.float16)
+    np.testing.assert_allclose(tr.maxsim_naive(torch.from_numpy(Q), torch.from_numpy(D), chunk=16).numpy(),
+                               orc.maxsim_f64(Q, D), rtol=1e-5, atol=1e-5)
+    lens = rng.integers(1, 40, size=55)
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    Df = rng.standard_normal((int(offs[-1]), 64)).astype(np.float16)
+    got = tr.maxsim_varlen_masked(torch.from_numpy(Q), torch.from_numpy(Df), torch.from_numpy(offs), chunk=9)
+    np.testing.assert_allclose(got.numpy(), orc.maxsim_varlen(Q, Df, offs, f64=True), rtol=1e-5, atol=1e-5)
+    C = rng.standard_normal((8, 40, 8)).astype(np.float16)
+    codes = rng.integers(0, 40, size=(33, 11, 8)).astype(np.uint8)
+    got = tr.pq_decompress_score(torch.from_numpy(Q), torch.from_numpy(C), torch.from_numpy(codes), chunk=10)
+    np.testing.assert_allclose(got.numpy(), orc.pq_decompress_score(Q, C, codes, f64=True), rtol=1e-5, atol=1e-5)
