@@ -9,24 +9,43 @@ at ``:328-333``) receives documents that ColBERT's search has already decompress
 its residual-compressed index. ColBERT is a third-party dependency absent from the
 reference checkout: the package ``colbert-ai``, pinned at **0.2.22**
 (``src/plaid_integration_benchmark.py:23``). Its codec is ``ResidualCodec`` in
-``colbert/indexing/codecs/residual.py`` of that package. This module restates the
-codec's published algorithm (Santhanam et al., "ColBERTv2", NAACL 2022, section 3;
-the package's compress / binarize / decompress):
+``colbert/indexing/codecs/residual.py`` of that package. The package is not installed
+here and its source is not in ``/root/reference``, so the citations below name the
+package's functions, not line numbers. This module restates the codec's published
+algorithm (Santhanam et al., "ColBERTv2", NAACL 2022, section 3):
 
 index build (:func:`compress`)
-  * ``code[t] = argmax_c <centroid[c], emb[t]>``;
-  * ``r = fp16(emb[t] - centroid[code[t]])``;
-  * ``bucket[j] = #{i : cutoffs[i] < r[j]}`` (``torch.bucketize``, ``right=False``),
-    with ``2**nbits - 1`` cutoffs;
-  * bits ``0 .. nbits-1`` of every dimension's bucket, least significant bit first,
-    dimensions in order, packed eight to a byte with the first bit in the most
-    significant position (``numpy.packbits``). A token's residual row is
-    ``d * nbits / 8`` bytes (:func:`pack_buckets`).
+  * ``code[t] = argmax_c <centroid[c], emb[t]>`` (``ResidualCodec.compress_into_codes``);
+  * ``r = fp16(emb[t] - centroid[code[t]])`` (``ResidualCodec.compress``: the batch is
+    half and ``lookup_centroids`` returns half rows);
+  * ``bucket[j] = #{i : cutoffs[i] < r[j]}`` (``ResidualCodec.binarize``:
+    ``torch.bucketize`` with its default ``right=False``), with ``2**nbits - 1``
+    cutoffs;
+  * bits ``0 .. nbits-1`` of every dimension's bucket, least significant bit first
+    (``binarize``: ``(bucket >> arange(nbits)) & 1``), dimensions in order, packed eight
+    to a byte with the first bit in the most significant position (``binarize`` calls
+    ``numpy.packbits`` on the CPU and the package's ``packbits`` extension on the GPU,
+    which packs the same way). A token's residual row is ``d * nbits / 8`` bytes
+    (:func:`pack_buckets`).
 
-decompression, GPU path of the codec (:func:`decompress`)
-  * ``v = fp16(centroid[code] + bucket_weights[bucket])`` (half arithmetic);
+decompression, GPU path of the codec (:func:`decompress`; ``ResidualCodec.decompress``
+with ``use_gpu``, whose per-element work is the package's ``decompress_residuals``
+CUDA extension, ``colbert/indexing/codecs/decompress_residuals.cu``)
+  * ``v = fp16(centroid[code] + bucket_weights[bucket])``: a half add per element; the
+    bucket comes from ``decompression_lookup_table[reversed_bit_map[byte]]`` (the two
+    tables built in ``ResidualCodec.__init__``, restated in :func:`colbert_tables`);
   * ``n = fp16(sqrt(sum_j v_j**2))``, accumulated in fp32;
-  * ``out = fp16(v / n)``: ``torch.nn.functional.normalize`` applied to a half tensor.
+  * ``out = fp16(v / n)``: ``torch.nn.functional.normalize(v, p=2, dim=-1)`` applied to a
+    half tensor.
+
+One case differs on purpose: a token whose decoded vector is all zeros. ``normalize``
+clamps the norm at ``eps = 1e-12``, which is 0 once the clamp is done in half
+precision, so the codec's 0 / 0 gives NaN in every dimension. This oracle clamps the
+norm at 1e-12 in fp32 and the HIP kernels at fp16's smallest subnormal (the two clamps
+agree for every nonzero fp16 vector, whose half norm is at least that subnormal); both
+return the zero vector, whose dot product with any query token is 0. Real indexes do
+not hold such tokens: it takes a centroid that the residual weights cancel exactly in
+every dimension.
 
 The codec's own decoder does not extract bits directly. It maps each residual byte
 through a bit-reversal table and then through the ``itertools.product`` table of bucket

@@ -64,6 +64,48 @@ def test_decompress_matches_codec(cuda, nbits, d):
     assert np.array_equal(got64, got)
 
 
+# Residual rows written byte by byte, with each dimension's bucket derived by hand from
+# the format (per dimension, bits 0..nbits-1 of the bucket, least significant first, enter
+# one bit stream that fills each byte from its most significant bit), not by the oracle:
+#   nbits=1: 0xA5 = 1010 0101 -> 1,0,1,0,0,1,0,1; 0x0F -> 0,0,0,0,1,1,1,1; 0x80 -> 1,0..0;
+#            0x01 -> 0..0,1
+#   nbits=2: 0xC9 = 11 00 10 01 -> 3,0,1,2; 0x1B = 00 01 10 11 -> 0,2,1,3; 0xFF -> 3,3,3,3;
+#            0x80 -> 1,0,0,0; 0x40 -> 2,0,0,0; 0x01 -> 0,0,0,2; 0x02 -> 0,0,0,1
+#   nbits=4: 0x3C = 0011 1100 -> 12,3; 0x81 -> 1,8; 0xF0 -> 15,0; 0x96 = 1001 0110 -> 9,6;
+#            0x07 -> 0,14
+_HAND_ROWS = {
+    1: ([0xA5, 0x0F, 0x80, 0x01],
+        [1, 0, 1, 0, 0, 1, 0, 1] + [0, 0, 0, 0, 1, 1, 1, 1] + [1] + [0] * 7 + [0] * 7 + [1]),
+    2: ([0xC9, 0x1B, 0x00, 0xFF, 0x80, 0x40, 0x01, 0x02],
+        [3, 0, 1, 2, 0, 2, 1, 3, 0, 0, 0, 0, 3, 3, 3, 3, 1, 0, 0, 0, 2, 0, 0, 0, 0, 0, 0, 2, 0, 0, 0, 1]),
+    4: ([0x3C, 0x81, 0xF0, 0x96] + [0x00] * 11 + [0x07],
+        [12, 3, 1, 8, 15, 0, 9, 6] + [0] * 22 + [0, 14]),
+}
+_HAND_WEIGHTS = {1: [-0.5, 0.25], 2: [-0.5, -0.125, 0.25, 1.0], 4: [(i - 7.5) / 8 for i in range(16)]}
+
+
+@pytest.mark.parametrize("nbits", [1, 2, 4])
+def test_decompress_hand_built_bytes(cuda, nbits):
+    """tms_residual_decompress on residual bytes written by hand, against the closed form
+    v = centroid[code] + weight[bucket] (every value exact in fp16), out = v / |v|."""
+    from tilemaxsim_amd import decompress_residual
+    d = 32
+    row, buckets = _HAND_ROWS[nbits]
+    assert len(row) == d * nbits // 8 and len(buckets) == d
+    res = np.array([row, row], dtype=np.uint8)
+    C = np.zeros((3, d), dtype=np.float16)
+    C[2] = 0.25
+    codes = np.array([0, 2], dtype=np.int32)
+    w = np.array(_HAND_WEIGHTS[nbits], dtype=np.float16)
+    got = decompress_residual(_gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits).cpu().numpy().astype(np.float64)
+    wb = np.array([_HAND_WEIGHTS[nbits][b] for b in buckets], dtype=np.float64)
+    for t, base in enumerate((0.0, 0.25)):
+        v = base + wb
+        expect = v / np.linalg.norm(v)
+        # fp16 norm and fp16 output: within 2 fp16 ulps of the exact quotient
+        np.testing.assert_allclose(got[t], expect, rtol=2 * 2.0 ** -10, atol=2.0 ** -24, err_msg=f"token {t}")
+
+
 @pytest.mark.parametrize("nbits,d,nq", [(2, 128, 32), (1, 128, 32), (4, 128, 32), (2, 64, 20), (2, 32, 1),
                                         (2, 96, 33), (4, 128, 64), (2, 128, 100)])
 @pytest.mark.parametrize("padding", ["zeros", "mask"])
