@@ -54,7 +54,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--config", default="c2",
                    choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "prec", "copy",
-                            "readprobe"])
+                            "readprobe", "ldsprobe"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--dtype", default="fp16", choices=["fp16", "bf16", "fp32"],
                    help="embedding dtype for --config c1, c2, c4 and prec")
@@ -691,6 +691,68 @@ class ReadProbe:
         return None
 
 
+class LdsProbe:
+    """LDS gather probe (tms_lds_probe): the cost of a ds_read_b128 wave-instruction when
+    16 consecutive lanes hit 16 different bank groups (pattern 0), when they read random
+    rows of one codebook subspace as the PQ kernel's gathers do (pattern 1, the timed
+    one), when they all hit one bank group (pattern 2), and when each bank group gets
+    four lanes of every 16 (pattern 3). LDS bytes, not HBM bytes."""
+    kernel = "lds_probe_kernel"
+    PATTERNS = {0: "conflict-free (lane l -> bank group l % 16, random rows)",
+                1: "PQ codebook gather (one subspace per 16-lane group, random codes)",
+                2: "one bank group per 16-lane group, random rows",
+                3: "lane l -> bank group (l / 4) % 16: balanced over the wave, 4-way within 16 lanes"}
+
+    def __init__(self, torch):
+        from tilemaxsim_amd import _lib
+        self.torch, self.lib, self.check = torch, _lib.load(), _lib.check
+        self.nw = _lib.TMS_LDS_PROBE_WAVES
+        self.cycles = torch.empty(self.nw, dtype=torch.int64, device="cuda")
+        self.sink = torch.empty(self.nw * 64, dtype=torch.int32, device="cuda")
+        self.instr_per_wave = 4096 * 16
+
+    def run(self, pattern):
+        stream = self.torch.cuda.current_stream().cuda_stream
+        self.check(self.lib.tms_lds_probe(pattern, self.cycles.data_ptr(), self.nw, self.sink.data_ptr(),
+                                          self.sink.numel(), stream))
+
+    def step(self, timer):
+        timer(lambda: self.run(1))
+
+    def bytes_per_launch(self):
+        return self.nw * self.instr_per_wave * 1024  # LDS bytes read by all waves
+
+    def pairs_per_step(self):
+        return 0
+
+    def config(self):
+        return {"workload": "ldsprobe: 256 workgroups x 16 waves x 65,536 ds_read_b128 per wave over 128 KiB "
+                            "of LDS, four lane -> address patterns"}
+
+    def cpu_baseline(self, seconds):
+        return None
+
+    def extra_roofline(self, k_mean):
+        torch = self.torch
+        out = {}
+        for p, what in self.PATTERNS.items():
+            self.run(p)
+            ms = []
+            for _ in range(5):
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                self.run(p)
+                e.record()
+                e.synchronize()
+                ms.append(s.elapsed_time(e))
+            cyc = float(self.cycles.double().mean().item())
+            per_instr = cyc / (16 * self.instr_per_wave)  # 16 waves share one CU's LDS
+            out[str(p)] = {"pattern": what, "ms": round(float(np.mean(ms)), 4),
+                           "s_memtime_cycles_per_wave_instr": round(per_instr, 3),
+                           "bytes_per_cycle_per_cu": round(1024 / per_instr, 1)}
+        return {"bound": "lds", "peak": None, "frac": None, "unit": "GB/s (LDS reads, all CUs)", "patterns": out}
+
+
 def _cpu_model():
     """The host CPU's model name (Linux /proc/cpuinfo), else the architecture."""
     try:
@@ -798,6 +860,8 @@ def main():
         wl = ResidualBatched(torch, 32, 2_000_000, 32, 300)
     elif args.config == "readprobe":
         wl = ReadProbe(torch)
+    elif args.config == "ldsprobe":
+        wl = LdsProbe(torch)
     else:
         wl = Copy(torch)
     torch.cuda.synchronize()
@@ -849,7 +913,8 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": getattr(wl, "dtype", "fp16"),
         "data": "synthetic (seeded; no dataset)", "config": wl.config(),
-        "hbm_gbs": round(achieved, 1), "hbm_pct_of_peak": round(100 * achieved / HBM_PEAK_GBS, 2),
+        "hbm_gbs": round(achieved, 1) if roofline["bound"] != "lds" else None,
+        "hbm_pct_of_peak": round(100 * achieved / HBM_PEAK_GBS, 2) if roofline["bound"] != "lds" else None,
         "roofline": roofline, "cpu_baseline": cpu,
     }
     batched = wl.batched_line(torch) if hasattr(wl, "batched_line") else None

@@ -271,6 +271,20 @@ int tms_maxsim_residual_batched(const void* Qs, int64_t nQ, int64_t nq, int64_t 
 #define TMS_READ_PROBE_SINK_WORDS 524288
 int tms_read_probe(const void* buf, int64_t bytes, uint32_t* sink, int64_t sink_words, void* stream);
 
+/*
+ * Measurement helper, not part of the scoring path and with no counterpart in the
+ * reference: times 16 x 4096 x 16 ds_read_b128 wave-instructions per CU (256 workgroups
+ * of 16 waves, 128 KiB of LDS each) for one lane -> address pattern (0: conflict-free,
+ * 1: the PQ kernel's codebook gather, 2: every lane group on one bank group, 3: four
+ * lanes of each 16-lane group per bank group) and writes
+ * each wave's elapsed s_memtime cycles to `cycles` (TMS_LDS_PROBE_WAVES words) and one
+ * XOR word per thread to `sink` (64 x TMS_LDS_PROBE_WAVES words). `bench.py --config
+ * ldsprobe` runs the four patterns.
+ */
+#define TMS_LDS_PROBE_WAVES 4096
+int tms_lds_probe(int pattern, int64_t* cycles, int64_t cycle_words, uint32_t* sink, int64_t sink_words,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

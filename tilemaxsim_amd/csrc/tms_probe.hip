@@ -53,3 +53,75 @@ extern "C" int tms_read_probe(const void* buf, int64_t bytes, uint32_t* sink, in
                      bytes / kProbeChunk, sink);
   return check_launch("read_probe_kernel");
 }
+
+// ---------------------------------------------------------------------------------
+// LDS gather probe: the cost of one ds_read_b128 wave-instruction for three lane ->
+// address patterns over a 128 KiB LDS buffer (one 16-wave workgroup per CU, every
+// offset masked into the buffer). It backs the PQ kernel's floor: its codebook gathers
+// are pattern 1. Not part of the scoring path; no reference counterpart.
+//   0: 16 consecutive lanes read 16 different 16-byte bank groups of random 256-byte
+//      rows (lane l -> group l % 16): conflict-free;
+//   1: the PQ gather: the 16 lanes of an MFMA lane group read random 16-byte rows of one
+//      4 KiB subspace block (bank group = row % 16, random);
+//   2: the 16 lanes of a lane group all read one bank group at random rows;
+//   3: lane l -> bank group (l / 4) % 16 at random rows: every bank group gets exactly
+//      four lanes of the wave, but four lanes of each 16-lane group share one.
+namespace tms {
+
+constexpr int kLdsProbeUnits = 8192;  // 16-byte units (128 KiB)
+constexpr int kLdsProbeOffs = 16;     // offsets per lane, cycled
+constexpr int kLdsProbeIters = 4096;
+
+__device__ __forceinline__ uint32_t probe_hash(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+__global__ void __launch_bounds__(1024) lds_probe_kernel(int pattern, int64_t* __restrict__ cycles,
+                                                         uint32_t* __restrict__ sink) {
+  extern __shared__ u32x4 probe_lds[];
+  for (int i = threadIdx.x; i < kLdsProbeUnits; i += 1024) probe_lds[i] = u32x4{(uint32_t)i, 1u, 2u, 3u};
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t o[kLdsProbeOffs];
+#pragma unroll
+  for (int j = 0; j < kLdsProbeOffs; j++) {
+    const uint32_t h = probe_hash((uint32_t)(((blockIdx.x * 16 + wave) * 64 + lane) * kLdsProbeOffs + j));
+    uint32_t u;
+    if (pattern == 0) u = (h % 512u) * 16u + (uint32_t)(lane & 15);
+    else if (pattern == 1) u = (uint32_t)((j + 4 * (lane >> 4)) & 15) * 256u + (h % 256u);
+    else if (pattern == 2) u = (h % 512u) * 16u + (uint32_t)(lane >> 4);
+    else u = (h % 512u) * 16u + (uint32_t)((lane >> 2) & 15);
+    o[j] = u & (kLdsProbeUnits - 1);
+  }
+  __syncthreads();
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const uint64_t t0 = __builtin_readcyclecounter();
+  for (int it = 0; it < kLdsProbeIters; it++) {
+#pragma unroll
+    for (int j = 0; j < kLdsProbeOffs; j++) acc ^= probe_lds[o[j]];
+#pragma unroll
+    for (int j = 0; j < kLdsProbeOffs; j++) asm volatile("" : "+v"(o[j]));  // keeps the loads in the loop
+  }
+  const uint64_t t1 = __builtin_readcyclecounter();
+  if (lane == 0) cycles[blockIdx.x * 16 + wave] = (int64_t)(t1 - t0);
+  sink[blockIdx.x * 1024 + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+}
+
+}  // namespace tms
+
+extern "C" int tms_lds_probe(int pattern, int64_t* cycles, int64_t cycle_words, uint32_t* sink, int64_t sink_words,
+                             void* stream) {
+  const char* fn = "tms_lds_probe";
+  if (pattern < 0 || pattern > 3) return fail(TMS_ERR_INVALID, "%s: pattern=%d must be 0 to 3", fn, pattern);
+  if (!cycles || cycle_words < TMS_LDS_PROBE_WAVES)
+    return fail(TMS_ERR_INVALID, "%s: cycles needs %d words", fn, TMS_LDS_PROBE_WAVES);
+  if (!sink || sink_words < TMS_LDS_PROBE_WAVES * 64)
+    return fail(TMS_ERR_INVALID, "%s: the sink needs %d words", fn, TMS_LDS_PROBE_WAVES * 64);
+  hipLaunchKernelGGL(lds_probe_kernel, dim3(TMS_LDS_PROBE_WAVES / 16), dim3(1024), kLdsProbeUnits * 16,
+                     (hipStream_t)stream, pattern, cycles, sink);
+  return check_launch("lds_probe_kernel");
+}
