@@ -11,8 +11,12 @@
 // shrinks a row by kChunk / k until one chunk holds it; the last level sorts its k keys.
 // Intermediate keys live in a caller-provided workspace. Selection is a radix select on
 // the 64-bit keys held in registers (16 per thread): one 256-bin LDS histogram per 8-bit
-// digit, from the top, narrowed to the keys that share the digits fixed so far, until
-// the k-th largest key is known or a whole bin is needed (usually 3-4 passes).
+// digit, from the highest bit at which the chunk's real keys differ, narrowed to the
+// keys that share the digits fixed so far, until the k-th largest key is known or a
+// whole bin is needed (two or three passes for rows of similar scores). Padding keys are
+// all 0 and a chunk's keys often share a digit, so the histogram updates would pile onto
+// a few bins: each thread adds a run of equal bins with one atomic, and each wave counts
+// into its own copy of the histogram.
 #include <string.h>
 
 #include <atomic>
@@ -23,8 +27,9 @@
 namespace tms {
 
 constexpr int kChunk = 4096;  // keys sorted per workgroup (32 KiB of LDS)
-constexpr int kTopkThreads = 256;
+constexpr int kTopkThreads = 1024;  // 16 waves: four per SIMD, so the serial steps of one chunk overlap
 constexpr int kMaxK = kChunk / 4;
+constexpr int kRankSortMaxK = 256;  // the last level orders up to this many keys by rank, more by a bitonic sort
 
 // Order-preserving image of a float's bits. -0.0 is taken as +0.0 (they compare equal,
 // so they tie and go by index) and every NaN as the positive quiet NaN, so that a NaN
@@ -39,8 +44,60 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 // FIRST: input is fp32 scores (row stride in_stride), indices are positions in the row.
 // Otherwise input is keys. LAST: write (value, index) pairs in descending order;
 // otherwise write the best k keys of the chunk, in no particular order.
-constexpr int kPerThread = kChunk / kTopkThreads;  // 16 keys per thread
-static_assert(kTopkThreads == 256, "one histogram bin per thread; wave 0 scans four bins per lane");
+constexpr int kPerThread = kChunk / kTopkThreads;  // 4 keys per thread
+constexpr int kHistCopies = 4;                     // wave w counts into copy w % 4
+static_assert(kTopkThreads == kHistCopies * 256, "each thread clears one histogram entry; wave 0 scans four bins per lane");
+constexpr int kTopkWaves = kTopkThreads / 64;
+
+// Cross-lane steps without the LDS: DPP within 16-lane rows, row swaps across them.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, true);
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  return ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL>((uint32_t)v);
+}
+// The value of lane l ^ 32 (permlane32_swap) or of the other row of the pair (row ^ 1,
+// permlane16_swap), for a value every lane holds.
+__device__ __forceinline__ uint32_t swap32_u32(uint32_t v, int lane) {
+  const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return lane < 32 ? (uint32_t)p[1] : (uint32_t)p[0];
+}
+__device__ __forceinline__ uint32_t swap16_u32(uint32_t v, int lane) {
+  const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return ((lane >> 4) & 1) ? (uint32_t)p[0] : (uint32_t)p[1];
+}
+__device__ __forceinline__ uint64_t swap32_u64(uint64_t v, int lane) {
+  return ((uint64_t)swap32_u32((uint32_t)(v >> 32), lane) << 32) | swap32_u32((uint32_t)v, lane);
+}
+__device__ __forceinline__ uint64_t swap16_u64(uint64_t v, int lane) {
+  return ((uint64_t)swap16_u32((uint32_t)(v >> 32), lane) << 32) | swap16_u32((uint32_t)v, lane);
+}
+// Wave-wide min and max of 64-bit values and sum of counts; every lane gets the result.
+__device__ __forceinline__ void wave_minmax(uint64_t& lo, uint64_t& hi, uint32_t& n, int lane) {
+  auto step = [&](uint64_t l2, uint64_t h2, uint32_t n2) {
+    lo = l2 < lo ? l2 : lo;
+    hi = h2 > hi ? h2 : hi;
+    n += n2;
+  };
+  step(dpp_u64<0xB1>(lo), dpp_u64<0xB1>(hi), dpp_u32<0xB1>(n));     // quad_perm [1,0,3,2]
+  step(dpp_u64<0x4E>(lo), dpp_u64<0x4E>(hi), dpp_u32<0x4E>(n));     // quad_perm [2,3,0,1]
+  step(dpp_u64<0x141>(lo), dpp_u64<0x141>(hi), dpp_u32<0x141>(n));  // row_half_mirror
+  step(dpp_u64<0x140>(lo), dpp_u64<0x140>(hi), dpp_u32<0x140>(n));  // row_mirror
+  step(swap16_u64(lo, lane), swap16_u64(hi, lane), swap16_u32(n, lane));
+  step(swap32_u64(lo, lane), swap32_u64(hi, lane), swap32_u32(n, lane));
+}
+// Inclusive prefix sum over the 64 lanes (lane order): row shifts, then row broadcasts.
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x) {
+  x += dpp_u32<0x111>(x);  // row_shr:1
+  x += dpp_u32<0x112>(x);  // row_shr:2
+  x += dpp_u32<0x114>(x);  // row_shr:4
+  x += dpp_u32<0x118>(x);  // row_shr:8
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);  // row_bcast:15 into rows 1, 3
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);  // row_bcast:31 into rows 2, 3
+  return x;
+}
 
 // The values written by the LAST level are read back from the scores (vals, row stride
 // val_stride) at the selected indices, so they keep the input's bits (-0.0, NaN payloads).
@@ -50,52 +107,123 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
                                                                   int64_t in_stride, uint64_t* __restrict__ keys_out,
                                                                   int64_t out_stride, float* __restrict__ out_vals,
                                                                   int64_t* __restrict__ out_idx, int k) {
-  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist[kHistCopies][256];
   __shared__ uint32_t pick[3];  // digit, keys above its bin, keys in its bin
   __shared__ uint32_t n_gt, n_eq;
   __shared__ uint64_t sel[LAST ? kMaxK : 1];
+  // FIRST && LAST (a row that fits one chunk): the selected scores' own bits, kept from
+  // the loads so the output needs no second read of the scores.
+  __shared__ uint32_t sel_bits[(FIRST && LAST) ? kMaxK : 1];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t row = blockIdx.y;
   const int64_t c0 = (int64_t)blockIdx.x * kChunk;
+  // All loads are issued before any key is formed (one memory round trip, not one per
+  // element); positions past the row read its last element and become padding.
   uint64_t key[kPerThread];
+  float v[kPerThread];
+  if constexpr (FIRST) {
 #pragma unroll
-  for (int e = 0; e < kPerThread; e++) {
-    const int64_t p = c0 + e * kTopkThreads + tid;
-    key[e] = 0;  // below every real element
-    if (p < n_in) {
-      if constexpr (FIRST) {
-        key[e] = ((uint64_t)order_key(vals[row * val_stride + p]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)p);
-      } else {
-        key[e] = keys_in[row * in_stride + p];
-      }
+    for (int e = 0; e < kPerThread; e++) {
+      const int64_t p = c0 + e * kTopkThreads + tid;
+      v[e] = vals[row * val_stride + (p < n_in ? p : n_in - 1)];
+    }
+#pragma unroll
+    for (int e = 0; e < kPerThread; e++) {
+      const int64_t p = c0 + e * kTopkThreads + tid;
+      key[e] = p < n_in ? ((uint64_t)order_key(v[e]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)p)
+                        : 0ull;  // below every real element
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kPerThread; e++) {
+      const int64_t p = c0 + e * kTopkThreads + tid;
+      key[e] = keys_in[row * in_stride + (p < n_in ? p : n_in - 1)];
+    }
+#pragma unroll
+    for (int e = 0; e < kPerThread; e++) {
+      const int64_t p = c0 + e * kTopkThreads + tid;
+      key[e] = p < n_in ? key[e] : 0ull;
     }
   }
 
-  // Radix select. After a pass, `prefix` holds the digits fixed so far and `need` the
-  // number of keys still to take among the keys that share them.
-  uint64_t prefix = 0;
-  uint32_t need = (uint32_t)k;
+  // Where the real keys differ: the radix passes start below the bits that every real
+  // key shares (scores in one binade share sign, exponent and the top mantissa bits), so
+  // a row of similar scores takes two or three passes instead of up to eight. Padding
+  // keys (0) are not real; a chunk with fewer than k real keys starts from the top.
+  __shared__ uint64_t red_lo[kTopkWaves], red_hi[kTopkWaves];
+  __shared__ uint32_t red_n[kTopkWaves];
+  {
+    uint64_t lo = ~0ull, hi = 0ull;
+    uint32_t nr = 0u;
+#pragma unroll
+    for (int e = 0; e < kPerThread; e++) {
+      if (key[e] != 0ull) {
+        lo = key[e] < lo ? key[e] : lo;
+        hi = key[e] > hi ? key[e] : hi;
+        nr++;
+      }
+    }
+    wave_minmax(lo, hi, nr, lane);
+    if (lane == 0) {
+      red_lo[wid] = lo;
+      red_hi[wid] = hi;
+      red_n[wid] = nr;
+    }
+  }
+  __syncthreads();
+  uint64_t prefix = 0;  // the key bits fixed so far: candidates have key >> shift == prefix
   int shift = 64;
+  {
+    uint64_t lo = red_lo[0], hi = red_hi[0];
+    uint32_t nr = red_n[0];
+#pragma unroll
+    for (int w = 1; w < kTopkWaves; w++) {
+      lo = red_lo[w] < lo ? red_lo[w] : lo;
+      hi = red_hi[w] > hi ? red_hi[w] : hi;
+      nr += red_n[w];
+    }
+    if (nr >= (uint32_t)k) {
+      const uint64_t diff = hi ^ lo;
+      shift = diff == 0ull ? 0 : 64 - __builtin_clzll(diff);
+      prefix = shift == 64 ? 0ull : hi >> shift;
+    }
+  }
+
+  // Radix select, 8-bit digits (narrower for the last one). After a pass, `need` is the
+  // number of keys still to take among the keys that share the prefix.
+  uint32_t need = (uint32_t)k;
   bool whole_bin = false;  // the selection is every key >= prefix << shift
   while (shift > 0) {
-    shift -= 8;
-    hist[tid] = 0u;
+    const int w = shift < 8 ? shift : 8;
+    shift -= w;
+    (&hist[0][0])[tid] = 0u;
     __syncthreads();
+    {
+      uint32_t run_bin = 0u, run_n = 0u;  // a run of this thread's keys in one bin
 #pragma unroll
-    for (int e = 0; e < kPerThread; e++)
-      if (shift == 56 || (key[e] >> (shift + 8)) == prefix) atomicAdd(&hist[(uint32_t)(key[e] >> shift) & 255u], 1u);
+      for (int e = 0; e < kPerThread; e++) {
+        if (shift + w == 64 || (key[e] >> (shift + w)) == prefix) {
+          const uint32_t bin = (uint32_t)(key[e] >> shift) & ((1u << w) - 1u);
+          if (run_n != 0u && bin != run_bin) {
+            atomicAdd(&hist[wid % kHistCopies][run_bin], run_n);
+            run_n = 0u;
+          }
+          run_bin = bin;
+          run_n++;
+        }
+      }
+      if (run_n != 0u) atomicAdd(&hist[wid % kHistCopies][run_bin], run_n);
+    }
     __syncthreads();
     if (wid == 0) {  // lane l scans bins 255 - 4l .. 252 - 4l, high to low
       uint32_t c[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) c[j] = hist[255 - 4 * lane - j];
-      const uint32_t own = c[0] + c[1] + c[2] + c[3];
-      uint32_t incl = own;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t y = __shfl_up(incl, o);
-        if (lane >= o) incl += y;
+      for (int j = 0; j < 4; j++) {
+        const int bin = 255 - 4 * lane - j;
+        c[j] = hist[0][bin] + hist[1][bin] + hist[2][bin] + hist[3][bin];
       }
+      const uint32_t own = c[0] + c[1] + c[2] + c[3];
+      const uint32_t incl = wave_inclusive_sum(own);
       const uint32_t excl = incl - own;
       if (excl < need && need <= incl) {  // exactly one lane: the need-th key is in its bins
         uint32_t above = excl;
@@ -109,13 +237,14 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
     __syncthreads();
     const uint32_t d = pick[0], above = pick[1], cnt = pick[2];
     need -= above;
-    prefix = (prefix << 8) | d;
+    prefix = (prefix << w) | d;
     if (cnt == need && prefix != 0) {  // the whole bin is needed (keys are unique but padding)
       whole_bin = true;
       break;
     }
   }
   // Selection: every key > T, then `need` keys equal to T (only padding keys repeat).
+  // Each wave reserves its slots with one atomic per 64 keys (ballot and lane count).
   const uint64_t T = whole_bin ? (prefix << shift) - 1 : prefix;
   const uint32_t need_eq = whole_bin ? 0u : need;
   if (tid == 0) {
@@ -123,21 +252,77 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
     n_eq = 0u;
   }
   __syncthreads();
-  auto put = [&](uint32_t pos, uint64_t kv) {
+  auto put = [&](uint32_t pos, uint64_t kv, int e) {
+    if constexpr (FIRST && LAST) sel_bits[pos] = __builtin_bit_cast(uint32_t, v[e]);
     if constexpr (LAST) sel[pos] = kv;
     else keys_out[row * out_stride + (int64_t)blockIdx.x * k + pos] = kv;
   };
+  auto below = [&](uint64_t m) -> uint32_t {  // set bits of m in lanes below this one
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+  };
+  // The wave's selected keys in element order: ballots first, then one atomic per wave
+  // for all of them (and one for the keys equal to T, which only padding can need).
+  uint64_t mg[kPerThread];
+  uint32_t wave_gt = 0u, wave_eq = 0u;
+  uint64_t any_eq = 0ull;
 #pragma unroll
   for (int e = 0; e < kPerThread; e++) {
-    if (key[e] > T) {
-      const uint32_t pos = atomicAdd(&n_gt, 1u);
-      if (pos < (uint32_t)k - need_eq) put(pos, key[e]);  // always true; bounds every write
-    } else if (key[e] == T && need_eq > 0u) {
-      const uint32_t j = atomicAdd(&n_eq, 1u);
-      if (j < need_eq) put((uint32_t)k - need_eq + j, key[e]);
+    mg[e] = __ballot(key[e] > T);
+    wave_gt += (uint32_t)__popcll(mg[e]);
+    if (need_eq > 0u) {
+      const uint64_t me = __ballot(key[e] == T);
+      any_eq |= me;
+      wave_eq += (uint32_t)__popcll(me);
+    }
+  }
+  uint32_t base_gt = 0u, base_eq = 0u;
+  if (lane == 0 && wave_gt > 0u) base_gt = atomicAdd(&n_gt, wave_gt);
+  if (lane == 0 && wave_eq > 0u) base_eq = atomicAdd(&n_eq, wave_eq);
+  base_gt = (uint32_t)__builtin_amdgcn_readlane((int)base_gt, 0);
+  base_eq = (uint32_t)__builtin_amdgcn_readlane((int)base_eq, 0);
+#pragma unroll
+  for (int e = 0; e < kPerThread; e++) {
+    if (mg[e] != 0ull) {
+      const uint32_t pos = base_gt + below(mg[e]);
+      if (key[e] > T && pos < (uint32_t)k - need_eq) put(pos, key[e], e);  // always below; bounds every write
+      base_gt += (uint32_t)__popcll(mg[e]);
+    }
+    if (any_eq != 0ull) {
+      const uint64_t me = __ballot(key[e] == T);
+      const uint32_t j = base_eq + below(me);
+      if (key[e] == T && j < need_eq) put((uint32_t)k - need_eq + j, key[e], e);
+      base_eq += (uint32_t)__popcll(me);
     }
   }
   if constexpr (LAST) {
+    __syncthreads();
+    if (k <= kRankSortMaxK) {  // every selected key is real, so all are distinct: rank = keys above it
+      const int k8 = (k + 7) & ~7;  // k rounded up to a multiple of 8; the slots past k hold 0, below every real key
+      if (tid < k8 - k) sel[k + tid] = 0ull;
+      __syncthreads();
+      // Eight lanes share a key (k <= 128): lane part p counts the keys above it among
+      // slots [p * k8 / 8, (p + 1) * k8 / 8), and three DPP steps add the eight counts.
+      const bool split8 = k * 8 <= kTopkThreads;
+      const int per = split8 ? k8 / 8 : k8;
+      for (int t = tid; t < (split8 ? 8 * k8 : k); t += kTopkThreads) {
+        const int i = split8 ? t >> 3 : t;
+        const uint64_t me = sel[i];  // slots in [k, k8) are padding zeros: they rank below
+        const int j0 = split8 ? (t & 7) * per : 0;
+        uint32_t rank = 0u;
+        for (int j = j0; j < j0 + per; j++) rank += sel[j] > me ? 1u : 0u;
+        if (split8) {
+          rank += dpp_u32<0xB1>(rank);   // quad_perm [1,0,3,2]
+          rank += dpp_u32<0x4E>(rank);   // quad_perm [2,3,0,1]
+          rank += dpp_u32<0x141>(rank);  // row_half_mirror: the other quad of the eight
+          if ((t & 7) != 0 || i >= k) continue;
+        }
+        const int64_t idx = (int64_t)(0xffffffffu - (uint32_t)me);
+        if constexpr (FIRST) out_vals[row * k + rank] = __builtin_bit_cast(float, sel_bits[i]);
+        else out_vals[row * k + rank] = vals[row * val_stride + (idx < val_stride ? idx : val_stride - 1)];
+        out_idx[row * k + rank] = idx;
+      }
+      return;
+    }
     int P = 1;  // bitonic sort of the k survivors, padded to a power of two
     while (P < k) P <<= 1;
     for (int i = k + tid; i < P; i += kTopkThreads) sel[i] = 0;
