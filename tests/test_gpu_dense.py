@@ -172,6 +172,29 @@ def test_determinism(cuda):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+@pytest.mark.parametrize("nq,Nd,d,dtype,B", [(32, 128, 128, "fp16", 6000), (64, 180, 128, "fp16", 6000),
+                                             (20, 33, 96, "bf16", 60000), (70, 7, 64, "fp16", 300000),
+                                             (32, 300, 32, "bf16", 6000)])
+def test_scores_do_not_depend_on_the_batch(cuda, nq, Nd, d, dtype, B):
+    """A wave walks a run of documents whose length depends on B (192 tokens' worth for
+    large B, one document for small B), so the same document lands at a different place
+    in a different wave's run. Its score must not depend on that: the first documents of
+    a B-document call, scored again in calls of 1000, 300 and 37 documents, give the same
+    bits, and match the oracle."""
+    import torch
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(nq + Nd + d)
+    Q = torch.nn.functional.normalize(torch.randn(nq, d, device="cuda", generator=g), dim=-1).to(tdt)
+    D = torch.nn.functional.normalize(torch.randn(B, Nd, d, device="cuda", generator=g), dim=-1).to(tdt)
+    big = flash_maxsim_v2_multiquery(Q, D).cpu().numpy()
+    for b in (1000, 300, 37):
+        small = flash_maxsim_v2_multiquery(Q, D[:b].contiguous()).cpu().numpy()
+        assert np.array_equal(small.view(np.uint32), big[:b].view(np.uint32)), f"B={b}"
+    _assert_scores(big[:37], orc.maxsim_f64(Q.float().cpu().numpy(), D[:37].float().cpu().numpy()),
+                   "first 37 documents")
+
+
 def test_single_and_batch_entry_points(cuda):
     from tilemaxsim_amd import flash_maxsim_batch, flash_maxsim_single, flash_maxsim_v2
     rng = _rng(21)
