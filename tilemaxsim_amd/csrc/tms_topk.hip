@@ -10,7 +10,7 @@
 // Tournament: a workgroup selects the best k of a chunk of kChunk keys and each level
 // shrinks a row by kChunk / k until one chunk holds it; the last level sorts its k keys.
 // Intermediate keys live in a caller-provided workspace. Selection is a radix select on
-// the 64-bit keys held in registers (16 per thread): one 256-bin LDS histogram per 8-bit
+// the 64-bit keys held in registers (4 or 16 per thread): one 256-bin LDS histogram per 8-bit
 // digit, from the highest bit at which the chunk's real keys differ, narrowed to the
 // keys that share the digits fixed so far, until the k-th largest key is known or a
 // whole bin is needed (two or three passes for rows of similar scores). Padding keys are
@@ -27,7 +27,13 @@
 namespace tms {
 
 constexpr int kChunk = 4096;  // keys sorted per workgroup (32 KiB of LDS)
-constexpr int kTopkThreads = 1024;  // 16 waves: four per SIMD, so the serial steps of one chunk overlap
+// Threads per workgroup: a level that shrinks many chunks at once runs 4 waves per chunk
+// (16 keys per thread); the last level, one chunk per row and nothing else running
+// beside it, runs 16 waves (4 keys per thread, four waves per SIMD to overlap its serial
+// steps). Measured on MaxSim-like and Gaussian rows, each is the faster of the two for
+// its level.
+constexpr int kLevelThreads = 256;
+constexpr int kLastThreads = 1024;
 constexpr int kMaxK = kChunk / 4;
 constexpr int kRankSortMaxK = 256;  // the last level orders up to this many keys by rank, more by a bitonic sort
 
@@ -44,10 +50,7 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 // FIRST: input is fp32 scores (row stride in_stride), indices are positions in the row.
 // Otherwise input is keys. LAST: write (value, index) pairs in descending order;
 // otherwise write the best k keys of the chunk, in no particular order.
-constexpr int kPerThread = kChunk / kTopkThreads;  // 4 keys per thread
-constexpr int kHistCopies = 4;                     // wave w counts into copy w % 4
-static_assert(kTopkThreads == kHistCopies * 256, "each thread clears one histogram entry; wave 0 scans four bins per lane");
-constexpr int kTopkWaves = kTopkThreads / 64;
+constexpr int kHistCopies = 4;  // wave w counts into copy w % 4; wave 0 scans four bins per lane
 
 // Cross-lane steps without the LDS: DPP within 16-lane rows, row swaps across them.
 template <int CTRL>
@@ -101,12 +104,15 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x) {
 
 // The values written by the LAST level are read back from the scores (vals, row stride
 // val_stride) at the selected indices, so they keep the input's bits (-0.0, NaN payloads).
-template <bool FIRST, bool LAST>
-__global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* __restrict__ vals, int64_t val_stride,
+template <bool FIRST, bool LAST, int NT>
+__global__ void __launch_bounds__(NT) topk_level_kernel(const float* __restrict__ vals, int64_t val_stride,
                                                                   const uint64_t* __restrict__ keys_in, int64_t n_in,
                                                                   int64_t in_stride, uint64_t* __restrict__ keys_out,
                                                                   int64_t out_stride, float* __restrict__ out_vals,
                                                                   int64_t* __restrict__ out_idx, int k) {
+  constexpr int kPerThread = kChunk / NT;
+  constexpr int kTopkWaves = NT / 64;
+  static_assert(NT % 256 == 0 && NT <= kHistCopies * 256, "histogram clearing and the per-wave copies");
   __shared__ uint32_t hist[kHistCopies][256];
   __shared__ uint32_t pick[3];  // digit, keys above its bin, keys in its bin
   __shared__ uint32_t n_gt, n_eq;
@@ -124,24 +130,24 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
   if constexpr (FIRST) {
 #pragma unroll
     for (int e = 0; e < kPerThread; e++) {
-      const int64_t p = c0 + e * kTopkThreads + tid;
+      const int64_t p = c0 + e * NT + tid;
       v[e] = vals[row * val_stride + (p < n_in ? p : n_in - 1)];
     }
 #pragma unroll
     for (int e = 0; e < kPerThread; e++) {
-      const int64_t p = c0 + e * kTopkThreads + tid;
+      const int64_t p = c0 + e * NT + tid;
       key[e] = p < n_in ? ((uint64_t)order_key(v[e]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)p)
                         : 0ull;  // below every real element
     }
   } else {
 #pragma unroll
     for (int e = 0; e < kPerThread; e++) {
-      const int64_t p = c0 + e * kTopkThreads + tid;
+      const int64_t p = c0 + e * NT + tid;
       key[e] = keys_in[row * in_stride + (p < n_in ? p : n_in - 1)];
     }
 #pragma unroll
     for (int e = 0; e < kPerThread; e++) {
-      const int64_t p = c0 + e * kTopkThreads + tid;
+      const int64_t p = c0 + e * NT + tid;
       key[e] = p < n_in ? key[e] : 0ull;
     }
   }
@@ -196,7 +202,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
   while (shift > 0) {
     const int w = shift < 8 ? shift : 8;
     shift -= w;
-    (&hist[0][0])[tid] = 0u;
+    for (int i = tid; i < kHistCopies * 256; i += NT) (&hist[0][0])[i] = 0u;
     __syncthreads();
     {
       uint32_t run_bin = 0u, run_n = 0u;  // a run of this thread's keys in one bin
@@ -302,9 +308,9 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
       __syncthreads();
       // Eight lanes share a key (k <= 128): lane part p counts the keys above it among
       // slots [p * k8 / 8, (p + 1) * k8 / 8), and three DPP steps add the eight counts.
-      const bool split8 = k * 8 <= kTopkThreads;
+      const bool split8 = k * 8 <= NT;
       const int per = split8 ? k8 / 8 : k8;
-      for (int t = tid; t < (split8 ? 8 * k8 : k); t += kTopkThreads) {
+      for (int t = tid; t < (split8 ? 8 * k8 : k); t += NT) {
         const int i = split8 ? t >> 3 : t;
         const uint64_t me = sel[i];  // slots in [k, k8) are padding zeros: they rank below
         const int j0 = split8 ? (t & 7) * per : 0;
@@ -325,11 +331,11 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
     }
     int P = 1;  // bitonic sort of the k survivors, padded to a power of two
     while (P < k) P <<= 1;
-    for (int i = k + tid; i < P; i += kTopkThreads) sel[i] = 0;
+    for (int i = k + tid; i < P; i += NT) sel[i] = 0;
     __syncthreads();
     for (int size = 2; size <= P; size <<= 1) {
       for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int i = tid; i < P / 2; i += kTopkThreads) {
+        for (int i = tid; i < P / 2; i += NT) {
           const int pos = 2 * i - (i & (stride - 1));
           const int partner = pos + stride;
           const bool desc = (pos & size) == 0;
@@ -342,7 +348,7 @@ __global__ void __launch_bounds__(kTopkThreads) topk_level_kernel(const float* _
         __syncthreads();
       }
     }
-    for (int i = tid; i < k; i += kTopkThreads) {
+    for (int i = tid; i < k; i += NT) {
       const int64_t idx = (int64_t)(0xffffffffu - (uint32_t)sel[i]);
       // a selected key is always a real element (k <= n); the clamp only bounds the read
       out_vals[row * k + i] = vals[row * val_stride + (idx < val_stride ? idx : val_stride - 1)];
@@ -458,15 +464,15 @@ static int topk_run(const float* scores, int64_t nrows, int64_t n, int64_t k, vo
   int64_t strides[2] = {amax, 0};
   for (int64_t i = 1; i < lv; i += 2) strides[1] = sizes[i] > strides[1] ? sizes[i] : strides[1];
 
-  const dim3 block(kTopkThreads);
+  const dim3 last_block(kLastThreads), level_block(kLevelThreads);
   if (lv == 0) {
-    hipLaunchKernelGGL((topk_level_kernel<true, true>), dim3(1, (unsigned)nrows), block, 0, st, scores, n, nullptr, n,
-                       n, nullptr, 0, out_values, out_indices, (int)k);
+    hipLaunchKernelGGL((topk_level_kernel<true, true, kLastThreads>), dim3(1, (unsigned)nrows), last_block, 0, st,
+                       scores, n, nullptr, n, n, nullptr, 0, out_values, out_indices, (int)k);
     return check_launch("topk_level_kernel");
   }
   // level 0: scores -> keys
-  hipLaunchKernelGGL((topk_level_kernel<true, false>), dim3((unsigned)ceil_div(n, kChunk), (unsigned)nrows), block, 0,
-                     st, scores, n, nullptr, n, n, bufs[0], strides[0], nullptr, nullptr, (int)k);
+  hipLaunchKernelGGL((topk_level_kernel<true, false, kLevelThreads>), dim3((unsigned)ceil_div(n, kChunk), (unsigned)nrows),
+                     level_block, 0, st, scores, n, nullptr, n, n, bufs[0], strides[0], nullptr, nullptr, (int)k);
   int rc = check_launch("topk_level_kernel");
   if (rc) return rc;
   for (int64_t i = 1; i <= lv; i++) {
@@ -474,12 +480,12 @@ static int topk_run(const float* scores, int64_t nrows, int64_t n, int64_t k, vo
     const uint64_t* in = bufs[(i - 1) % 2];
     const int64_t in_stride = strides[(i - 1) % 2];
     if (i == lv) {
-      hipLaunchKernelGGL((topk_level_kernel<false, true>), dim3(1, (unsigned)nrows), block, 0, st, scores, n, in,
-                         n_in, in_stride, nullptr, 0, out_values, out_indices, (int)k);
+      hipLaunchKernelGGL((topk_level_kernel<false, true, kLastThreads>), dim3(1, (unsigned)nrows), last_block, 0, st,
+                         scores, n, in, n_in, in_stride, nullptr, 0, out_values, out_indices, (int)k);
     } else {
-      hipLaunchKernelGGL((topk_level_kernel<false, false>), dim3((unsigned)ceil_div(n_in, kChunk), (unsigned)nrows),
-                         block, 0, st, scores, n, in, n_in, in_stride, bufs[i % 2], strides[i % 2], nullptr,
-                         nullptr, (int)k);
+      hipLaunchKernelGGL((topk_level_kernel<false, false, kLevelThreads>),
+                         dim3((unsigned)ceil_div(n_in, kChunk), (unsigned)nrows), level_block, 0, st, scores, n, in,
+                         n_in, in_stride, bufs[i % 2], strides[i % 2], nullptr, nullptr, (int)k);
     }
     rc = check_launch("topk_level_kernel");
     if (rc) return rc;
