@@ -57,7 +57,7 @@ def parse():
                             "readprobe", "ldsprobe"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--dtype", default="fp16", choices=["fp16", "bf16", "fp32"],
-                   help="embedding dtype for --config c1, c2, c4 and prec")
+                   help="embedding dtype for --config c1, c2, c2b, c4 and prec")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
@@ -144,7 +144,7 @@ class Dense:
         """C2 only, after the timed steps: the same step (every query against every
         document, then the top-k) with all queries in one flash_maxsim_batched_queries
         call per step; HIP events around each call and around each whole step."""
-        if self.name != "c2" or self.dtype == "fp32":  # fp32 has no shared-tile kernel
+        if self.name != "c2" or self.dtype == "fp32":  # fp32 runs batched as --config c2b --dtype fp32
             return None
         from tilemaxsim_amd import flash_maxsim_batched_queries
         calls, whole = [], []
@@ -255,6 +255,7 @@ class DenseBatched(Dense):
     eight waves hold 32 query blocks and share one HBM pass over the documents, which
     moves the path from the HBM roof to the MFMA roof."""
     MFMA_PEAK_TFLOPS = 2500.0
+    MFMA_PEAK_TFLOPS_F32 = 157.3
 
     def __init__(self, *args, **kw):
         super().__init__(*args, **kw)
@@ -270,12 +271,20 @@ class DenseBatched(Dense):
         return 2 * self.nQ * self.Nq * self.B * self.Nd * self.d
 
     def bytes_per_launch(self):  # algorithmic: every query against one read of the corpus
-        return self.nQ * self.Nq * self.d * 2 + self.B * self.Nd * self.d * 2 + self.nQ * self.B * 4
+        return (self.nQ * self.Nq * self.d + self.B * self.Nd * self.d) * self.esize + self.nQ * self.B * 4
 
     launch_desc = "one flash_maxsim_batched_queries call (one kernel per 32 query blocks)"
 
     def extra_roofline(self, launch_ms):
-        return gemm_ceiling(self.torch, self.flops_per_launch() / (launch_ms * 1e-3) / 1e12)
+        tf = self.flops_per_launch() / (launch_ms * 1e-3) / 1e12
+        if self.dtype != "fp32":
+            return gemm_ceiling(self.torch, tf)
+        # fp32: priced against the fp32 dense MFMA peak; the kernel runs each product as
+        # three bf16 MFMAs (hi*hi + hi*lo + lo*hi), whose rate is given against bf16's peak
+        return {"peak": self.MFMA_PEAK_TFLOPS_F32, "frac": round(tf / self.MFMA_PEAK_TFLOPS_F32, 4),
+                "peak_note": "fp32 dense MFMA peak; products run as three bf16 MFMAs",
+                "bf16_mfma_executed_tflops": round(3 * tf, 1),
+                "bf16_mfma_executed_frac": round(3 * tf / self.MFMA_PEAK_TFLOPS, 4)}
 
     def config(self):
         c = super().config()
@@ -825,8 +834,8 @@ def main():
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); documents shard across GPUs "
               "with no communication besides a top-k merge, which is not part of this build", file=sys.stderr)
         sys.exit(2)
-    if args.dtype != "fp16" and args.config not in ("c1", "c2", "c4", "prec"):
-        print(f"bench.py: --dtype applies to --config c1, c2, c4 and prec (got {args.config})", file=sys.stderr)
+    if args.dtype != "fp16" and args.config not in ("c1", "c2", "c2b", "c4", "prec"):
+        print(f"bench.py: --dtype applies to --config c1, c2, c2b, c4 and prec (got {args.config})", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
@@ -843,7 +852,7 @@ def main():
         # the reference's precision experiment: 1 query, B = 10K, Nd = 128, d = 128, raw randn
         wl = Dense(torch, 1, 10_000, 128, 128, name="prec", dtype=args.dtype, normalize=False)
     elif args.config == "c2b":
-        wl = DenseBatched(torch, 64, 1_000_000, 180, 128, name="c2b")
+        wl = DenseBatched(torch, 64, 1_000_000, 180, 128, name="c2b", dtype=args.dtype)
     elif args.config == "c3":
         wl = Varlen(torch, 32, 2_000_000, 32, 300, 128)
     elif args.config == "c3b":

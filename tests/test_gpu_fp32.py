@@ -125,6 +125,37 @@ def test_fp32_misaligned_pointer_and_mixed_dtypes(cuda):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("nQ,nq,d", [(20, 32, 128), (6, 64, 64), (5, 40, 96), (3, 32, 32), (17, 64, 128)])
+def test_fp32_shared_tiles(cuda, nQ, nq, d):
+    """Several fp32 queries over the same fp32 documents: the shared-tile kernel (tiles
+    split into bf16 hi + lo in the LDS ring, 1 or 2 query blocks per wave, up to 16 per
+    pass), fixed-length and variable-length (empty documents, invalid offsets)."""
+    from tilemaxsim_amd import flash_maxsim_batched_queries, flash_maxsim_multi_doc_batched
+    rng = _rng(nQ * 100 + nq + d)
+    Qs = _randn(rng, (nQ, nq, d), True)
+    Dfix = _randn(rng, (70, 33, d), True)
+    got = flash_maxsim_batched_queries(_gpu(Qs), _gpu(Dfix)).cpu().numpy()
+    for q in range(nQ):
+        _assert_fp32_scores(got[q], orc.maxsim_f64(Qs[q], Dfix), orc.maxsim_f64(np.abs(Qs[q]), np.abs(Dfix)), d,
+                            f"fixed fp32 shared tiles q={q}")
+    lens = rng.integers(0, 60, 90)
+    lens[[0, 7, 89]] = 0
+    lens[1] = 10
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    flat = _randn(rng, (int(offsets[-1]), d), True)
+    got = flash_maxsim_multi_doc_batched(_gpu(Qs), _gpu(flat), _gpu(offsets)).cpu().numpy()
+    for q in range(nQ):
+        _assert_fp32_scores(got[q], orc.maxsim_varlen(Qs[q], flat, offsets, f64=True),
+                            orc.maxsim_varlen(np.abs(Qs[q]), np.abs(flat), offsets, f64=True), d,
+                            f"varlen fp32 shared tiles q={q}")
+    bad = offsets.copy()
+    bad[5] = bad[4] - 1  # document 4 ends before it starts (document 5 starts a row early)
+    got = flash_maxsim_multi_doc_batched(_gpu(Qs), _gpu(flat), _gpu(bad), validate=False).cpu().numpy()
+    assert np.all(np.isnan(got[:, 4]))
+    assert not np.isnan(np.delete(got, 4, axis=1)).any()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("d", [128, 768])  # Q in VGPRs; Q in LDS above 80 KiB (8-wave workgroups)
 def test_fp32_masked_varlen_and_batched(cuda, d):
     import torch

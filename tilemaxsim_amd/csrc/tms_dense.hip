@@ -118,6 +118,11 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   a.pad_len = pad_len;
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
   const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
+  // fp32 documents, several query blocks: the shared-tile kernel (one pass for up to 16
+  // blocks, three bf16 MFMAs per product) instead of one pass per two blocks
+  if (dtype == TMS_DTYPE_F32 && mode != MODE_MASKED && qreg && a.nbq <= 2 && nQ * a.nbq > 2)
+    return run_varlen_batched(Q, nQ, nq, d, D, mode == MODE_VARLEN ? total_tokens : B * nd,
+                              mode == MODE_VARLEN ? offsets : nullptr, nd, B, pad_len, dtype, out, st);
   if (dtype == TMS_DTYPE_F32) return run_dense<TMS_DTYPE_F32, TMS_DTYPE_F32>(a, nQ, mode, aligned, st);
   if (q32) return run_dense_q32(a, nQ, dtype, mode, aligned, st);
   if (mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, dtype, out, st);

@@ -248,19 +248,38 @@ struct BatchedArgs {
 
 // Tile sources. A loading wave fetches, per tile, the raw data of its lane's 8-dimension
 // chunk c of token `row`; the source turns it into the MFMA A-operand fragment.
+// Each tile chunk goes to the LDS ring as kParts 16-byte MFMA fragments: the fragment
+// itself, or (fp32 rows) its bf16 hi and lo terms.
 struct DenseTiles {  // fp16 / bf16 rows, stored to the ring as loaded
   static constexpr bool kDirect = true;
+  static constexpr int kParts = 1;
   typedef u32x4 Raw;
   __device__ static Raw load(const BatchedArgs& a, int64_t row, int c) {
     return *(const u32x4*)(a.D + row * a.d * 2 + 16 * c);
   }
   __device__ static u32x4 decode(const u32x4*, int, Raw raw, int) { return raw; }
+  __device__ static void parts(const Raw& raw, u32x4 (&out)[1]) { out[0] = raw; }
+};
+// fp32 rows (and fp32 queries): every element split into bf16 hi + lo terms as it goes
+// to the ring, a product formed from three bf16 MFMAs (lo*q_hi + hi*q_lo + hi*q_hi, the
+// per-query fp32 kernel's order), as in tms_dense_kernel.h.
+struct F32Tiles {
+  static constexpr bool kDirect = true;
+  static constexpr int kParts = 2;
+  typedef u32x8 Raw;
+  __device__ static Raw load(const BatchedArgs& a, int64_t row, int c) {
+    const u32x4* p = (const u32x4*)(a.D + row * a.d * 4 + 32 * c);
+    const u32x4 x0 = p[0], x1 = p[1];
+    return Raw{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+  }
+  __device__ static void parts(const Raw& raw, u32x4 (&out)[2]) { split_bf16(raw, out[0], out[1]); }
 };
 // uint8 PQ codes (M per token), decoded through the codebook held in LDS: chunk c covers
 // subspaces 8c / DSUB .. (8c + 7) / DSUB. Codes >= K are clamped into the table.
 template <int DSUB>
 struct PqTiles {
   static constexpr bool kDirect = false;
+  static constexpr int kParts = 1;
   typedef uint32_t Raw;
   __device__ static Raw load(const BatchedArgs& a, int64_t row, int c) {
     const uint8_t* p = a.D + row * a.M;
@@ -300,7 +319,10 @@ struct PqTiles {
 template <int DT, int KS, int NB, class SRC>
 __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel(BatchedArgs a) {
   constexpr int NS = 4;  // LDS ring slots and load lead, in tiles
-  __shared__ u32x4 ring[NS][4][64];
+  constexpr int NP = SRC::kParts;
+  constexpr bool SPLIT = NP == 2;  // fp32 rows and queries: DT is the MFMA type, bf16
+  static_assert(!SPLIT || DT == TMS_DTYPE_BF16, "split fp32 terms are bf16");
+  __shared__ u32x4 ring[NS][NP][4][64];
   extern __shared__ u32x4 cb[];  // PQ codebook
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g = lane >> 4;
@@ -320,6 +342,7 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
   int my_nblk = a.blk_end - my_blk0;  // <= 0 for a wave with no query
   if (my_nblk > a.nblk) my_nblk = a.nblk;
   u32x4 qf[NB][KS][2];
+  u32x4 qfl[SPLIT ? NB : 1][SPLIT ? KS : 1][2];  // fp32 queries: the lo terms
   bool qv[NB][2];
 #pragma unroll
   for (int j = 0; j < NB; j++)
@@ -332,8 +355,17 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
       const int64_t row = qv[j][h] ? (int64_t)qi * a.nq + tok : 0;
 #pragma unroll
       for (int s = 0; s < KS; s++) {
-        const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2);
-        qf[j][s][h] = qv[j][h] ? v : u32x4{0u, 0u, 0u, 0u};
+        if constexpr (SPLIT) {
+          const u32x4* p = (const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 4);
+          const u32x4 x0 = p[0], x1 = p[1];
+          u32x4 hi, lo;
+          split_bf16(u32x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]}, hi, lo);
+          qf[j][s][h] = qv[j][h] ? hi : u32x4{0u, 0u, 0u, 0u};
+          qfl[j][s][h] = qv[j][h] ? lo : u32x4{0u, 0u, 0u, 0u};
+        } else {
+          const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2);
+          qf[j][s][h] = qv[j][h] ? v : u32x4{0u, 0u, 0u, 0u};
+        }
       }
     }
 
@@ -426,14 +458,26 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
     u32x4 ahead = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int t = 0; t < NS; t++) stg[t] = load();
+    auto put = [&](int slot, const Raw& raw) {  // a direct source's tile to a ring slot
+      u32x4 pv[NP];
+      if constexpr (SRC::kDirect) SRC::parts(raw, pv);
+#pragma unroll
+      for (int p = 0; p < NP; p++) ring[slot][p][wid][lane] = pv[p];
+    };
     if constexpr (LD) {
-      ring[0][wid][lane] = SRC::decode(cb, a.K, stg[0], chunk);
-      if constexpr (!SRC::kDirect) ahead = SRC::decode(cb, a.K, stg[1], chunk);
+      if constexpr (SRC::kDirect) {
+        put(0, stg[0]);
+      } else {
+        ring[0][0][wid][lane] = SRC::decode(cb, a.K, stg[0], chunk);
+        ahead = SRC::decode(cb, a.K, stg[1], chunk);
+      }
     }
     sync();
-    u32x4 frag[2][KS];
+    u32x4 frag[2][NP][KS];
 #pragma unroll
-    for (int s = 0; s < KS; s++) frag[0][s] = ring[0][s][lane];
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+      for (int s = 0; s < KS; s++) frag[0][p][s] = ring[0][p][s][lane];
     float rmax[NB][2];
 #pragma unroll
     for (int j = 0; j < NB; j++) rmax[j][0] = rmax[j][1] = NEG_INF;
@@ -445,16 +489,19 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
       stg[i] = load();  // tile i + NS (stg[i] was tile i, in the ring since the last step)
       if constexpr (LD) {
         if constexpr (SRC::kDirect) {
-          ring[s1][wid][lane] = stg[s1];  // tile i+1
+          put(s1, stg[s1]);  // tile i+1
         } else {
-          ring[s1][wid][lane] = ahead;                               // tile i+1
+          ring[s1][0][wid][lane] = ahead;                            // tile i+1
           ahead = SRC::decode(cb, a.K, stg[(i + 2) % NS], chunk);  // tile i+2
         }
       }
       sync();
 #pragma unroll
-      for (int s = 0; s < KS; s++) frag[f ^ 1][s] = ring[s1][s][lane];
-      const u32x4(&t)[KS] = frag[f];
+      for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int s = 0; s < KS; s++) frag[f ^ 1][p][s] = ring[s1][p][s][lane];
+      const u32x4(&t)[KS] = frag[f][0];
+      const u32x4(&tl)[KS] = frag[f][NP - 1];  // SPLIT: the lo terms
       f32x4 acc[NB][2];
 #pragma unroll
       for (int j = 0; j < NB; j++) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -464,7 +511,13 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
 #pragma unroll
         for (int j = 0; j < NB; j++)
 #pragma unroll
-          for (int h = 0; h < 2; h++) acc[j][h] = mfma16x16x32<DT>(t[s], qf[j][s][h], acc[j][h]);
+          for (int h = 0; h < 2; h++) {
+            if constexpr (SPLIT) {
+              acc[j][h] = mfma16x16x32<DT>(tl[s], qf[j][s][h], acc[j][h]);
+              acc[j][h] = mfma16x16x32<DT>(t[s], qfl[j][s][h], acc[j][h]);
+            }
+            acc[j][h] = mfma16x16x32<DT>(t[s], qf[j][s][h], acc[j][h]);
+          }
       __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int j = 0; j < NB; j++)
@@ -533,28 +586,39 @@ static int batched_ks(const BatchedArgs& a, int64_t grid, size_t lds, hipStream_
   }
   return check_launch("batched_tile_kernel");
 }
+// Query blocks a wave holds in VGPRs: 4 for 16-bit data, 2 for fp32 (their hi and lo
+// terms take twice the registers).
+template <class SRC>
+constexpr int batched_max_blocks() {
+  return SRC::kParts == 2 ? 2 : kMaxBlocksPerWave;
+}
 template <int DT, class SRC>
 static int batched_nb(int nb, const BatchedArgs& a, int64_t grid, size_t lds, hipStream_t st) {
   switch (nb) {
     case 1: return batched_ks<DT, 1, SRC>(a, grid, lds, st);
     case 2: return batched_ks<DT, 2, SRC>(a, grid, lds, st);
-    default: return batched_ks<DT, kMaxBlocksPerWave, SRC>(a, grid, lds, st);
+    default:
+      if constexpr (batched_max_blocks<SRC>() > 2) return batched_ks<DT, kMaxBlocksPerWave, SRC>(a, grid, lds, st);
+      else return fail(TMS_ERR_UNSUPPORTED, "batched MaxSim: %d query blocks per wave", nb);
   }
 }
 template <class SRC>
 static int batched_dt(int dtype, int nb, const BatchedArgs& a, int64_t grid, size_t lds, hipStream_t st) {
-  return dtype == TMS_DTYPE_F16 ? batched_nb<TMS_DTYPE_F16, SRC>(nb, a, grid, lds, st)
-                                : batched_nb<TMS_DTYPE_BF16, SRC>(nb, a, grid, lds, st);
+  if constexpr (SRC::kParts == 2) return batched_nb<TMS_DTYPE_BF16, SRC>(nb, a, grid, lds, st);  // fp32
+  else
+    return dtype == TMS_DTYPE_F16 ? batched_nb<TMS_DTYPE_F16, SRC>(nb, a, grid, lds, st)
+                                  : batched_nb<TMS_DTYPE_BF16, SRC>(nb, a, grid, lds, st);
 }
 
 // Blocks per wave and launches over the query blocks, shared by the entry points below:
-// the smallest of 1, 2, 4 blocks per wave whose launch covers every block in one pass (a
-// wave computes all of its slots, used or not), else 4; a wave holds whole queries.
+// the smallest of 1, 2, 4 (at most max_nb) blocks per wave whose launch covers every block
+// in one pass (a wave computes all of its slots, used or not), else max_nb; a wave holds
+// whole queries.
 template <class LAUNCH>
-static int batched_launches(BatchedArgs& a, int64_t nQ, LAUNCH launch) {
+static int batched_launches(BatchedArgs& a, int64_t nQ, LAUNCH launch, int max_nb = kMaxBlocksPerWave) {
   const int64_t nblocks = nQ * (int64_t)a.nbq;
-  int nb = kMaxBlocksPerWave;
-  for (int c = 1; c < kMaxBlocksPerWave; c *= 2)
+  int nb = max_nb;
+  for (int c = 1; c < max_nb; c *= 2)
     if (c >= a.nbq && nblocks <= (int64_t)TMS_BATCHED_WAVES * ((c / a.nbq) * a.nbq)) {
       nb = c;
       break;
@@ -574,8 +638,9 @@ static int batched_launches(BatchedArgs& a, int64_t nQ, LAUNCH launch) {
 #define TMS_VARLEN_BATCHED_TOKENS 4096  // document tokens one workgroup walks (whole documents, at most 64)
 #endif
 
-// Batched-query entry (tms_dense.hip for variable-length documents, run_stream for fixed
-// ones): d in {32, 64, 96, 128}, 16-byte aligned Q and D, queries of at most 4 blocks.
+// Batched-query entry (tms_dense.hip for variable-length documents and fp32 ones,
+// run_stream for fixed 16-bit ones): d in {32, 64, 96, 128}, 16-byte aligned Q and D,
+// queries of at most 4 blocks (2 for fp32).
 int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t T,
                        const int64_t* offsets, int64_t nd, int64_t B, int64_t pad_len, int dtype, float* out,
                        hipStream_t st) {
@@ -600,6 +665,9 @@ int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const v
   a.docs_per_wg = (int32_t)dpw;
   const int64_t grid = (B + dpw - 1) / dpw;
   if (grid > 0x7fffffff) return fail(TMS_ERR_UNSUPPORTED, "batched MaxSim: too many documents");
+  if (dtype == TMS_DTYPE_F32)
+    return batched_launches(a, nQ, [&](int nb) { return batched_dt<F32Tiles>(dtype, nb, a, grid, 0, st); },
+                            batched_max_blocks<F32Tiles>());
   return batched_launches(a, nQ, [&](int nb) { return batched_dt<DenseTiles>(dtype, nb, a, grid, 0, st); });
 }
 
