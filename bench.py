@@ -58,6 +58,8 @@ def parse():
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--dtype", default="fp16", choices=["fp16", "bf16", "fp32"],
                    help="embedding dtype for --config c1, c2, c2b, c4 and prec")
+    p.add_argument("--qdtype", default=None, choices=["fp32"],
+                   help="--config c2b: fp32 queries against the --dtype documents (split, never rounded)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
@@ -257,9 +259,13 @@ class DenseBatched(Dense):
     MFMA_PEAK_TFLOPS = 2500.0
     MFMA_PEAK_TFLOPS_F32 = 157.3
 
-    def __init__(self, *args, **kw):
+    def __init__(self, *args, qdtype=None, **kw):
         super().__init__(*args, **kw)
         self.kernel = "batched_tile_kernel"  # fixed-length documents at implicit offsets
+        self.qdtype = qdtype
+        if qdtype == "fp32":  # fp32 queries against 16-bit documents: two MFMAs per product
+            gen = self.torch.Generator(device="cuda").manual_seed(99)
+            self.Q = normalized_fp16(self.torch, tuple(self.Q.shape), gen, dtype=self.torch.float32)
 
     def step(self, timer):
         from tilemaxsim_amd import flash_maxsim_batched_queries
@@ -277,6 +283,11 @@ class DenseBatched(Dense):
 
     def extra_roofline(self, launch_ms):
         tf = self.flops_per_launch() / (launch_ms * 1e-3) / 1e12
+        if self.dtype != "fp32" and self.qdtype == "fp32":  # two 16-bit MFMAs per product (q_lo, q_hi)
+            out = gemm_ceiling(self.torch, tf)
+            out.update({"mfma_executed_tflops": round(2 * tf, 1),
+                        "mfma_executed_frac": round(2 * tf / self.MFMA_PEAK_TFLOPS, 4)})
+            return out
         if self.dtype != "fp32":
             return gemm_ceiling(self.torch, tf)
         # fp32: priced against the fp32 dense MFMA peak; the kernel runs each product as
@@ -290,6 +301,10 @@ class DenseBatched(Dense):
         c = super().config()
         c["workload"] += " (batched-query kernel)"
         c["kernel"] = "flash_maxsim_batched_queries (32 query blocks per HBM pass)"
+        if self.qdtype:
+            c["workload"] += f", {self.qdtype} queries"
+            c["query_dtype"] = self.qdtype
+            c["kernel"] = "flash_maxsim_batched_queries (16 split query blocks per HBM pass)"
         return c
 
 
@@ -834,6 +849,9 @@ def main():
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); documents shard across GPUs "
               "with no communication besides a top-k merge, which is not part of this build", file=sys.stderr)
         sys.exit(2)
+    if args.qdtype and args.config != "c2b":
+        print("bench.py: --qdtype applies to --config c2b", file=sys.stderr)
+        sys.exit(2)
     if args.dtype != "fp16" and args.config not in ("c1", "c2", "c2b", "c4", "prec"):
         print(f"bench.py: --dtype applies to --config c1, c2, c2b, c4 and prec (got {args.config})", file=sys.stderr)
         sys.exit(2)
@@ -852,7 +870,7 @@ def main():
         # the reference's precision experiment: 1 query, B = 10K, Nd = 128, d = 128, raw randn
         wl = Dense(torch, 1, 10_000, 128, 128, name="prec", dtype=args.dtype, normalize=False)
     elif args.config == "c2b":
-        wl = DenseBatched(torch, 64, 1_000_000, 180, 128, name="c2b", dtype=args.dtype)
+        wl = DenseBatched(torch, 64, 1_000_000, 180, 128, name="c2b", dtype=args.dtype, qdtype=args.qdtype)
     elif args.config == "c3":
         wl = Varlen(torch, 32, 2_000_000, 32, 300, 128)
     elif args.config == "c3b":
@@ -894,6 +912,8 @@ def main():
     nbytes = wl.bytes_per_launch()
     achieved = nbytes / (k_mean * 1e-3) / 1e9
     tconf = args.config if args.config != "c4" else f"c4_d{args.d}"
+    if args.qdtype:  # another kernel instantiation and pass count: its own traffic file
+        tconf += f"_q{args.qdtype}"
     traffic, traffic_src = _traffic(wl.kernel, tconf if args.dtype == "fp16" else f"{tconf}_{args.dtype}")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -111,6 +111,38 @@ def test_q32_masked_varlen_batched(cuda, ddt, d):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("ddt", ["fp16", "bf16"])
+@pytest.mark.parametrize("nQ,nq,d", [(20, 64, 128), (9, 32, 64), (3, 50, 96)])
+def test_q32_shared_tiles(cuda, ddt, nQ, nq, d):
+    """Several fp32 queries over 16-bit documents share each tile (the shared-tile kernel
+    with split query fragments, up to 16 blocks per pass: 40 blocks here take three
+    passes). Some query tokens are scaled far outside fp16's range or deep into its
+    subnormals, which the per-token power-of-two scale must absorb."""
+    import torch
+    from tilemaxsim_amd import flash_maxsim_batched_queries, flash_maxsim_multi_doc_batched
+    dt = torch.float16 if ddt == "fp16" else torch.bfloat16
+    rng = _rng(nQ * 31 + nq + d)
+    Qs = np.stack([_coherent(rng, (nq, d), ddt) for _ in range(nQ)])
+    Qs[0, 3] *= np.float32(2.0 ** 24)
+    Qs[1, 0] *= np.float32(2.0 ** -40)
+    D, Dt = _docs16(rng, (60, 37, d), dt)
+    got = flash_maxsim_batched_queries(_gpu(Qs), Dt.cuda()).cpu().numpy()
+    assert np.all(np.isfinite(got))
+    for q in range(nQ):
+        _assert_fp32_scores(got[q], orc.maxsim_f64(Qs[q], D), orc.maxsim_f64(np.abs(Qs[q]), np.abs(D)), d,
+                            f"fixed, fp32 Q / {ddt} q={q}")
+    lens = rng.integers(0, 50, 70)
+    lens[[0, 33]] = 0
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    flat, flat_t = _docs16(rng, (int(offsets[-1]), d), dt)
+    got = flash_maxsim_multi_doc_batched(_gpu(Qs), flat_t.cuda(), _gpu(offsets)).cpu().numpy()
+    for q in range(nQ):
+        _assert_fp32_scores(got[q], orc.maxsim_varlen(Qs[q], flat, offsets, f64=True),
+                            orc.maxsim_varlen(np.abs(Qs[q]), np.abs(flat), offsets, f64=True), d,
+                            f"varlen, fp32 Q / {ddt} q={q}")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("scale", [2.0 ** 24, 2.0 ** -40])
 def test_q32_fp16_docs_any_query_magnitude(cuda, scale):
     """fp32 queries far outside fp16's range (2^24 ~ 1.7e7 > 65504) or deep in its

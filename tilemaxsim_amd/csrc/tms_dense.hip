@@ -18,7 +18,7 @@ int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, 
 // Variable-length documents, d in {32, 64, 96, 128}, several query blocks (tms_stream.hip).
 int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t T,
                        const int64_t* offsets, int64_t nd, int64_t B, int64_t pad_len, int dtype, float* out,
-                       hipStream_t st);
+                       hipStream_t st, bool q32);
 // fp32 queries against fp16 / bf16 documents (tms_dense_q32.hip).
 int run_dense_q32(DenseArgs a, int64_t nQ, int dtype, int mode, bool aligned, hipStream_t st);
 
@@ -120,14 +120,18 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
   // fp32 documents, several query blocks: the shared-tile kernel (one pass for up to 16
   // blocks, three bf16 MFMAs per product) instead of one pass per two blocks
-  if (dtype == TMS_DTYPE_F32 && mode != MODE_MASKED && qreg && a.nbq <= 2 && nQ * a.nbq > 2)
+  // fp32 documents or fp32 queries, several query blocks: the shared-tile kernel (one pass
+  // for up to 16 blocks; three or two MFMAs per product) instead of one pass per one or
+  // two blocks
+  if ((dtype == TMS_DTYPE_F32 || q32) && mode != MODE_MASKED && qreg && a.nbq <= 2 && nQ * a.nbq > 2)
     return run_varlen_batched(Q, nQ, nq, d, D, mode == MODE_VARLEN ? total_tokens : B * nd,
-                              mode == MODE_VARLEN ? offsets : nullptr, nd, B, pad_len, dtype, out, st);
+                              mode == MODE_VARLEN ? offsets : nullptr, nd, B, pad_len, dtype, out, st,
+                              dtype != TMS_DTYPE_F32);
   if (dtype == TMS_DTYPE_F32) return run_dense<TMS_DTYPE_F32, TMS_DTYPE_F32>(a, nQ, mode, aligned, st);
   if (q32) return run_dense_q32(a, nQ, dtype, mode, aligned, st);
   if (mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, dtype, out, st);
   if (mode == MODE_VARLEN && qreg && a.nbq <= 4 && nQ * a.nbq >= 4)  // one pass for up to 32 blocks
-    return run_varlen_batched(Q, nQ, nq, d, D, total_tokens, offsets, 0, B, pad_len, dtype, out, st);
+    return run_varlen_batched(Q, nQ, nq, d, D, total_tokens, offsets, 0, B, pad_len, dtype, out, st, false);
   if (dtype == TMS_DTYPE_F16) return run_dense<TMS_DTYPE_F16, TMS_DTYPE_F16>(a, nQ, mode, aligned, st);
   return run_dense<TMS_DTYPE_BF16, TMS_DTYPE_BF16>(a, nQ, mode, aligned, st);
 }

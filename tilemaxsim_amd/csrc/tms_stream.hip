@@ -253,6 +253,7 @@ struct BatchedArgs {
 struct DenseTiles {  // fp16 / bf16 rows, stored to the ring as loaded
   static constexpr bool kDirect = true;
   static constexpr int kParts = 1;
+  static constexpr bool kQ32 = false;  // queries of the rows' type
   typedef u32x4 Raw;
   __device__ static Raw load(const BatchedArgs& a, int64_t row, int c) {
     return *(const u32x4*)(a.D + row * a.d * 2 + 16 * c);
@@ -260,12 +261,20 @@ struct DenseTiles {  // fp16 / bf16 rows, stored to the ring as loaded
   __device__ static u32x4 decode(const u32x4*, int, Raw raw, int) { return raw; }
   __device__ static void parts(const Raw& raw, u32x4 (&out)[1]) { out[0] = raw; }
 };
+// fp16 / bf16 rows scored against fp32 queries: each query element is split into hi + lo
+// terms of the rows' type (fp16 after the token's power-of-two scale, split_f16) and a
+// product takes two MFMAs, d*q_lo + d*q_hi, as in the per-query kernels: the query is
+// never rounded to 16 bits.
+struct DenseTilesQ32 : DenseTiles {
+  static constexpr bool kQ32 = true;
+};
 // fp32 rows (and fp32 queries): every element split into bf16 hi + lo terms as it goes
 // to the ring, a product formed from three bf16 MFMAs (lo*q_hi + hi*q_lo + hi*q_hi, the
 // per-query fp32 kernel's order), as in tms_dense_kernel.h.
 struct F32Tiles {
   static constexpr bool kDirect = true;
   static constexpr int kParts = 2;
+  static constexpr bool kQ32 = true;
   typedef u32x8 Raw;
   __device__ static Raw load(const BatchedArgs& a, int64_t row, int c) {
     const u32x4* p = (const u32x4*)(a.D + row * a.d * 4 + 32 * c);
@@ -280,6 +289,7 @@ template <int DSUB>
 struct PqTiles {
   static constexpr bool kDirect = false;
   static constexpr int kParts = 1;
+  static constexpr bool kQ32 = false;
   typedef uint32_t Raw;
   __device__ static Raw load(const BatchedArgs& a, int64_t row, int c) {
     const uint8_t* p = a.D + row * a.M;
@@ -320,7 +330,9 @@ template <int DT, int KS, int NB, class SRC>
 __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel(BatchedArgs a) {
   constexpr int NS = 4;  // LDS ring slots and load lead, in tiles
   constexpr int NP = SRC::kParts;
-  constexpr bool SPLIT = NP == 2;  // fp32 rows and queries: DT is the MFMA type, bf16
+  constexpr bool SPLIT = NP == 2;        // fp32 rows and queries: DT is the MFMA type, bf16
+  constexpr bool QLO = SRC::kQ32;        // fp32 queries: every query fragment has a lo term
+  constexpr bool QSCALE = QLO && !SPLIT && DT == TMS_DTYPE_F16;  // fp16 terms of a scaled token
   static_assert(!SPLIT || DT == TMS_DTYPE_BF16, "split fp32 terms are bf16");
   __shared__ u32x4 ring[NS][NP][4][64];
   extern __shared__ u32x4 cb[];  // PQ codebook
@@ -342,7 +354,8 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
   int my_nblk = a.blk_end - my_blk0;  // <= 0 for a wave with no query
   if (my_nblk > a.nblk) my_nblk = a.nblk;
   u32x4 qf[NB][KS][2];
-  u32x4 qfl[SPLIT ? NB : 1][SPLIT ? KS : 1][2];  // fp32 queries: the lo terms
+  u32x4 qfl[QLO ? NB : 1][QLO ? KS : 1][2];  // fp32 queries: the lo terms
+  float qinv[QSCALE ? NB : 1][2];           // QSCALE: 1 / the token's scale (a power of two)
   bool qv[NB][2];
 #pragma unroll
   for (int j = 0; j < NB; j++)
@@ -353,16 +366,31 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
       const int tok = (jb - qi * a.nbq) * 32 + 16 * h + r;
       qv[j][h] = j < my_nblk && tok < a.nq;
       const int64_t row = qv[j][h] ? (int64_t)qi * a.nq + tok : 0;
+      if constexpr (QLO) {
+        u32x8 raw[KS];
+        float am = 0.f;
 #pragma unroll
-      for (int s = 0; s < KS; s++) {
-        if constexpr (SPLIT) {
+        for (int s = 0; s < KS; s++) {
           const u32x4* p = (const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 4);
           const u32x4 x0 = p[0], x1 = p[1];
-          u32x4 hi, lo;
-          split_bf16(u32x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]}, hi, lo);
-          qf[j][s][h] = qv[j][h] ? hi : u32x4{0u, 0u, 0u, 0u};
-          qfl[j][s][h] = qv[j][h] ? lo : u32x4{0u, 0u, 0u, 0u};
-        } else {
+          raw[s] = qv[j][h] ? u32x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]}
+                            : u32x8{0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+          if constexpr (QSCALE) am = fmaxf(am, absmax8(raw[s]));
+        }
+        float sc = 1.f;
+        if constexpr (QSCALE) {  // the token's chunks sit in lanes r, r+16, r+32, r+48
+          am = fmaxf(am, __shfl_xor(am, 16));
+          am = fmaxf(am, __shfl_xor(am, 32));
+          sc = pow2_scale(am, qinv[j][h]);
+        }
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+          if constexpr (QSCALE) split_f16(raw[s], sc, qf[j][s][h], qfl[j][s][h]);
+          else split_bf16(raw[s], qf[j][s][h], qfl[j][s][h]);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
           const u32x4 v = *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2);
           qf[j][s][h] = qv[j][h] ? v : u32x4{0u, 0u, 0u, 0u};
         }
@@ -512,10 +540,8 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
         for (int j = 0; j < NB; j++)
 #pragma unroll
           for (int h = 0; h < 2; h++) {
-            if constexpr (SPLIT) {
-              acc[j][h] = mfma16x16x32<DT>(tl[s], qf[j][s][h], acc[j][h]);
-              acc[j][h] = mfma16x16x32<DT>(t[s], qfl[j][s][h], acc[j][h]);
-            }
+            if constexpr (SPLIT) acc[j][h] = mfma16x16x32<DT>(tl[s], qf[j][s][h], acc[j][h]);
+            if constexpr (QLO) acc[j][h] = mfma16x16x32<DT>(t[s], qfl[j][s][h], acc[j][h]);
             acc[j][h] = mfma16x16x32<DT>(t[s], qf[j][s][h], acc[j][h]);
           }
       __builtin_amdgcn_s_setprio(0);
@@ -532,6 +558,7 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel
 #pragma unroll
           for (int h = 0; h < 2; h++) {
             float m = cross_row_max(rmax[j][h]);
+            if constexpr (QSCALE) m *= qinv[j][h];  // exact: a power of two
             if (padded) m = fmaxf(m, 0.f);
             s += qv[j][h] ? m : 0.f;
             rmax[j][h] = NEG_INF;
@@ -586,11 +613,11 @@ static int batched_ks(const BatchedArgs& a, int64_t grid, size_t lds, hipStream_
   }
   return check_launch("batched_tile_kernel");
 }
-// Query blocks a wave holds in VGPRs: 4 for 16-bit data, 2 for fp32 (their hi and lo
-// terms take twice the registers).
+// Query blocks a wave holds in VGPRs: 4 for 16-bit queries, 2 for fp32 ones (their hi
+// and lo terms take twice the registers).
 template <class SRC>
 constexpr int batched_max_blocks() {
-  return SRC::kParts == 2 ? 2 : kMaxBlocksPerWave;
+  return SRC::kQ32 ? 2 : kMaxBlocksPerWave;
 }
 template <int DT, class SRC>
 static int batched_nb(int nb, const BatchedArgs& a, int64_t grid, size_t lds, hipStream_t st) {
@@ -640,10 +667,10 @@ static int batched_launches(BatchedArgs& a, int64_t nQ, LAUNCH launch, int max_n
 
 // Batched-query entry (tms_dense.hip for variable-length documents and fp32 ones,
 // run_stream for fixed 16-bit ones): d in {32, 64, 96, 128}, 16-byte aligned Q and D,
-// queries of at most 4 blocks (2 for fp32).
+// queries of at most 4 blocks (2 for fp32 queries, q32: fp32 queries against 16-bit rows).
 int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t T,
                        const int64_t* offsets, int64_t nd, int64_t B, int64_t pad_len, int dtype, float* out,
-                       hipStream_t st) {
+                       hipStream_t st, bool q32) {
   BatchedArgs a;
   memset(&a, 0, sizeof(a));
   a.Q = (const uint8_t*)Q;
@@ -668,6 +695,9 @@ int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const v
   if (dtype == TMS_DTYPE_F32)
     return batched_launches(a, nQ, [&](int nb) { return batched_dt<F32Tiles>(dtype, nb, a, grid, 0, st); },
                             batched_max_blocks<F32Tiles>());
+  if (q32)
+    return batched_launches(a, nQ, [&](int nb) { return batched_dt<DenseTilesQ32>(dtype, nb, a, grid, 0, st); },
+                            batched_max_blocks<DenseTilesQ32>());
   return batched_launches(a, nQ, [&](int nb) { return batched_dt<DenseTiles>(dtype, nb, a, grid, 0, st); });
 }
 
@@ -720,7 +750,7 @@ int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, 
   a.d = (int32_t)d;
   const int64_t nblocks = nQ * (int64_t)a.nbq;
   if (a.nbq <= kMaxBlocksPerWave && nblocks >= 4)  // batched: documents at implicit offsets b * nd
-    return run_varlen_batched(Q, nQ, nq, d, D, B * nd, nullptr, nd, B, 0, dtype, out, st);
+    return run_varlen_batched(Q, nQ, nq, d, D, B * nd, nullptr, nd, B, 0, dtype, out, st, false);
   int64_t dpw = nd > 0 ? TMS_STREAM_TOKENS_PER_WAVE / nd : 1;
   const int64_t min_waves = (int64_t)256 * 16 * 2;
   if (dpw > 1 && B / dpw < min_waves) dpw = B / min_waves;
