@@ -54,7 +54,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--config", default="c2",
                    choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "prec", "copy",
-                            "readprobe", "ldsprobe"])
+                            "readprobe", "ldsprobe", "mfmaprobe"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--dtype", default="fp16", choices=["fp16", "bf16", "fp32"],
                    help="embedding dtype for --config c1, c2, c2b, c4 and prec")
@@ -777,6 +777,50 @@ class LdsProbe:
         return {"bound": "lds", "peak": None, "frac": None, "unit": "GB/s (LDS reads, all CUs)", "patterns": out}
 
 
+class MfmaProbe:
+    """MFMA probe (tms_mfma_probe): v_mfma_f32_16x16x32_f16 and nothing else, 2 waves per
+    SIMD, on random fp16 operands: the sustained MFMA rate of this part at the clock it
+    holds under that load, the practical ceiling of the shared-tile kernels."""
+    kernel = "mfma_probe_kernel"
+    MFMA_PEAK_TFLOPS = 2500.0
+    launch_desc = "one tms_mfma_probe launch"
+
+    def __init__(self, torch):
+        import ctypes
+        from tilemaxsim_amd import _lib
+        self.torch, self.lib, self.check = torch, _lib.load(), _lib.check
+        gen = torch.Generator(device="cuda").manual_seed(5)
+        self.ops = (torch.rand(512 * 8, device="cuda", generator=gen) * 2 - 1).half()
+        self.sink = torch.empty(_lib.TMS_MFMA_PROBE_SINK_WORDS, dtype=torch.float32, device="cuda")
+        self._flops = ctypes.c_int64(0)
+        self.run()
+
+    def run(self):
+        import ctypes
+        stream = self.torch.cuda.current_stream().cuda_stream
+        self.check(self.lib.tms_mfma_probe(self.ops.data_ptr(), self.sink.data_ptr(), self.sink.numel(),
+                                           ctypes.addressof(self._flops), stream))
+
+    def step(self, timer):
+        timer(self.run)
+
+    def flops_per_launch(self):
+        return self._flops.value
+
+    def bytes_per_launch(self):
+        return 0
+
+    def pairs_per_step(self):
+        return 0
+
+    def config(self):
+        return {"workload": "mfmaprobe: 512 workgroups x 4 waves, 20,000 x 8 v_mfma_f32_16x16x32_f16 per wave on "
+                            "random fp16 operands held in registers"}
+
+    def cpu_baseline(self, seconds):
+        return None
+
+
 def _cpu_model():
     """The host CPU's model name (Linux /proc/cpuinfo), else the architecture."""
     try:
@@ -889,6 +933,8 @@ def main():
         wl = ReadProbe(torch)
     elif args.config == "ldsprobe":
         wl = LdsProbe(torch)
+    elif args.config == "mfmaprobe":
+        wl = MfmaProbe(torch)
     else:
         wl = Copy(torch)
     torch.cuda.synchronize()
@@ -942,8 +988,8 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": getattr(wl, "dtype", "fp16"),
         "data": "synthetic (seeded; no dataset)", "config": wl.config(),
-        "hbm_gbs": round(achieved, 1) if roofline["bound"] != "lds" else None,
-        "hbm_pct_of_peak": round(100 * achieved / HBM_PEAK_GBS, 2) if roofline["bound"] != "lds" else None,
+        "hbm_gbs": round(achieved, 1) if roofline["bound"] == "hbm" else None,
+        "hbm_pct_of_peak": round(100 * achieved / HBM_PEAK_GBS, 2) if roofline["bound"] == "hbm" else None,
         "roofline": roofline, "cpu_baseline": cpu,
     }
     batched = wl.batched_line(torch) if hasattr(wl, "batched_line") else None

@@ -285,6 +285,18 @@ int tms_read_probe(const void* buf, int64_t bytes, uint32_t* sink, int64_t sink_
 int tms_lds_probe(int pattern, int64_t* cycles, int64_t cycle_words, uint32_t* sink, int64_t sink_words,
                   void* stream);
 
+/*
+ * Measurement helper, not part of the scoring path and with no counterpart in the
+ * reference: 512 workgroups of 4 waves (2 waves per SIMD) issue nothing but
+ * v_mfma_f32_16x16x32_f16 on operands read once from `ops` (512 16-byte fp16
+ * fragments), eight accumulators per wave, and write one word per thread to `sink`
+ * (TMS_MFMA_PROBE_SINK_WORDS words). `*flops` receives the launch's MFMA FLOPs.
+ * `bench.py --config mfmaprobe` times it on random operands: the sustained MFMA rate
+ * of this part at the clock it holds under that load.
+ */
+#define TMS_MFMA_PROBE_SINK_WORDS 131072
+int tms_mfma_probe(const void* ops, float* sink, int64_t sink_words, int64_t* flops, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,7 @@ TMS_CODES_I16 = 0x200  # OR-ed into a PQ dtype: int16 codes
 TMS_CODES_I32 = 0x400  # OR-ed into a PQ dtype: int32 codes
 TMS_READ_PROBE_SINK_WORDS = 524288  # words of the sink tms_read_probe writes
 TMS_LDS_PROBE_WAVES = 4096  # waves of one tms_lds_probe launch (one cycle count each)
+TMS_MFMA_PROBE_SINK_WORDS = 131072  # words of the sink tms_mfma_probe writes
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -49,6 +50,7 @@ SIGNATURES = {
     "tms_topk_noalloc": [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p],
     "tms_read_probe": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p],
     "tms_lds_probe": [_int, _c_void_p, _i64, _c_void_p, _i64, _c_void_p],
+    "tms_mfma_probe": [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p],
     "tms_residual_decompress": [_c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _int, _c_void_p,
                                 _c_void_p],
     "tms_maxsim_residual": [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p, _int, _c_void_p, _c_void_p, _i64,

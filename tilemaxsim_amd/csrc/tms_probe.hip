@@ -125,3 +125,42 @@ extern "C" int tms_lds_probe(int pattern, int64_t* cycles, int64_t cycle_words, 
                      (hipStream_t)stream, pattern, cycles, sink);
   return check_launch("lds_probe_kernel");
 }
+
+// ---------------------------------------------------------------------------------
+// MFMA probe: the sustained rate of v_mfma_f32_16x16x32_f16 with operands in registers
+// and nothing else to do, on the operand values the caller passes (random fp16 in
+// `bench.py --config mfmaprobe`: the switching activity of real data sets the clock this
+// part holds). Two 4-wave workgroups per CU (2 waves per SIMD, as the shared-tile
+// kernels run), eight independent accumulators per wave. It is the practical MFMA
+// ceiling the batched kernels are read against. Not part of the scoring path; no
+// reference counterpart.
+namespace tms {
+
+constexpr int kMfmaProbeIters = 20000;
+
+__global__ void __launch_bounds__(256) mfma_probe_kernel(const u32x4* __restrict__ ops, float* __restrict__ sink) {
+  const u32x4 a = ops[threadIdx.x], b = ops[256 + threadIdx.x];
+  f32x4 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < kMfmaProbeIters; it++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = mfma16x16x32<TMS_DTYPE_F16>(a, b, acc[i]);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) s += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
+  sink[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
+}  // namespace tms
+
+extern "C" int tms_mfma_probe(const void* ops, float* sink, int64_t sink_words, int64_t* flops, void* stream) {
+  const char* fn = "tms_mfma_probe";
+  const int grid = 256 * 2;
+  if (!ops || !sink || !flops) return fail(TMS_ERR_INVALID, "%s: NULL pointer", fn);
+  if (sink_words < (int64_t)grid * 256) return fail(TMS_ERR_INVALID, "%s: the sink needs %d words", fn, grid * 256);
+  *flops = (int64_t)grid * 4 * kMfmaProbeIters * 8 * (16 * 16 * 32 * 2);
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const u32x4*)ops, sink);
+  return check_launch("mfma_probe_kernel");
+}
