@@ -49,16 +49,18 @@ def topk(scores: torch.Tensor, k: int):
         lib = _lib.load()
         per_call = min(rows, 65535)  # grid-y limit per call
         ws_bytes = _workspace_bytes(per_call, n, k)
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=s2.device)
+        # rows that fit one chunk need no workspace (the C entry point takes NULL then)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=s2.device) if ws_bytes > 0 else None
+        ws_ptr = ws.data_ptr() if ws is not None else None
         with _lib.on_device(s2.device):
             stream = _lib.stream_of(s2)
             if rows == per_call:
-                _lib.check(lib.tms_topk(s2.data_ptr(), rows, n, k, ws.data_ptr(), ws_bytes, vals.data_ptr(),
+                _lib.check(lib.tms_topk(s2.data_ptr(), rows, n, k, ws_ptr, ws_bytes, vals.data_ptr(),
                                         idx.data_ptr(), stream))
             else:
                 for r0 in range(0, rows, per_call):
                     r1 = min(rows, r0 + per_call)
-                    _lib.check(lib.tms_topk(s2[r0:r1].data_ptr(), r1 - r0, n, k, ws.data_ptr(), ws_bytes,
+                    _lib.check(lib.tms_topk(s2[r0:r1].data_ptr(), r1 - r0, n, k, ws_ptr, ws_bytes,
                                             vals[r0:r1].data_ptr(), idx[r0:r1].data_ptr(), stream))
     if scores.dim() == 1:
         return vals[0], idx[0]
