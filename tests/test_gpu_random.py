@@ -6,7 +6,8 @@ that take the register paths, widths that take the LDS path, and widths that are
 a multiple of 8), the dtype, whether the embeddings are L2-normalised, and the entry
 point. The bar is the one of the other parity tests: 1e-3 relative (+1e-3 absolute)
 for fp16 / bf16 inputs scored against the oracle on the same rounded values, and the
-split-product bound of ``test_gpu_fp32.py`` for fp32 inputs; -inf exactly where the
+split-product bound of ``test_gpu_fp32.py`` for fp32 inputs (and for fp32 queries against
+fp16 / bf16 documents, which are split, not rounded); -inf exactly where the
 oracle has it.
 """
 import numpy as np
@@ -117,6 +118,40 @@ def test_random_case(cuda, seed):
         got = tms.flashmaxsim_score_packed(Q_t.to(dev), Df_t.to(dev), torch.from_numpy(lens).to(dev)).cpu().numpy()
         ref = orc.maxsim_packed_zero_padded(Qh.float().numpy(), Dh.float().numpy()[:T], lens)
         _check(got, ref, None, "fp16", d, what)
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_random_split_query_case(cuda, seed):
+    """fp32 queries against fp16 / bf16 documents (never rounded: split into two terms of
+    the documents' type), one and several queries, fixed-length and variable-length
+    documents; the fp32 bar against the float64 oracle on the unrounded queries."""
+    import torch
+    import tilemaxsim_amd as tms
+    rng = np.random.default_rng(50_000 + seed)
+    nq = int(rng.choice([1, 5, 16, 32, 33, 64, 70]))
+    B, nd = int(rng.integers(1, 200)), int(rng.choice([1, 7, 33, 64, 128]))
+    d = int(rng.choice([32, 64, 96, 128, 40, 136, 256]))
+    ddt = str(rng.choice(["fp16", "bf16"]))
+    nQ = int(rng.integers(1, 7))
+    norm = bool(rng.integers(0, 2))
+    what = f"seed={seed} nq={nq} B={B} nd={nd} d={d} {ddt} nQ={nQ} norm={norm}"
+    print(what, flush=True)
+    dev = torch.device("cuda")
+    Qs = _emb(rng, (nQ, nq, d), norm) * np.float32(rng.choice([1.0, 3e3, 1e-3]))
+    if seed % 2 == 0:
+        D_t, D = _round(_emb(rng, (B, nd, d), norm), ddt)
+        got = tms.flash_maxsim_batched_queries(torch.from_numpy(Qs).to(dev), D_t.to(dev)).cpu().numpy()
+        refs = [(orc.maxsim_f64(Qs[q], D), orc.maxsim_f64(np.abs(Qs[q]), np.abs(D))) for q in range(nQ)]
+    else:
+        lens = rng.integers(0, nd + 1, B)
+        offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        Df_t, Df = _round(_emb(rng, (max(int(offsets[-1]), 1), d), norm), ddt)
+        got = tms.flash_maxsim_multi_doc_batched(torch.from_numpy(Qs).to(dev), Df_t.to(dev),
+                                                 torch.from_numpy(offsets).to(dev)).cpu().numpy()
+        refs = [(orc.maxsim_varlen(Qs[q], Df, offsets, f64=True),
+                 orc.maxsim_varlen(np.abs(Qs[q]), np.abs(Df), offsets, f64=True)) for q in range(nQ)]
+    for q in range(nQ):
+        _check(got[q], refs[q][0], refs[q][1], "fp32", d, f"{what} q={q}")
 
 
 PQ_SHAPES = [  # (M, K, dsub)

@@ -139,3 +139,41 @@ def test_topk_errors(cuda):
         topk(torch.zeros(5000, device="cuda"), 2000)
     v, i = topk(x, 0)
     assert v.shape == (0,)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_topk_random_rows(cuda, seed):
+    """Seeded sweep: row count, row length (around the 4096-key chunk and the 1024-thread
+    block), k (up to the row length and the 1024 maximum), and the value pattern (spread,
+    concentrated, few distinct values, sprinkled NaN / +-inf / signed zeros)."""
+    import torch
+    from tilemaxsim_amd import topk
+    rng = np.random.default_rng(70_000 + seed)
+    rows_n = int(rng.choice([1, 2, 3, 8, 33]))
+    n = int(rng.choice([1, 5, 100, 1023, 1024, 1025, 4095, 4096, 4097, 8192, 12289, 65536, 200_001]))
+    k = int(min(n, rng.choice([1, 2, 31, 64, 100, 256, 257, 1000, 1024])))
+    pattern = seed % 4
+    if pattern == 0:
+        x = rng.standard_normal((rows_n, n))
+    elif pattern == 1:
+        x = 40.0 + 1e-4 * rng.random((rows_n, n))
+    elif pattern == 2:
+        x = rng.integers(-3, 4, (rows_n, n)).astype(np.float64)
+    else:
+        x = rng.standard_normal((rows_n, n))
+        m = rng.random((rows_n, n))
+        x[m < 0.002] = np.nan
+        x[(m >= 0.002) & (m < 0.004)] = np.inf
+        x[(m >= 0.004) & (m < 0.006)] = -np.inf
+        x[(m >= 0.006) & (m < 0.02)] = -0.0
+        x[(m >= 0.02) & (m < 0.03)] = 0.0
+    x = x.astype(np.float32)
+    print(f"seed={seed} rows={rows_n} n={n} k={k} pattern={pattern}", flush=True)
+    v, i = topk(torch.from_numpy(x).cuda(), k)
+    v, i = v.cpu().numpy(), i.cpu().numpy()
+    for r in range(rows_n):
+        ev, ei = orc.topk(x[r], k)
+        assert np.array_equal(i[r], ei), (seed, r)
+        got_nan, exp_nan = np.isnan(v[r]), np.isnan(ev)
+        assert np.array_equal(got_nan, exp_nan), (seed, r)
+        assert np.array_equal(v[r][~got_nan].view(np.uint32), ev[~exp_nan].astype(np.float32).view(np.uint32)), (seed, r)
