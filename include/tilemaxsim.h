@@ -57,6 +57,22 @@ int tms_version(void);
 const char* tms_last_error(void);
 
 /*
+ * Small-batch dispatch limit of the dense entry points (tms_maxsim_dense, _masked,
+ * _varlen, _varlen_padded, and the batched ones with at most three 32-token query
+ * blocks in all): a call whose documents span at most `tiles` 16-token tiles
+ * (B * ceil(mean tokens per document / 16)), with fp16 / bf16 embeddings and d in
+ * {32, 64, 96, 128}, takes the small-batch kernel, which splits each document over up
+ * to four waves so that a few hundred candidates still fill the chip; larger calls
+ * stream whole documents per wave. Default 16384 tiles (measured on MI355X: the
+ * small-batch kernel takes 0.6-0.7x the time up to about 500 documents and about the
+ * same at 1,000-2,000). Sets the limit when tiles >= 0 and returns the previous one
+ * (tiles < 0 only returns it). Process-wide. Both kernels give the same bits. No
+ * reference counterpart (a tuning control, and what tests use to run both kernels on
+ * the same inputs).
+ */
+int64_t tms_set_rerank_limit(int64_t tiles);
+
+/*
  * Dense fixed-length MaxSim, every d (the d <= 128 kernel and the d-tiled kernel).
  * Replaces flash_maxsim_v2_multiquery (src/flash_maxsim_v2.py:227-289) and its two
  * kernels _flash_maxsim_v2_multiquery_kernel (:73-130) and

@@ -16,6 +16,20 @@ RTOL = 1e-3
 ATOL = 1e-3
 
 
+@pytest.fixture(autouse=True, params=["default", "small_batch", "streaming"])
+def dense_path(request):
+    """Every test runs at the default dispatch, with the small-batch kernel taking every
+    call it can (fp16 / bf16, d in {32, 64, 96, 128}, at most three query blocks), and
+    with it off (the streaming kernels)."""
+    from tilemaxsim_amd import _lib
+    limit = {"default": None, "small_batch": 1 << 40, "streaming": 0}[request.param]
+    if limit is None:
+        yield request.param
+        return
+    with _lib.rerank_limit(limit):
+        yield request.param
+
+
 def _rng(seed):
     return np.random.default_rng(seed)
 

@@ -68,8 +68,16 @@ def _emb(rng, shape, norm):
     return x
 
 
+@pytest.mark.parametrize("path", ["small_batch", "streaming"])
 @pytest.mark.parametrize("seed", range(160))
-def test_random_case(cuda, seed):
+def test_random_case(cuda, seed, path):
+    """Each case with the small-batch kernel taking every call it can, and with it off."""
+    from tilemaxsim_amd import _lib
+    with _lib.rerank_limit(1 << 40 if path == "small_batch" else 0):
+        _random_case(seed)
+
+
+def _random_case(seed):
     import torch
     import tilemaxsim_amd as tms
     c, rng = _case(seed)

@@ -31,6 +31,19 @@ def test_library_exports_every_declared_symbol():
     assert lib.tms_version() >= 100
 
 
+def test_rerank_limit_sets_and_restores():
+    from tilemaxsim_amd import _lib
+    lib = _lib.load()
+    default = lib.tms_set_rerank_limit(-1)
+    assert default == 16384
+    with _lib.rerank_limit(0) as prev:
+        assert prev == default and lib.tms_set_rerank_limit(-1) == 0
+        with _lib.rerank_limit(1 << 40):
+            assert lib.tms_set_rerank_limit(-1) == 1 << 40
+        assert lib.tms_set_rerank_limit(-1) == 0
+    assert lib.tms_set_rerank_limit(-1) == default
+
+
 def test_library_is_built_for_gfx950():
     from tilemaxsim_amd import _lib
     blob = open(_lib.LIB_PATH, "rb").read()

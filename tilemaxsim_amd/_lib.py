@@ -5,6 +5,7 @@ PyTorch fallback, so a missing or unloadable library raises immediately.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -35,6 +36,7 @@ _int = ctypes.c_int
 # name -> argtypes (restype is int for every entry point except tms_last_error)
 SIGNATURES = {
     "tms_version": [],
+    "tms_set_rerank_limit": [_i64],
     "tms_maxsim_dense": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _int, _c_void_p, _c_void_p],
     "tms_maxsim_masked": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _i64, _int, _c_void_p, _c_void_p],
     "tms_maxsim_varlen": [_c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p, _i64, _int, _c_void_p, _c_void_p],
@@ -62,7 +64,7 @@ SIGNATURES = {
     "tms_maxsim_residual_batched": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _int, _c_void_p,
                                     _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p, _c_void_p],
 }
-RESTYPES = {"tms_topk_workspace_size": ctypes.c_int64}
+RESTYPES = {"tms_topk_workspace_size": ctypes.c_int64, "tms_set_rerank_limit": ctypes.c_int64}
 
 _lib = None
 _lock = threading.Lock()
@@ -95,6 +97,18 @@ def load() -> ctypes.CDLL:
         lib.tms_last_error.restype = ctypes.c_char_p
         _lib = lib
     return _lib
+
+
+@contextlib.contextmanager
+def rerank_limit(tiles: int):
+    """Within the block, dense calls whose documents span at most ``tiles`` 16-token tiles
+    take the small-batch kernel (0: none do; ``tms_set_rerank_limit``). Process-wide."""
+    lib = load()
+    prev = lib.tms_set_rerank_limit(int(tiles))
+    try:
+        yield prev
+    finally:
+        lib.tms_set_rerank_limit(prev)
 
 
 def check(status: int) -> None:

@@ -19,6 +19,11 @@ int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, 
 int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t T,
                        const int64_t* offsets, int64_t nd, int64_t B, int64_t pad_len, int dtype, float* out,
                        hipStream_t st, bool q32);
+// Small batches (candidate reranking), documents split over several waves (tms_rerank.hip).
+bool rerank_fits(int64_t B, int64_t tokens_per_doc);
+int run_rerank(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int64_t T,
+               const int64_t* offsets, const uint8_t* mask, int64_t pad_len, int mode, int dtype, float* out,
+               hipStream_t st);
 // fp32 queries against fp16 / bf16 documents (tms_dense_q32.hip).
 int run_dense_q32(DenseArgs a, int64_t nQ, int dtype, int mode, bool aligned, hipStream_t st);
 
@@ -129,6 +134,10 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
                               dtype != TMS_DTYPE_F32);
   if (dtype == TMS_DTYPE_F32) return run_dense<TMS_DTYPE_F32, TMS_DTYPE_F32>(a, nQ, mode, aligned, st);
   if (q32) return run_dense_q32(a, nQ, dtype, mode, aligned, st);
+  // a few thousand documents or fewer against one or two query blocks: each document split
+  // over up to four waves, so that small calls still fill the chip
+  if (qreg && nQ * a.nbq <= 3 && rerank_fits(B, hint))
+    return run_rerank(Q, nQ, nq, d, D, B, nd, total_tokens, offsets, mask, pad_len, mode, dtype, out, st);
   if (mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, dtype, out, st);
   if (mode == MODE_VARLEN && qreg && a.nbq <= 4 && nQ * a.nbq >= 4)  // one pass for up to 32 blocks
     return run_varlen_batched(Q, nQ, nq, d, D, total_tokens, offsets, 0, B, pad_len, dtype, out, st, false);

@@ -185,9 +185,10 @@ def maxsim_score(Q: torch.Tensor, D: torch.Tensor, D_mask: torch.Tensor | None =
     _check.same_device(Q=Q, D=D, D_mask=D_mask)
     Q, code = _check.query_for(Q, D.dtype)
     mask = D_mask
-    if mask.dtype != torch.uint8:
-        mask = mask != 0
-        mask = mask.view(torch.uint8) if mask.dtype == torch.bool else mask.to(torch.uint8)
+    if mask.dtype in (torch.bool, torch.int8):  # one byte per token: read as is (non-zero = real)
+        mask = mask.view(torch.uint8)
+    elif mask.dtype != torch.uint8:
+        mask = (mask != 0).view(torch.uint8)
     mask = mask.contiguous()
     scores = torch.empty(B, dtype=torch.float32, device=Q.device)
     if B == 0:
