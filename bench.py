@@ -6,7 +6,8 @@ Gaussian embeddings (~46 GB resident in HBM). One step scores every query agains
 every document with ``flash_maxsim_v2_multiquery`` (one HBM pass over the corpus per
 query, as the reference's V2-MQ kernel) and takes the top-100 per query.
 
-Other workloads (``--config``): c1 (CPU-sized plumbing check), c2b (C2 with all 64
+Other workloads (``--config``): c1 (CPU-sized plumbing check), rerank (the reference's
+end-to-end reranking call: 1 query x 256 candidates x 180 tokens), c2b (C2 with all 64
 queries through the batched-query kernel), c3 (2M variable-length documents), c3b (c3
 through the batched-query kernel), c4
 (d-tiled, ``--d 256|512|768``), c5 (PQ/ADC, 5M documents of uint8 codes), c5b (c5
@@ -16,7 +17,7 @@ corpus as a ColBERTv2 residual-compressed index, fused decode + MaxSim per query
 reference's precision experiment: 1 query x 10K raw-Gaussian documents, Nd = 128,
 d = 128), copy (counter calibration), readprobe (a read-only streaming kernel over a
 C2-sized 46 GB buffer: the read rate any streaming kernel reaches on this part).
-``--dtype fp16|bf16|fp32`` sets the embedding dtype of c1, c2, c4 and prec.
+``--dtype fp16|bf16|fp32`` sets the embedding dtype of c1, rerank, c2, c4 and prec.
 
 Prints ONE JSON line on stdout. ``value`` is (query, document) pairs scored per second
 over the whole step; ``roofline`` is the dominant kernel's algorithmic bandwidth from
@@ -53,11 +54,11 @@ def parse():
     p.add_argument("--steps", type=int, default=5)
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--config", default="c2",
-                   choices=["c1", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "prec", "copy",
+                   choices=["c1", "rerank", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "prec", "copy",
                             "readprobe", "ldsprobe", "mfmaprobe"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--dtype", default="fp16", choices=["fp16", "bf16", "fp32"],
-                   help="embedding dtype for --config c1, c2, c2b, c4 and prec")
+                   help="embedding dtype for --config c1, rerank, c2, c2b, c4 and prec")
     p.add_argument("--qdtype", default=None, choices=["fp32"],
                    help="--config c2b: fp32 queries against the --dtype documents (split, never rounded)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
@@ -119,9 +120,13 @@ class Dense:
         self.torch, self.nQ, self.B, self.Nd, self.d, self.Nq, self.k = torch, n_queries, B, Nd, d, Nq, topk
         self.name, self.dtype, self.normalize = name, dtype, normalize
         tname, self.esize = DTYPES[dtype]
-        # fixed-length fp16 / bf16 documents with d in {32, 64, 96, 128} run the streaming kernel
-        self.kernel = ("stream_maxsim_kernel" if d <= 128 and d % 32 == 0 and dtype != "fp32"
-                       else "dense_maxsim_kernel")
+        # fixed-length fp16 / bf16 documents with d in {32, 64, 96, 128} run the streaming
+        # kernel, or the small-batch kernel when the call spans few tiles
+        self.kernel = "dense_maxsim_kernel"
+        if d <= 128 and d % 32 == 0 and dtype != "fp32":
+            from tilemaxsim_amd import _lib
+            small = B * ((Nd + 15) // 16) <= _lib.load().tms_set_rerank_limit(-1) and (Nq + 31) // 32 <= 3
+            self.kernel = "rerank_maxsim_kernel" if small else "stream_maxsim_kernel"
         gen = torch.Generator(device="cuda").manual_seed(1234)
         log(f"[bench] generating {B} docs x {Nd} x {d} {dtype} ({B * Nd * d * self.esize / 1e9:.2f} GB)")
         tdt = getattr(torch, tname)
@@ -172,11 +177,11 @@ class Dense:
         return line
 
     def graph_line(self, torch, replays=200):
-        """C1 only, after the timed steps: the same step (score, then top-k) captured once
+        """C1 and rerank only, after the timed steps: the same step (score, then top-k) captured once
         in a HIP graph (torch.cuda.CUDAGraph) and replayed, as a serving loop would for
         each new query; HIP events around the replays. The eager step pays the Python
         and launch cost of every call; a replay pays one graph launch."""
-        if self.name != "c1":
+        if self.name not in ("c1", "rerank"):
             return None
         ident = lambda f: f()
         side = torch.cuda.Stream()
@@ -896,8 +901,9 @@ def main():
     if args.qdtype and args.config != "c2b":
         print("bench.py: --qdtype applies to --config c2b", file=sys.stderr)
         sys.exit(2)
-    if args.dtype != "fp16" and args.config not in ("c1", "c2", "c2b", "c4", "prec"):
-        print(f"bench.py: --dtype applies to --config c1, c2, c2b, c4 and prec (got {args.config})", file=sys.stderr)
+    if args.dtype != "fp16" and args.config not in ("c1", "rerank", "c2", "c2b", "c4", "prec"):
+        print(f"bench.py: --dtype applies to --config c1, rerank, c2, c2b, c4 and prec (got {args.config})",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
@@ -908,6 +914,10 @@ def main():
 
     if args.config == "c1":
         wl = Dense(torch, 1, 1000, 128, 128, name="c1", dtype=args.dtype)
+    elif args.config == "rerank":
+        # the reference's end-to-end reranking call: one query against a chunk of 256
+        # candidates zero-padded to 180 tokens (src/e2e_retrieval_quality.py:267-291)
+        wl = Dense(torch, 1, 256, 180, 128, name="rerank", dtype=args.dtype)
     elif args.config == "c2":
         wl = Dense(torch, 64, 1_000_000, 180, 128, name="c2", dtype=args.dtype)
     elif args.config == "prec":
@@ -973,6 +983,11 @@ def main():
                          "frac": round(tf / wl.MFMA_PEAK_TFLOPS, 4), "flops_per_launch": wl.flops_per_launch(),
                          "launch": wl.launch_desc})
 
+    # GPU-side extra lines first: the CPU baseline's threads can keep the host busy for a
+    # while after it returns, which slows a loop of short launches
+    batched = wl.batched_line(torch) if hasattr(wl, "batched_line") else None
+    graph = wl.graph_line(torch) if hasattr(wl, "graph_line") else None
+
     cpu = None
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline on {os.cpu_count()} threads, ~{1.5 * args.cpu_seconds:.0f} s")
@@ -992,11 +1007,9 @@ def main():
         "hbm_pct_of_peak": round(100 * achieved / HBM_PEAK_GBS, 2) if roofline["bound"] == "hbm" else None,
         "roofline": roofline, "cpu_baseline": cpu,
     }
-    batched = wl.batched_line(torch) if hasattr(wl, "batched_line") else None
     if batched:  # c2: the same workload through the batched-query path
         out["batched_queries"] = batched
-    graph = wl.graph_line(torch) if hasattr(wl, "graph_line") else None
-    if graph:  # c1: the same step replayed from a HIP graph
+    if graph:  # c1, rerank: the same step replayed from a HIP graph
         out["graph_replay"] = graph
     print(json.dumps(out), flush=True)
 

@@ -8,7 +8,8 @@
 // and compared as integers (no float NaN semantics involved).
 //
 // Tournament: a workgroup selects the best k of a chunk of kChunk keys and each level
-// shrinks a row by kChunk / k until one chunk holds it; the last level sorts its k keys.
+// shrinks a row by kChunk / k until one chunk holds it; the last level sorts its k keys
+// (a last level of at most kShortRow keys runs a chunk of that size over four waves).
 // Intermediate keys live in a caller-provided workspace. Selection is a radix select on
 // the 64-bit keys held in registers (4 or 16 per thread): one 256-bin LDS histogram per 8-bit
 // digit, from the highest bit at which the chunk's real keys differ, narrowed to the
@@ -35,6 +36,11 @@ constexpr int kChunk = 4096;  // keys sorted per workgroup (32 KiB of LDS)
 constexpr int kLevelThreads = 256;
 constexpr int kLastThreads = 1024;
 constexpr int kMaxK = kChunk / 4;
+// Rows (or last levels) of at most kShortRow keys: one chunk of that size over four
+// waves, one per SIMD, so the serial steps (scans, reductions) are not repeated by four
+// waves on every SIMD.
+constexpr int kShortRow = 1024;
+constexpr int kShortThreads = 256;
 constexpr int kRankSortMaxK = 256;  // the last level orders up to this many keys by rank, more by a bitonic sort
 
 // Order-preserving image of a float's bits. -0.0 is taken as +0.0 (they compare equal,
@@ -104,17 +110,20 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x) {
 
 // The values written by the LAST level are read back from the scores (vals, row stride
 // val_stride) at the selected indices, so they keep the input's bits (-0.0, NaN payloads).
-template <bool FIRST, bool LAST, int NT>
+template <bool FIRST, bool LAST, int NT, int CH = kChunk>
 __global__ void __launch_bounds__(NT) topk_level_kernel(const float* __restrict__ vals, int64_t val_stride,
                                                                   const uint64_t* __restrict__ keys_in, int64_t n_in,
                                                                   int64_t in_stride, uint64_t* __restrict__ keys_out,
                                                                   int64_t out_stride, float* __restrict__ out_vals,
                                                                   int64_t* __restrict__ out_idx, int k) {
-  constexpr int kPerThread = kChunk / NT;
+  constexpr int kPerThread = CH / NT;
   constexpr int kTopkWaves = NT / 64;
   static_assert(NT % 256 == 0 && NT <= kHistCopies * 256, "histogram clearing and the per-wave copies");
-  __shared__ uint32_t hist[kHistCopies][256];
-  __shared__ uint32_t pick[3];  // digit, keys above its bin, keys in its bin
+  static_assert(kTopkWaves <= 64, "one lane per wave in the cross-wave reduction");
+  // Three histogram buffers: pass p counts into buffer p % 3, and buffer (p + 2) % 3 is
+  // cleared after pass p's barrier, when no wave can still be scanning it (its last
+  // scan, in pass p - 1, ended before that barrier) -- one barrier per pass.
+  __shared__ uint32_t hist[3][kHistCopies][256];
   __shared__ uint32_t n_gt, n_eq;
   __shared__ uint64_t sel[LAST ? kMaxK : 1];
   // FIRST && LAST (a row that fits one chunk): the selected scores' own bits, kept from
@@ -122,7 +131,7 @@ __global__ void __launch_bounds__(NT) topk_level_kernel(const float* __restrict_
   __shared__ uint32_t sel_bits[(FIRST && LAST) ? kMaxK : 1];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t row = blockIdx.y;
-  const int64_t c0 = (int64_t)blockIdx.x * kChunk;
+  const int64_t c0 = (int64_t)blockIdx.x * CH;
   // All loads are issued before any key is formed (one memory round trip, not one per
   // element); positions past the row read its last element and become padding.
   uint64_t key[kPerThread];
@@ -152,6 +161,18 @@ __global__ void __launch_bounds__(NT) topk_level_kernel(const float* __restrict_
     }
   }
 
+  // Set-up that the first barrier below orders before its use: the first two histogram
+  // buffers, the slot counters, and (last level) the padding slots of the rank sort.
+  for (int i = tid; i < 2 * kHistCopies * 256; i += NT) (&hist[0][0][0])[i] = 0u;
+  if (tid == 0) {
+    n_gt = 0u;
+    n_eq = 0u;
+  }
+  if constexpr (LAST) {
+    const int k8 = (k + 7) & ~7;
+    if (k <= kRankSortMaxK && tid < k8 - k) sel[k + tid] = 0ull;
+  }
+
   // Where the real keys differ: the radix passes start below the bits that every real
   // key shares (scores in one binade share sign, exponent and the top mantissa bits), so
   // a row of similar scores takes two or three passes instead of up to eight. Padding
@@ -179,15 +200,11 @@ __global__ void __launch_bounds__(NT) topk_level_kernel(const float* __restrict_
   __syncthreads();
   uint64_t prefix = 0;  // the key bits fixed so far: candidates have key >> shift == prefix
   int shift = 64;
-  {
-    uint64_t lo = red_lo[0], hi = red_hi[0];
-    uint32_t nr = red_n[0];
-#pragma unroll
-    for (int w = 1; w < kTopkWaves; w++) {
-      lo = red_lo[w] < lo ? red_lo[w] : lo;
-      hi = red_hi[w] > hi ? red_hi[w] : hi;
-      nr += red_n[w];
-    }
+  {  // lane w brings wave w's partial results; every lane gets the chunk's
+    uint64_t lo = lane < kTopkWaves ? red_lo[lane] : ~0ull;
+    uint64_t hi = lane < kTopkWaves ? red_hi[lane] : 0ull;
+    uint32_t nr = lane < kTopkWaves ? red_n[lane] : 0u;
+    wave_minmax(lo, hi, nr, lane);
     if (nr >= (uint32_t)k) {
       const uint64_t diff = hi ^ lo;
       shift = diff == 0ull ? 0 : 64 - __builtin_clzll(diff);
@@ -199,11 +216,10 @@ __global__ void __launch_bounds__(NT) topk_level_kernel(const float* __restrict_
   // number of keys still to take among the keys that share the prefix.
   uint32_t need = (uint32_t)k;
   bool whole_bin = false;  // the selection is every key >= prefix << shift
-  while (shift > 0) {
+  for (int pass = 0; shift > 0; pass++) {
     const int w = shift < 8 ? shift : 8;
     shift -= w;
-    for (int i = tid; i < kHistCopies * 256; i += NT) (&hist[0][0])[i] = 0u;
-    __syncthreads();
+    uint32_t(&hb)[kHistCopies][256] = hist[pass % 3];
     {
       uint32_t run_bin = 0u, run_n = 0u;  // a run of this thread's keys in one bin
 #pragma unroll
@@ -211,37 +227,37 @@ __global__ void __launch_bounds__(NT) topk_level_kernel(const float* __restrict_
         if (shift + w == 64 || (key[e] >> (shift + w)) == prefix) {
           const uint32_t bin = (uint32_t)(key[e] >> shift) & ((1u << w) - 1u);
           if (run_n != 0u && bin != run_bin) {
-            atomicAdd(&hist[wid % kHistCopies][run_bin], run_n);
+            atomicAdd(&hb[wid % kHistCopies][run_bin], run_n);
             run_n = 0u;
           }
           run_bin = bin;
           run_n++;
         }
       }
-      if (run_n != 0u) atomicAdd(&hist[wid % kHistCopies][run_bin], run_n);
+      if (run_n != 0u) atomicAdd(&hb[wid % kHistCopies][run_bin], run_n);
     }
     __syncthreads();
-    if (wid == 0) {  // lane l scans bins 255 - 4l .. 252 - 4l, high to low
-      uint32_t c[4];
+    for (int i = tid; i < kHistCopies * 256; i += NT) (&hist[(pass + 2) % 3][0][0])[i] = 0u;
+    // Every wave scans the histogram itself (lane l: bins 255 - 4l .. 252 - 4l, high to
+    // low) and finds the bin that holds the need-th key.
+    uint32_t c[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int bin = 255 - 4 * lane - j;
-        c[j] = hist[0][bin] + hist[1][bin] + hist[2][bin] + hist[3][bin];
-      }
-      const uint32_t own = c[0] + c[1] + c[2] + c[3];
-      const uint32_t incl = wave_inclusive_sum(own);
-      const uint32_t excl = incl - own;
-      if (excl < need && need <= incl) {  // exactly one lane: the need-th key is in its bins
-        uint32_t above = excl;
-        int j = 0;
-        while (above + c[j] < need) above += c[j++];
-        pick[0] = (uint32_t)(255 - 4 * lane - j);
-        pick[1] = above;
-        pick[2] = c[j];
-      }
+    for (int j = 0; j < 4; j++) {
+      const int bin = 255 - 4 * lane - j;
+      c[j] = hb[0][bin] + hb[1][bin] + hb[2][bin] + hb[3][bin];
     }
-    __syncthreads();
-    const uint32_t d = pick[0], above = pick[1], cnt = pick[2];
+    const uint32_t own = c[0] + c[1] + c[2] + c[3];
+    const uint32_t incl = wave_inclusive_sum(own);
+    const uint32_t excl = incl - own;
+    const bool mine = excl < need && need <= incl;  // exactly one lane
+    uint32_t above = excl, j = 0;
+    if (mine)
+      while (above + c[j] < need) above += c[j++];
+    const uint32_t cj = c[0] * (j == 0) + c[1] * (j == 1) + c[2] * (j == 2) + c[3] * (j == 3);
+    const int src = (int)__builtin_ctzll(__ballot(mine)) & 63;
+    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)(255 - 4 * lane - j), src);
+    const uint32_t cnt = (uint32_t)__builtin_amdgcn_readlane((int)cj, src);
+    above = (uint32_t)__builtin_amdgcn_readlane((int)above, src);
     need -= above;
     prefix = (prefix << w) | d;
     if (cnt == need && prefix != 0) {  // the whole bin is needed (keys are unique but padding)
@@ -253,11 +269,6 @@ __global__ void __launch_bounds__(NT) topk_level_kernel(const float* __restrict_
   // Each wave reserves its slots with one atomic per 64 keys (ballot and lane count).
   const uint64_t T = whole_bin ? (prefix << shift) - 1 : prefix;
   const uint32_t need_eq = whole_bin ? 0u : need;
-  if (tid == 0) {
-    n_gt = 0u;
-    n_eq = 0u;
-  }
-  __syncthreads();
   auto put = [&](uint32_t pos, uint64_t kv, int e) {
     if constexpr (FIRST && LAST) sel_bits[pos] = __builtin_bit_cast(uint32_t, v[e]);
     if constexpr (LAST) sel[pos] = kv;
@@ -303,24 +314,34 @@ __global__ void __launch_bounds__(NT) topk_level_kernel(const float* __restrict_
   if constexpr (LAST) {
     __syncthreads();
     if (k <= kRankSortMaxK) {  // every selected key is real, so all are distinct: rank = keys above it
-      const int k8 = (k + 7) & ~7;  // k rounded up to a multiple of 8; the slots past k hold 0, below every real key
-      if (tid < k8 - k) sel[k + tid] = 0ull;
-      __syncthreads();
-      // Eight lanes share a key (k <= 128): lane part p counts the keys above it among
-      // slots [p * k8 / 8, (p + 1) * k8 / 8), and three DPP steps add the eight counts.
-      const bool split8 = k * 8 <= NT;
-      const int per = split8 ? k8 / 8 : k8;
-      for (int t = tid; t < (split8 ? 8 * k8 : k); t += NT) {
-        const int i = split8 ? t >> 3 : t;
+      const int k8 = (k + 7) & ~7;  // k rounded up to a multiple of 8; the slots past k hold 0 (set at the
+                                    // start), below every real key
+      // S = 8, 4 or 2 lanes share a key (as many as the threads allow): lane part p
+      // counts the keys above it among slots [p * k8 / S, (p + 1) * k8 / S), and DPP steps
+      // add the S counts.
+      const int lg = k * 8 <= NT ? 3 : (k * 4 <= NT ? 2 : (k * 2 <= NT ? 1 : 0));
+      const int S = 1 << lg;
+      const int per = k8 >> lg;
+      for (int t = tid; t < (S > 1 ? S * k8 : k); t += NT) {
+        const int i = t >> lg;
         const uint64_t me = sel[i];  // slots in [k, k8) are padding zeros: they rank below
-        const int j0 = split8 ? (t & 7) * per : 0;
+        const int j0 = (t & (S - 1)) * per;
         uint32_t rank = 0u;
-        for (int j = j0; j < j0 + per; j++) rank += sel[j] > me ? 1u : 0u;
-        if (split8) {
-          rank += dpp_u32<0xB1>(rank);   // quad_perm [1,0,3,2]
-          rank += dpp_u32<0x4E>(rank);   // quad_perm [2,3,0,1]
-          rank += dpp_u32<0x141>(rank);  // row_half_mirror: the other quad of the eight
-          if ((t & 7) != 0 || i >= k) continue;
+        // eight reads in flight per step (a loop with one read per step waits for each)
+        int j = j0;
+        for (; j + 8 <= j0 + per; j += 8) {
+          uint64_t x[8];
+#pragma unroll
+          for (int q = 0; q < 8; q++) x[q] = sel[j + q];
+#pragma unroll
+          for (int q = 0; q < 8; q++) rank += x[q] > me ? 1u : 0u;
+        }
+        for (; j < j0 + per; j++) rank += sel[j] > me ? 1u : 0u;
+        if (S > 1) {
+          rank += dpp_u32<0xB1>(rank);                 // quad_perm [1,0,3,2]: pairs
+          if (S > 2) rank += dpp_u32<0x4E>(rank);      // quad_perm [2,3,0,1]: quads
+          if (S > 4) rank += dpp_u32<0x141>(rank);     // row_half_mirror: the other quad of the eight
+          if ((t & (S - 1)) != 0 || i >= k) continue;
         }
         const int64_t idx = (int64_t)(0xffffffffu - (uint32_t)me);
         if constexpr (FIRST) out_vals[row * k + rank] = __builtin_bit_cast(float, sel_bits[i]);
@@ -466,8 +487,13 @@ static int topk_run(const float* scores, int64_t nrows, int64_t n, int64_t k, vo
 
   const dim3 last_block(kLastThreads), level_block(kLevelThreads);
   if (lv == 0) {
-    hipLaunchKernelGGL((topk_level_kernel<true, true, kLastThreads>), dim3(1, (unsigned)nrows), last_block, 0, st,
-                       scores, n, nullptr, n, n, nullptr, 0, out_values, out_indices, (int)k);
+    if (n <= kShortRow)
+      hipLaunchKernelGGL((topk_level_kernel<true, true, kShortThreads, kShortRow>), dim3(1, (unsigned)nrows),
+                         dim3(kShortThreads), 0, st, scores, n, nullptr, n, n, nullptr, 0, out_values, out_indices,
+                         (int)k);
+    else
+      hipLaunchKernelGGL((topk_level_kernel<true, true, kLastThreads>), dim3(1, (unsigned)nrows), last_block, 0, st,
+                         scores, n, nullptr, n, n, nullptr, 0, out_values, out_indices, (int)k);
     return check_launch("topk_level_kernel");
   }
   // level 0: scores -> keys
@@ -479,7 +505,11 @@ static int topk_run(const float* scores, int64_t nrows, int64_t n, int64_t k, vo
     const int64_t n_in = sizes[i - 1];
     const uint64_t* in = bufs[(i - 1) % 2];
     const int64_t in_stride = strides[(i - 1) % 2];
-    if (i == lv) {
+    if (i == lv && n_in <= kShortRow) {
+      hipLaunchKernelGGL((topk_level_kernel<false, true, kShortThreads, kShortRow>), dim3(1, (unsigned)nrows),
+                         dim3(kShortThreads), 0, st, scores, n, in, n_in, in_stride, nullptr, 0, out_values,
+                         out_indices, (int)k);
+    } else if (i == lv) {
       hipLaunchKernelGGL((topk_level_kernel<false, true, kLastThreads>), dim3(1, (unsigned)nrows), last_block, 0, st,
                          scores, n, in, n_in, in_stride, nullptr, 0, out_values, out_indices, (int)k);
     } else {
