@@ -65,10 +65,12 @@ const char* tms_last_error(void);
  * to four waves so that a few hundred candidates still fill the chip; larger calls
  * stream whole documents per wave. Default 16384 tiles (measured on MI355X: the
  * small-batch kernel takes 0.6-0.7x the time up to about 500 documents and about the
- * same at 1,000-2,000). Sets the limit when tiles >= 0 and returns the previous one
- * (tiles < 0 only returns it). Process-wide. Both kernels give the same bits. No
- * reference counterpart (a tuning control, and what tests use to run both kernels on
- * the same inputs).
+ * same at 1,000-2,000). The same limit (B * ceil(mean tokens per indexed document /
+ * 16)) lets tms_maxsim_residual split candidate documents over two or four waves while
+ * the call stays within three waves per SIMD (256 candidates: 16 -> 8 us). Sets the
+ * limit when tiles >= 0 and returns the previous one (tiles < 0 only returns it).
+ * Process-wide. Both forms give the same bits. No reference counterpart (a tuning
+ * control, and what tests use to run both forms on the same inputs).
  */
 int64_t tms_set_rerank_limit(int64_t tiles);
 

@@ -18,6 +18,20 @@ RTOL = 1e-3
 ATOL = 1e-3
 
 
+@pytest.fixture(params=["default", "split", "whole"])
+def fused_path(request):
+    """The fused kernel's tests run at the default dispatch, with documents split over
+    waves for every call small enough (tms_set_rerank_limit raised), and with every wave
+    walking whole documents (limit 0)."""
+    from tilemaxsim_amd import _lib
+    limit = {"default": None, "split": 1 << 40, "whole": 0}[request.param]
+    if limit is None:
+        yield request.param
+        return
+    with _lib.rerank_limit(limit):
+        yield request.param
+
+
 def _index(rng, T, d, nbits, ncent):
     """A synthetic index: unit-norm fp16 centroids, random codes and residual buckets,
     bucket weights at the quantiles of a small residual distribution (as the codec fits
@@ -109,7 +123,7 @@ def test_decompress_hand_built_bytes(cuda, nbits):
 @pytest.mark.parametrize("nbits,d,nq", [(2, 128, 32), (1, 128, 32), (4, 128, 32), (2, 64, 20), (2, 32, 1),
                                         (2, 96, 33), (4, 128, 64), (2, 128, 100)])
 @pytest.mark.parametrize("padding", ["zeros", "mask"])
-def test_fused_maxsim_matches_oracle(cuda, nbits, d, nq, padding):
+def test_fused_maxsim_matches_oracle(cuda, fused_path, nbits, d, nq, padding):
     from tilemaxsim_amd import flashmaxsim_score_residual
     rng = np.random.default_rng(nbits * 1000 + d + nq)
     ndocs = 900
@@ -130,7 +144,7 @@ def test_fused_maxsim_matches_oracle(cuda, nbits, d, nq, padding):
 
 
 @pytest.mark.parametrize("nbits,d", [(1, 128), (2, 128), (4, 128), (2, 64), (4, 64), (1, 32), (2, 96)])
-def test_fused_residual_offsets_alignment(cuda, nbits, d):
+def test_fused_residual_offsets_alignment(cuda, fused_path, nbits, d):
     """A residuals view that starts nbits bytes into its buffer is aligned for one chunk
     but not for a lane's whole run of chunks, so the fused kernel reads it chunk by chunk;
     the aligned tensor takes one load per token. Both read the same bytes: bit-identical
@@ -157,7 +171,7 @@ def test_fused_residual_offsets_alignment(cuda, nbits, d):
     _assert_scores(got_a, ro.maxsim_residual(Q, codes, res, C, w, nbits, offsets), f"nbits={nbits} d={d}")
 
 
-def test_fused_candidates_match_packed_scoring(cuda):
+def test_fused_candidates_match_packed_scoring(cuda, fused_path):
     """PLAID's flow: pick candidate pids, decompress their tokens, score them packed.
     The fused kernel must give the same scores without the decompressed copy."""
     import torch
@@ -187,7 +201,7 @@ def test_fused_candidates_match_packed_scoring(cuda):
         assert abs(ref[i] - kth) <= RTOL * abs(kth) + ATOL
 
 
-def test_invalid_documents_and_codes(cuda):
+def test_invalid_documents_and_codes(cuda, fused_path):
     from tilemaxsim_amd import flashmaxsim_score_residual
     rng = np.random.default_rng(5)
     d, nbits = 64, 2
@@ -212,7 +226,49 @@ def test_invalid_documents_and_codes(cuda):
     _assert_scores(got, ro.maxsim_residual(Q, clamped, res, C, w, nbits, offsets), "clamped codes")
 
 
-def test_edge_sizes(cuda):
+@pytest.mark.parametrize("nbits,d,nq", [(2, 128, 32), (1, 64, 20), (4, 96, 70), (2, 32, 1)])
+@pytest.mark.parametrize("B", [1, 3, 37, 700, 2047])
+def test_split_documents_same_bits(cuda, nbits, d, nq, B):
+    """Small candidate lists split each document over 2 or 4 waves (its tiles p, p + wpd,
+    ...), whose maxima meet in LDS. The scores must be the bits of the whole-document walk
+    (the same tile sums, exact maxima, the same summation order) and match the oracle, for
+    both paddings, with duplicate, invalid and empty candidates."""
+    from tilemaxsim_amd import _lib, flashmaxsim_score_residual
+    rng = np.random.default_rng(B * 10 + nbits + d + nq)
+    ndocs = 3000
+    lens = rng.integers(1, 260, ndocs)
+    lens[::29] = 0
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    C, codes, res, w = _index(rng, int(offsets[-1]), d, nbits, 333)
+    Q = rng.standard_normal((nq, d)).astype(np.float32)
+    Q = (Q / np.linalg.norm(Q, axis=1, keepdims=True)).astype(np.float16)
+    pids = rng.integers(0, ndocs, B).astype(np.int64)
+    if B > 3:
+        pids[1] = pids[2]                       # a duplicate candidate
+        pids[3] = int(np.nonzero(lens == 0)[0][0])  # an empty document
+    args = (_gpu(Q), _gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(offsets), _gpu(pids))
+    for padding in ("zeros", "mask"):
+        with _lib.rerank_limit(1 << 40):
+            split = flashmaxsim_score_residual(*args, padding=padding).cpu().numpy()
+        with _lib.rerank_limit(0):
+            whole = flashmaxsim_score_residual(*args, padding=padding).cpu().numpy()
+        assert np.array_equal(split.view(np.uint32), whole.view(np.uint32)), f"B={B} {padding}"
+        pad_len = int(lens[pids].max()) if padding == "zeros" else 0
+        ref = ro.maxsim_residual(Q, codes, res, C, w, nbits, offsets, pids, pad_len)
+        _assert_scores(split, ref, f"B={B} nbits={nbits} d={d} nq={nq} {padding}")
+    if B > 3:  # invalid candidates score NaN on both paths
+        bad = pids.copy()
+        bad[0], bad[-1] = -5, ndocs + 2
+        args = args[:-1] + (_gpu(bad),)
+        with _lib.rerank_limit(1 << 40):
+            split = flashmaxsim_score_residual(*args, padding="mask", validate=False).cpu().numpy()
+        with _lib.rerank_limit(0):
+            whole = flashmaxsim_score_residual(*args, padding="mask", validate=False).cpu().numpy()
+        assert np.isnan(split[0]) and np.isnan(split[-1])
+        assert np.array_equal(split.view(np.uint32), whole.view(np.uint32))
+
+
+def test_edge_sizes(cuda, fused_path):
     import torch
     from tilemaxsim_amd import decompress_residual, flashmaxsim_score_residual
     rng = np.random.default_rng(9)

@@ -52,6 +52,7 @@ struct ResArgs {
   int64_t B, ndocs, T, ncent, pad_len;
   int32_t nq, nbq, blk0, d, rb, docs_per_wave;
   int32_t nblk, blk_end;  // batched kernel: blocks per wave, one past the launch's last block
+  int32_t wpd;            // fused kernel: waves per document (1: each wave walks whole documents)
 };
 
 // Byte -> fp16 weights of its 8 / NBITS dimensions, in dimension order. The table is
@@ -172,13 +173,22 @@ template <int K>
 struct RingSlot {
   static constexpr int value = K;
 };
+bool rerank_fits(int64_t B, int64_t tokens_per_doc);  // tms_rerank.hip
+
+#ifndef TMS_RES_SPLIT_WAVES
+#define TMS_RES_SPLIT_WAVES 3072  // waves a split call may launch: three per SIMD
+#endif
 #ifndef TMS_RES1_RING
 #define TMS_RES1_RING 3  // ring slots of the single-query fused kernel (3..8)
 #endif
 static_assert(TMS_RES1_RING >= 3 && TMS_RES1_RING <= 8, "the fused kernel's step loop is unrolled up to 8 times");
 
 // ---------------------------------------------------------------------------------
-// Fused MaxSim. One wave streams whole documents; a tile is 16 * NSUB tokens x d.
+// Fused MaxSim. One wave streams whole documents; a tile is 16 * NSUB tokens x d. For
+// small calls (a.wpd > 1) the four waves of a workgroup split documents instead: part p
+// of a document scores its tiles p, p + wpd, p + 2 wpd, ..., the parts' per-column
+// maxima meet in LDS and part 0 sums them (in the same order, so the bits are those of
+// the one-wave walk).
 // With a ring of NS tiles, centroid ids are read NS tiles ahead and the centroid chunks
 // and residual bytes NS - 1 tiles ahead of the tile being decoded and scored.
 // QLDS: the query fragments sit in LDS (shared by the workgroup's four waves) instead of
@@ -187,7 +197,7 @@ static_assert(TMS_RES1_RING >= 3 && TMS_RES1_RING <= 8, "the fused kernel's step
 // residual bytes are one contiguous run: with WIDE they arrive in one load per token
 // instead of one per chunk. Each vector-memory instruction costs about as much as a
 // centroid gather, so this is what the gather rate depends on.
-template <int KS, int NBITS, int NSUB, bool QLDS, bool WIDE>
+template <int KS, int NBITS, int NSUB, bool QLDS, bool WIDE, bool SPLIT>
 __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
   constexpr int TT = 16 * NSUB;
   __shared__ __attribute__((aligned(16))) uint8_t lut[4096];
@@ -207,12 +217,19 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
 
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g = lane >> 4;
+  const int wid = threadIdx.x >> 6;
+  const int wpd = SPLIT ? a.wpd : 1;  // 2 or 4 when SPLIT
+  const int part = wid % wpd;  // 0 when each wave walks whole documents
   // wave-uniform, so the document walk below runs on the scalar unit
-  const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  const int64_t b_begin = wave_uniform(wave * a.docs_per_wave);
-  if (b_begin >= a.B) return;
-  const int64_t b_end = (b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B;
+  const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) + wid;
+  const int64_t b_begin =
+      wave_uniform(SPLIT ? (int64_t)blockIdx.x * (kThreads / 64 / wpd) + wid / wpd : wave * a.docs_per_wave);
+  const int64_t b_end =
+      b_begin >= a.B ? b_begin : ((b_begin + a.docs_per_wave < a.B) ? b_begin + a.docs_per_wave : a.B);
   const float NEG_INF = -__builtin_inff();
+  __shared__ float red[SPLIT ? kThreads / 64 : 1][2][16];  // each part's per-column maxima
+  if (SPLIT && g == 0) red[wid][0][r] = red[wid][1][r] = NEG_INF;
+  if (!SPLIT && b_begin >= a.B) return;  // (parts of a split document meet at a barrier)
 
   // query block a.blk0: query tokens 32 * blk0 + 16 h + r
   u32x4 qf[QLDS ? 1 : KS][2];
@@ -290,10 +307,12 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
         c.b = b;
         c.base = base;
         c.len = (int32_t)len;
-        c.t0 = 0;
+        c.t0 = part * TT;
+        if (SPLIT && c.t0 >= c.len) c.b = b_end;  // a part with no tile of the (single) document
         return;
       }
-      if (len < 0) {  // invalid pid or offsets: NaN, written as an integer by every launch
+      if (SPLIT && part != 0) {  // a document part: part 0 writes the score
+      } else if (len < 0) {  // invalid pid or offsets: NaN, written as an integer by every launch
         if (lane == 0) store_nan_score(a.out + b);
       } else {
         write(b, a.pad_len > 0 ? 0.f : NEG_INF);
@@ -303,7 +322,7 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
   };
   auto advance = [&](Cur& c) {
     if (c.b >= b_end) return;
-    c.t0 += TT;
+    c.t0 += TT * wpd;
     if (c.t0 >= c.len) seek(c, c.b + 1);
   };
   auto row_of = [&](const Cur& c, int sub) -> int64_t {
@@ -336,6 +355,17 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
 
   float rmax[2] = {NEG_INF, NEG_INF};
   auto finish = [&](int64_t b, int32_t len) {
+    if constexpr (SPLIT) {  // the part's maxima go to LDS; part 0 combines them after the walk
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        float m = rmax[h];
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        if (g == 0) red[wid][h][r] = m;
+        rmax[h] = NEG_INF;
+      }
+      return;
+    }
     const bool padded = len < a.pad_len;
     float s = 0.f;
 #pragma unroll
@@ -376,7 +406,7 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
         rmax[1] = fmaxf(rmax[1], acc[1][i] * sc);
       }
     }
-    if (c.t0 + TT >= c.len) finish(c.b, c.len);
+    if (c.t0 + TT * wpd >= c.len) finish(c.b, c.len);  // the last tile of this wave's share
   };
 
   // A ring of NS tiles. While tile i is scored, the bodies of tiles i+1 .. i+NS-1 and
@@ -387,6 +417,8 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
   // its positions. The step is unrolled NS times, so every ring slot is a compile-time
   // register.
   constexpr int NS = TMS_RES1_RING;
+  // The walk is a lambda so that its early exits still reach the parts' barrier below.
+  [&]() {
   Body bd[NS];
   int32_t ids[NS][NSUB];
   Cur cr[NS];
@@ -430,6 +462,28 @@ __global__ void __launch_bounds__(256) residual_maxsim_kernel(ResArgs a) {
     }
     if constexpr (NS > 7) {
       if (step(RingSlot<7>{})) return;
+    }
+  }
+  }();
+
+  if constexpr (SPLIT) {  // one document per wave group: part 0 combines the parts and writes
+    __syncthreads();
+    const int32_t len0 = __builtin_amdgcn_readlane(dlen, 0);  // lane 0 holds document b_begin
+    if (part == 0 && b_begin < b_end && len0 > 0) {
+      const bool padded = len0 < a.pad_len;
+      float s = 0.f;
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        float m = red[wid][h][r];
+        for (int p = 1; p < wpd; p++) m = fmaxf(m, red[wid + p][h][r]);
+        if (padded) m = fmaxf(m, 0.f);
+        s += qvalid[h] ? m : 0.f;
+      }
+      s += __shfl_xor(s, 8);
+      s += __shfl_xor(s, 4);
+      s += __shfl_xor(s, 2);
+      s += __shfl_xor(s, 1);
+      write(b_begin, s);
     }
   }
 }
@@ -808,18 +862,25 @@ static int check_format(const char* fn, int64_t d, int nbits, int64_t ncent, con
 #endif
 // One residual load per token when the lane's run of KS*nbits bytes is a power of two and
 // the residuals pointer is aligned to it (rows are 4*KS*nbits bytes, so every run is).
-template <int KS, int NBITS>
-static void launch_fused_nbits(const ResArgs& a, int64_t grid, hipStream_t st) {
+template <int KS, int NBITS, bool SPLIT>
+static void launch_fused_split(const ResArgs& a, int64_t grid, hipStream_t st) {
   constexpr int kNSub = 1;
   constexpr bool kQlds = TMS_RES_QLDS;
   constexpr int TB = NBITS * KS;
   if constexpr (res_run_pow2<NBITS, KS>()) {
     if (((uintptr_t)a.residuals % TB) == 0) {
-      hipLaunchKernelGGL((residual_maxsim_kernel<KS, NBITS, kNSub, kQlds, true>), dim3((unsigned)grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((residual_maxsim_kernel<KS, NBITS, kNSub, kQlds, true, SPLIT>), dim3((unsigned)grid),
+                         dim3(256), 0, st, a);
       return;
     }
   }
-  hipLaunchKernelGGL((residual_maxsim_kernel<KS, NBITS, kNSub, kQlds, false>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((residual_maxsim_kernel<KS, NBITS, kNSub, kQlds, false, SPLIT>), dim3((unsigned)grid), dim3(256),
+                     0, st, a);
+}
+template <int KS, int NBITS>
+static void launch_fused_nbits(const ResArgs& a, int64_t grid, hipStream_t st) {
+  if (a.wpd > 1) launch_fused_split<KS, NBITS, true>(a, grid, st);
+  else launch_fused_split<KS, NBITS, false>(a, grid, st);
 }
 template <int KS>
 static int launch_fused_ks(const ResArgs& a, int nbits, int64_t grid, hipStream_t st) {
@@ -948,7 +1009,16 @@ int tms_maxsim_residual(const void* Q, int64_t nq, int64_t d, const void* centro
   if (dpw < 1) dpw = 1;
   if (dpw > 64) dpw = 64;  // one lane per document holds its bounds
   a.docs_per_wave = (int32_t)dpw;
-  const int64_t grid = ((B + dpw - 1) / dpw + 3) / 4;
+  // Small calls (PLAID's final stage scores about 64 .. 1,024 candidates per query):
+  // documents split over up to four waves while the call still fits the waves the chip
+  // holds at once (three per SIMD at this kernel's registers), at most one wave per
+  // tile of an average document.
+  a.wpd = 1;
+  const int64_t tiles = (hint + 15) / 16;
+  if (rerank_fits(B, hint))  // the dense entry points' small-batch limit (tms_set_rerank_limit)
+    while (a.wpd < 4 && B * a.wpd * 2 <= TMS_RES_SPLIT_WAVES && 2 * a.wpd <= tiles) a.wpd *= 2;
+  if (a.wpd > 1) a.docs_per_wave = 1;
+  const int64_t grid = a.wpd > 1 ? (B * a.wpd + 3) / 4 : ((B + dpw - 1) / dpw + 3) / 4;
   for (int blk = 0; blk < a.nbq; blk++) {
     a.blk0 = blk;
     switch (d / 32) {
