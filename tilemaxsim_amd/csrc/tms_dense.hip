@@ -121,6 +121,7 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   int64_t hint = (mode == MODE_VARLEN) ? (B > 0 ? total_tokens / B : 0) : nd;
   a.docs_per_wave = pick_docs_per_wave(B, hint);
   a.pad_len = pad_len;
+  a.mask4 = (nd % 4 == 0 && ((uintptr_t)mask & 3) == 0) ? 1 : 0;
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
   const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
   // fp32 documents, several query blocks: the shared-tile kernel (one pass for up to 16

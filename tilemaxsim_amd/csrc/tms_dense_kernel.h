@@ -52,6 +52,7 @@ struct DenseArgs {
   int32_t d, nchunk, nstep, nkg;
   int32_t docs_per_wave;
   int64_t pad_len;         // varlen: score as if zero-padded to this many tokens (0 = off)
+  int32_t mask4;           // masked: nd % 4 == 0 and a 4-byte aligned mask (word loads)
 };
 
 // Elements 8c .. 8c+7 of row `row` (16 bytes; 32 for fp32), zero outside [0, d).
@@ -360,11 +361,18 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
       if constexpr (MODE == MODE_MASKED) {
         uint32_t bits = 0;
         if (c.kg == a.nkg - 1) {
+          const int64_t t0 = c.t0 + 16 * sub + 4 * g;
+          if (a.mask4 && c.t0 + 16 * sub + 16 <= c.len) {  // a whole 16-token block: one word per lane
+            const uint32_t w = *(const uint32_t*)(a.mask + c.b * a.nd + t0);
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            int64_t t = c.t0 + 16 * sub + 4 * g + i;
-            if (t > c.len - 1) t = c.len - 1;
-            bits |= (a.mask[c.b * a.nd + t] != 0 ? 1u : 0u) << i;
+            for (int i = 0; i < 4; i++) bits |= (((w >> (8 * i)) & 0xffu) != 0u ? 1u : 0u) << i;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              int64_t t = t0 + i;
+              if (t > c.len - 1) t = c.len - 1;
+              bits |= (a.mask[c.b * a.nd + t] != 0 ? 1u : 0u) << i;
+            }
           }
         }
         buf.m[sub] = bits;
