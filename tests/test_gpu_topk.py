@@ -177,3 +177,22 @@ def test_topk_random_rows(cuda, seed):
         got_nan, exp_nan = np.isnan(v[r]), np.isnan(ev)
         assert np.array_equal(got_nan, exp_nan), (seed, r)
         assert np.array_equal(v[r][~got_nan].view(np.uint32), ev[~exp_nan].astype(np.float32).view(np.uint32)), (seed, r)
+
+
+@pytest.mark.parametrize("n,k", [(n, k) for n in (1, 31, 200, 1000, 1024, 1025, 4096)
+                                 for k in (1, 32, 33, 100, 128, 129, 200, 256, 257, 700, 1024) if k <= n])
+def test_topk_short_rows_every_ordering_form(cuda, n, k):
+    """Rows of at most 1,024 scores (and last levels that small) run one 1,024-key chunk over
+    four waves; longer single-chunk rows run 16 waves. The k selected keys are ordered by
+    rank with 8, 4, 2 or 1 lanes per key (k <= 32, 64, 128, 256 at four waves) or by a
+    bitonic sort (k > 256). Every form against the oracle, bit for bit, on MaxSim-like
+    values with ties, over three rows."""
+    import torch
+    from tilemaxsim_amd import topk
+    rng = np.random.default_rng(n * 7 + k)
+    x = (10.0 + 0.5 * rng.standard_normal((3, n))).astype(np.float32)
+    x[1] = np.round(x[1], 1)  # many ties, resolved by the lower index
+    v, i = topk(torch.from_numpy(x).cuda(), k)
+    v, i = v.cpu().numpy(), i.cpu().numpy()
+    for r in range(3):
+        _check_row(v[r], i[r], x[r], k)
