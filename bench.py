@@ -51,8 +51,9 @@ def log(*a):
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=5)
-    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--steps", type=int, default=None,
+                   help="timed steps (default 5; 200 for the microsecond-scale c1 and rerank)")
+    p.add_argument("--warmup", type=int, default=None, help="untimed steps first (default 1; 20 for c1 and rerank)")
     p.add_argument("--config", default="c2",
                    choices=["c1", "rerank", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "prec", "copy",
                             "readprobe", "ldsprobe", "mfmaprobe"])
@@ -894,6 +895,11 @@ def _traffic(kernel, config):
 
 def main():
     args = parse()
+    tiny = args.config in ("c1", "rerank")  # steps of tens of microseconds: more of them
+    if args.steps is None:
+        args.steps = 200 if tiny else 5
+    if args.warmup is None:
+        args.warmup = 20 if tiny else 1
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); documents shard across GPUs "
               "with no communication besides a top-k merge, which is not part of this build", file=sys.stderr)
