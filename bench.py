@@ -209,6 +209,36 @@ class Dense:
                 "value": round(self.pairs_per_step() / (ms * 1e-3), 1), "unit": "docs/s",
                 "note": "the step captured once in a HIP graph and replayed"}
 
+    def one_launch_line(self, torch, steps=200, warmup=20):
+        """C1 and rerank only, after the timed steps: the same step through maxsim_topk, which
+        scores and ranks in one launch (tms_maxsim_topk) when the call has at most
+        ONE_LAUNCH_MAX_WORKGROUPS workgroups (rerank: 256; C1's 1,000 documents take the two
+        kernels); wall clock around eager steps, as for the timed steps, and a check that
+        the results are those of the timed step."""
+        if self.name not in ("c1", "rerank") or self.nQ != 1 or self.dtype == "fp32":
+            return None
+        from tilemaxsim_amd import maxsim_topk
+        from tilemaxsim_amd.topk import ONE_LAUNCH_MAX_WORKGROUPS, _one_launch_workgroups
+        wg = _one_launch_workgroups(self.B, self.Nd)
+        if wg > ONE_LAUNCH_MAX_WORKGROUPS:
+            return None
+        k = min(self.k, self.B)
+        q = self.Q[0]
+        v, i = maxsim_topk(q, self.D, k)
+        rv, ri = self.step(lambda f: f())
+        same = bool(torch.equal(i, ri[0]) and torch.equal(v.view(torch.int32), rv[0].view(torch.int32)))
+        for _ in range(warmup):
+            maxsim_topk(q, self.D, k)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            maxsim_topk(q, self.D, k)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        return {"ms_per_step": round(ms, 4), "steps": steps, "value": round(self.pairs_per_step() / (ms * 1e-3), 1),
+                "unit": "docs/s", "kernel": "rerank_topk_kernel", "workgroups": wg, "same_results": same,
+                "note": "maxsim_topk: scores and top-k in one launch (eager)"}
+
     def config(self):
         values = "L2-normalised Gaussian" if self.normalize else "unnormalised Gaussian"
         cfg = {"workload": f"{self.name}: {self.nQ} queries x {self.B:,} docs, Nq={self.Nq}, Nd={self.Nd}, d={self.d}, "
@@ -993,6 +1023,7 @@ def main():
     # while after it returns, which slows a loop of short launches
     batched = wl.batched_line(torch) if hasattr(wl, "batched_line") else None
     graph = wl.graph_line(torch) if hasattr(wl, "graph_line") else None
+    one_launch = wl.one_launch_line(torch) if hasattr(wl, "one_launch_line") else None
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -1017,6 +1048,8 @@ def main():
         out["batched_queries"] = batched
     if graph:  # c1, rerank: the same step replayed from a HIP graph
         out["graph_replay"] = graph
+    if one_launch:  # rerank: the same step scored and ranked in one launch
+        out["one_launch"] = one_launch
     print(json.dumps(out), flush=True)
 
 

@@ -62,6 +62,37 @@ def test_graph_dense_score_and_topk(cuda):
     _replay_and_check(graph, out, Q, [_normed(g0, (32, 128)) for _ in range(4)], step)
 
 
+def test_graph_one_launch_score_and_topk(cuda):
+    """tms_maxsim_topk (score + top-k in one launch) captured through the C ABI: the graph
+    holds its own ticket counter, zeroed by a fill kernel at the start of every replay;
+    every replay matches scoring, then ranking, eagerly. (maxsim_topk itself takes the two
+    kernels under capture, where one launch is no faster.)"""
+    import torch
+    from tilemaxsim_amd import _lib, flash_maxsim_v2_multiquery, topk
+    g0 = torch.Generator(device="cuda").manual_seed(5)
+    D = _normed(g0, (256, 180, 128))
+    Q = _normed(g0, (32, 128))
+    lib = _lib.load()
+
+    def step(q):
+        scores = torch.empty(256, device="cuda")
+        vals = torch.empty(100, device="cuda")
+        idx = torch.empty(100, dtype=torch.int64, device="cuda")
+        counter = torch.zeros(1, dtype=torch.int32, device="cuda")
+        rc = lib.tms_maxsim_topk(q.data_ptr(), 32, 128, D.data_ptr(), 256, 180, _lib.TMS_DTYPE_F16, 100,
+                                 scores.data_ptr(), vals.data_ptr(), idx.data_ptr(), counter.data_ptr(),
+                                 _lib.stream_of(D))
+        assert rc == 0, lib.tms_last_error().decode()
+        return scores, vals, idx
+
+    def eager(q):
+        s = flash_maxsim_v2_multiquery(q, D)
+        return (s, *topk(s, 100))
+
+    graph, out = _capture(lambda: step(Q))
+    _replay_and_check(graph, out, Q, [_normed(g0, (32, 128)) for _ in range(4)], eager)
+
+
 def test_graph_varlen_and_batched(cuda):
     import torch
     from tilemaxsim_amd import flash_maxsim_multi_doc, flash_maxsim_multi_doc_batched, topk

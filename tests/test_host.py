@@ -136,6 +136,46 @@ def test_topk_workspace_sizes():
     assert rc == 1 and "workspace" in msg
 
 
+def test_maxsim_topk_c_abi_rejects_bad_arguments():
+    # tms_maxsim_topk(Q, nq, d, D, B, nd, dtype, k, scores, out_values, out_indices, counter, stream)
+    ok = (16, 32, 128, 16, 10, 5, 0, 3, 16, 16, 16, 16, None)
+
+    def call(**kw):
+        names = ["Q", "nq", "d", "D", "B", "nd", "dtype", "k", "scores", "vals", "idx", "counter", "stream"]
+        args = dict(zip(names, ok))
+        args.update(kw)
+        return _c_call("tms_maxsim_topk", *[args[n] for n in names])
+
+    rc, msg = call(nq=-1)
+    assert rc == 1 and "negative" in msg
+    rc, msg = call(k=11)
+    assert rc == 1 and "exceeds" in msg
+    rc, msg = call(dtype=2)  # fp32: score, then tms_topk
+    assert rc == 2 and "fp16 / bf16" in msg and "tms_topk" in msg
+    for bad in (dict(nq=65), dict(d=48), dict(d=160), dict(B=1025, k=3), dict(k=0), dict(B=0, k=0), dict(nq=0)):
+        rc, msg = call(**bad)
+        assert rc == 2 and "tms_topk" in msg, bad
+    rc, msg = call(counter=None)
+    assert rc == 1 and "NULL" in msg
+    rc, msg = call(Q=24)
+    assert rc == 2 and "aligned" in msg
+    rc, msg = call(D=40)
+    assert rc == 2 and "aligned" in msg
+
+
+def test_one_launch_gate_counts_the_kernels_workgroups():
+    """maxsim_topk's gate counts tms_maxsim_topk's workgroups as the launch does: 1, 2 or 4
+    waves per document (while B x waves < 2,048 and at most one wave per 16-token tile),
+    four waves a workgroup."""
+    from tilemaxsim_amd.topk import ONE_LAUNCH_MAX_WORKGROUPS, _one_launch_workgroups
+    assert ONE_LAUNCH_MAX_WORKGROUPS == 256
+    # (B, nd) -> workgroups: 256 x 180 = 12 tiles -> 4 waves each; 1,024 documents stop at
+    # 2 waves (2,048 waves); 16 x 32 = 2 tiles -> 2 waves; 16-token documents -> 1 wave
+    for (B, nd), wg in {(256, 180): 256, (1000, 128): 1000, (64, 100): 64, (1024, 300): 512, (16, 32): 8,
+                        (1, 1): 1, (7, 16): 2, (5, 0): 2, (300, 64): 300, (512, 32): 256}.items():
+        assert _one_launch_workgroups(B, nd) == wg, (B, nd)
+
+
 def test_residual_c_abi_rejects_bad_arguments():
     # tms_residual_decompress(codes, residuals, T, centroids, ncent, d, weights, nbits, out, stream)
     rc, msg = _c_call("tms_residual_decompress", 16, 16, 10, 16, 4, 128, 16, 3, 16, None)

@@ -50,6 +50,8 @@ SIGNATURES = {
     "tms_topk": [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p],
     "tms_topk_workspace_size": [_i64, _i64, _i64],
     "tms_topk_noalloc": [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p],
+    "tms_maxsim_topk": [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _int, _i64, _c_void_p, _c_void_p, _c_void_p,
+                        _c_void_p, _c_void_p],
     "tms_read_probe": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p],
     "tms_lds_probe": [_int, _c_void_p, _i64, _c_void_p, _i64, _c_void_p],
     "tms_mfma_probe": [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p],

@@ -19,7 +19,7 @@
 
 #include <atomic>
 
-#include "tms_common.h"
+#include "tms_topk_kernel.h"
 
 namespace tms {
 
@@ -40,7 +40,7 @@ struct RerankArgs {
 };
 
 template <int DT, int KS, int NB, int MODE>
-__global__ void __launch_bounds__(256) rerank_maxsim_kernel(RerankArgs a) {
+__device__ __forceinline__ void rerank_body(const RerankArgs& a) {
   constexpr int R = 3;  // ring of tiles: two in flight while one is scored
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g = lane >> 4;
@@ -253,6 +253,44 @@ __global__ void __launch_bounds__(256) rerank_maxsim_kernel(RerankArgs a) {
   }
 }
 
+template <int DT, int KS, int NB, int MODE>
+__global__ void __launch_bounds__(256) rerank_maxsim_kernel(RerankArgs a) {
+  rerank_body<DT, KS, NB, MODE>(a);
+}
+
+// Scores plus their top-k in one launch (one query, B <= kShortRow documents): after a
+// workgroup's scores are stored, thread 0 makes them visible device-wide (release fence)
+// and takes a ticket; the workgroup that takes the last one fences (acquire), selects the
+// top k of the B scores with the 1,024-key chunk of the top-k kernel, and resets the
+// counter for the next call. Nothing waits on another workgroup.
+struct TopkTail {
+  uint32_t* counter;  // zero before the launch; zero again after it
+  float* values;      // (k)
+  int64_t* indices;   // (k)
+  int32_t k;
+};
+template <int DT, int KS, int NB>
+__global__ void __launch_bounds__(256) rerank_topk_kernel(RerankArgs a, TopkTail t) {
+  rerank_body<DT, KS, NB, RR_FIXED>(a);
+  __shared__ uint32_t last;
+  // The barrier orders every wave's score stores before thread 0's agent-scope release
+  // (cumulative: on this part it writes the XCD's L2 back, once per workgroup, not per
+  // wave); the ticket is a relaxed RMW in that release sequence; the last workgroup's
+  // thread 0 acquires before the second barrier hands the scores to its other waves.
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const uint32_t prev = __hip_atomic_fetch_add(t.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == gridDim.x - 1 ? 1u : 0u;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+  if (!last) return;
+  topk_chunk<true, true, kShortThreads, kShortRow>(a.out, a.B, nullptr, a.B, a.B, nullptr, 0, t.values, t.indices,
+                                                   t.k, 0, 0);
+  if (threadIdx.x == 0) *t.counter = 0u;
+}
+
 template <int DT, int KS, int NB>
 static int rerank_launch(const RerankArgs& a, int mode, int64_t grid, hipStream_t st) {
   if (mode == RR_VARLEN)
@@ -340,4 +378,61 @@ int run_rerank(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, 
 extern "C" int64_t tms_set_rerank_limit(int64_t tiles) {
   if (tiles < 0) return tms::g_rerank_tiles.load(std::memory_order_relaxed);
   return tms::g_rerank_tiles.exchange(tiles, std::memory_order_relaxed);
+}
+
+extern "C" int tms_maxsim_topk(const void* Q, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype,
+                               int64_t k, float* scores, float* out_values, int64_t* out_indices, uint32_t* counter,
+                               void* stream) {
+  using namespace tms;
+  const char* fn = "tms_maxsim_topk";
+  if (nq < 0 || d < 0 || B < 0 || nd < 0 || k < 0) return fail(TMS_ERR_INVALID, "%s: negative size", fn);
+  if (k > B) return fail(TMS_ERR_INVALID, "%s: k=%lld exceeds the %lld documents", fn, (long long)k, (long long)B);
+  if (dtype != TMS_DTYPE_F16 && dtype != TMS_DTYPE_BF16)
+    return fail(TMS_ERR_UNSUPPORTED, "%s: fp16 / bf16 only (dtype %d); score, then tms_topk", fn, dtype);
+  if (nq < 1 || nq > 64 || d < 32 || d > 128 || d % 32 != 0 || B < 1 || B > kShortRow || k < 1)
+    return fail(TMS_ERR_UNSUPPORTED,
+                "%s: one launch takes 1..64 query tokens, d in {32, 64, 96, 128} and 1..%d documents with k >= 1 "
+                "(nq=%lld d=%lld B=%lld k=%lld); score, then tms_topk",
+                fn, kShortRow, (long long)nq, (long long)d, (long long)B, (long long)k);
+  if (!Q || !scores || !out_values || !out_indices || !counter || (nd > 0 && !D))
+    return fail(TMS_ERR_INVALID, "%s: NULL pointer", fn);
+  if (((uintptr_t)Q & 15) || ((uintptr_t)D & 15))
+    return fail(TMS_ERR_UNSUPPORTED, "%s: Q and D must be 16-byte aligned; score, then tms_topk", fn);
+  RerankArgs a;
+  memset(&a, 0, sizeof(a));
+  a.Q = (const uint8_t*)Q;
+  a.D = (const uint8_t*)D;
+  a.out = scores;
+  a.B = B;
+  a.nd = nd;
+  a.nq = (int32_t)nq;
+  a.nbq = (int32_t)((nq + 31) / 32);
+  a.blk0 = 0;
+  a.nblk = a.nbq;
+  a.d = (int32_t)d;
+  const int64_t tiles = (nd + 15) / 16;
+  a.wpd = 1;
+  while (a.wpd < 4 && B * a.wpd < TMS_RERANK_TARGET_WAVES && 2 * a.wpd <= tiles) a.wpd *= 2;
+  const int64_t grid = (B * a.wpd + 3) / 4;
+  TopkTail t{counter, out_values, out_indices, (int32_t)k};
+  hipStream_t st = (hipStream_t)stream;
+  const bool two = a.nblk == 2;
+  switch (d / 32) {
+#define TMS_RR_TOPK(KS)                                                                                              \
+  case KS:                                                                                                           \
+    if (dtype == TMS_DTYPE_F16) {                                                                                    \
+      if (two) hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_F16, KS, 2>), dim3((unsigned)grid), dim3(256), 0, st, a, t); \
+      else hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_F16, KS, 1>), dim3((unsigned)grid), dim3(256), 0, st, a, t);     \
+    } else {                                                                                                         \
+      if (two) hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_BF16, KS, 2>), dim3((unsigned)grid), dim3(256), 0, st, a, t); \
+      else hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_BF16, KS, 1>), dim3((unsigned)grid), dim3(256), 0, st, a, t);    \
+    }                                                                                                                \
+    break;
+    TMS_RR_TOPK(1)
+    TMS_RR_TOPK(2)
+    TMS_RR_TOPK(3)
+    TMS_RR_TOPK(4)
+#undef TMS_RR_TOPK
+  }
+  return check_launch("rerank_topk_kernel");
 }

@@ -67,12 +67,78 @@ def topk(scores: torch.Tensor, k: int):
     return vals, idx
 
 
+_COUNTERS: dict = {}
+# Workgroups up to which one launch beats scoring, then ranking, for an eager call. Every
+# workgroup of the launch takes one device-scope ticket on a single counter and makes its
+# scores visible device-wide (an L2 write-back of its XCD) before the last one ranks
+# them, so the launch grows slower with its workgroup count. Measured on MI355X (32-token
+# query, d = 128, 16-180-300-token documents): 11.5-15 us against 20 us for the two calls
+# up to 256 workgroups, even at 512, behind from 768. A HIP graph replays two launches
+# without host cost, where one launch never wins by more than noise: captured calls take
+# the two kernels.
+ONE_LAUNCH_MAX_WORKGROUPS = 256
+
+
+def _one_launch_workgroups(B: int, nd: int) -> int:
+    """Workgroups of tms_maxsim_topk's launch: 1, 2 or 4 waves per document (enough for
+    about 2,048 waves, at most one per 16-token tile), four waves a workgroup."""
+    tiles, wpd = (nd + 15) // 16, 1
+    while wpd < 4 and B * wpd < 2048 and 2 * wpd <= tiles:
+        wpd *= 2
+    return (B * wpd + 3) // 4
+
+
+def _counter(dev: torch.device, stream: int) -> torch.Tensor:
+    """The zeroed ticket counter of the one-launch path for this device and stream: each
+    launch leaves it zero, and launches on one stream never overlap."""
+    key = (dev.index, stream)
+    c = _COUNTERS.get(key)
+    if c is None:
+        c = torch.zeros(1, dtype=torch.int32, device=dev)
+        _COUNTERS[key] = c
+    return c
+
+
+def _one_launch(Q: torch.Tensor, D: torch.Tensor, k: int):
+    """``tms_maxsim_topk`` for the eager calls it takes (one query of at most 64 fp16 /
+    bf16 tokens, d in {32, 64, 96, 128}, 1..1,024 contiguous documents, 1 <= k <= B,
+    16-byte aligned, at most ONE_LAUNCH_MAX_WORKGROUPS workgroups); None otherwise (the
+    caller scores, then ranks)."""
+    if not (isinstance(Q, torch.Tensor) and isinstance(D, torch.Tensor) and Q.dim() == 2 and D.dim() == 3):
+        return None
+    B, Nd, d = D.shape
+    Nq = Q.shape[0]
+    if (D.dtype not in (torch.float16, torch.bfloat16) or not D.is_cuda or not D.is_contiguous()
+            or Q.device != D.device or Q.shape[1] != d or d not in (32, 64, 96, 128)
+            or not 1 <= Nq <= 64 or not 1 <= B <= 1024 or not 1 <= k <= B
+            or _one_launch_workgroups(B, Nd) > ONE_LAUNCH_MAX_WORKGROUPS
+            or torch.cuda.is_current_stream_capturing()):
+        return None
+    Q2, code = _check.query_for(Q, D.dtype)
+    if code not in (_lib.TMS_DTYPE_F16, _lib.TMS_DTYPE_BF16) or Q2.data_ptr() % 16 or D.data_ptr() % 16:
+        return None
+    scores = torch.empty(B, dtype=torch.float32, device=D.device)
+    vals = torch.empty(k, dtype=torch.float32, device=D.device)
+    idx = torch.empty(k, dtype=torch.int64, device=D.device)
+    lib = _lib.load()
+    with _lib.on_device(D.device):
+        stream = _lib.stream_of(D)
+        _lib.check(lib.tms_maxsim_topk(Q2.data_ptr(), Nq, d, D.data_ptr(), B, Nd, code, k, scores.data_ptr(),
+                                       vals.data_ptr(), idx.data_ptr(), _counter(D.device, stream).data_ptr(), stream))
+    return vals, idx
+
+
 def maxsim_topk(Q: torch.Tensor, D: torch.Tensor, k: int):
     """Score ``Q`` against ``D`` (B, Nd, d) and return the top-``k`` documents.
 
     ``Q`` (Nq, d) gives ``(values (k,), indices (k,))``; ``Q`` (nQ, Nq, d) scores every
-    query in shared passes over ``D`` and gives (nQ, k) results.
+    query in shared passes over ``D`` and gives (nQ, k) results. An eager reranking call
+    (one query against a few hundred documents) scores and ranks in one launch
+    (``tms_maxsim_topk``), with the same bits as scoring and then ranking.
     """
     if Q.dim() == 3:
         return topk(flash_maxsim_batched_queries(Q, D), k)
+    one = _one_launch(Q, D, int(k))
+    if one is not None:
+        return one
     return topk(flash_maxsim_v2_multiquery(Q, D), k)
