@@ -158,6 +158,85 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
     }
   }
 
+  // The last level's ordering: each of the m distinct keys in sel[0, m) counts the keys
+  // above it among sel[0, m8) (m rounded up to a multiple of 8; slots [m, m8 + kRankPad)
+  // hold 0, below every real key), and a key of rank < k is written at its rank. S = 8, 4 or 2
+  // lanes share a key when the threads allow: lane part p counts among slots
+  // [p * m8 / S, (p + 1) * m8 / S), and DPP steps add the S counts.
+  constexpr int kRankPad = 48;  // zero slots past m8 that the one-lane-per-key loop may read
+  static_assert(kRankSortMaxK + kRankPad <= kMaxK, "the rank step's read ahead stays inside sel");
+  auto rank_out = [&](int m, int m8) {
+    const int lg = m * 8 <= NT ? 3 : (m * 4 <= NT ? 2 : (m * 2 <= NT ? 1 : 0));
+    const int S = 1 << lg;
+    const int per = m8 >> lg;
+    for (int t = tid; t < (S > 1 ? S * m8 : m); t += NT) {
+      const int i = t >> lg;
+      const uint64_t me = sel[i];
+      const int j0 = (t & (S - 1)) * per;
+      uint32_t rank = 0u;
+      int j = j0;
+      const int end = j0 + per;
+      if (S == 1) {
+        // One lane per key, the whole range [0, m8) in steps of 32 with the next 16 keys
+        // read ahead, so the LDS latency hides behind the compares (one wave per SIMD has
+        // nothing else to run meanwhile). No exit between a read and its use, so the
+        // compiler keeps the reads ahead. Reads run up to 40 slots past m8 and counts up
+        // to 24, into slots that hold 0 (set with the keys): a 0 key is above nothing.
+        uint64_t xa[16], xb[16];
+        auto load16 = [&](uint64_t(&x)[16], int at) {
+#pragma unroll
+          for (int q = 0; q < 16; q++) x[q] = sel[at + q];
+        };
+        auto count16 = [&](const uint64_t(&x)[16]) {
+#pragma unroll
+          for (int q = 0; q < 16; q++) rank += x[q] > me ? 1u : 0u;
+        };
+        load16(xa, 0);
+        for (j = 0; j < m8; j += 32) {
+          load16(xb, j + 16);
+          count16(xa);
+          load16(xa, j + 32);
+          count16(xb);
+        }
+        j = end;
+      }
+      for (; j + 8 <= end; j += 8) {  // eight reads in flight per step
+        uint64_t x[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) x[q] = sel[j + q];
+#pragma unroll
+        for (int q = 0; q < 8; q++) rank += x[q] > me ? 1u : 0u;
+      }
+      for (; j < end; j++) rank += sel[j] > me ? 1u : 0u;
+      if (S > 1) {
+        rank += dpp_u32<0xB1>(rank);                 // quad_perm [1,0,3,2]: pairs
+        if (S > 2) rank += dpp_u32<0x4E>(rank);      // quad_perm [2,3,0,1]: quads
+        if (S > 4) rank += dpp_u32<0x141>(rank);     // row_half_mirror: the other quad of the eight
+        if ((t & (S - 1)) != 0) continue;
+      }
+      if (i >= m || rank >= (uint32_t)k) continue;
+      const int64_t idx = (int64_t)(0xffffffffu - (uint32_t)me);
+      if constexpr (FIRST) out_vals[row * k + rank] = __builtin_bit_cast(float, sel_bits[i]);
+      else out_vals[row * k + rank] = vals[row * val_stride + (idx < val_stride ? idx : val_stride - 1)];
+      out_idx[row * k + rank] = idx;
+    }
+  };
+
+  if constexpr (FIRST && LAST) {
+    // A row of at most NT scores holds one key per thread (element tid), all real and
+    // distinct (the index is in the low word): the top k are the keys of rank < k, with
+    // no radix passes. n^2 / S compares per lane; at n = 256 about a quarter of the
+    // passes' time.
+    if (n_in <= NT && n_in <= kRankSortMaxK) {
+      const int m8 = ((int)n_in + 7) & ~7;
+      for (int t = tid; t < kRankSortMaxK + kRankPad; t += NT) sel[t] = t == tid ? key[0] : 0ull;  // 0 past the row
+      if (tid < m8) sel_bits[tid] = __builtin_bit_cast(uint32_t, v[0]);
+      __syncthreads();
+      rank_out((int)n_in, m8);
+      return;
+    }
+  }
+
   // Set-up that the first barrier below orders before its use: the first two histogram
   // buffers, the slot counters, and (last level) the padding slots of the rank sort.
   for (int i = tid; i < 2 * kHistCopies * 256; i += NT) (&hist[0][0][0])[i] = 0u;
@@ -167,7 +246,8 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
   }
   if constexpr (LAST) {
     const int k8 = (k + 7) & ~7;
-    if (k <= kRankSortMaxK && tid < k8 - k) sel[k + tid] = 0ull;
+    if (k <= kRankSortMaxK)
+      for (int t = k + tid; t < k8 + kRankPad; t += NT) sel[t] = 0ull;
   }
 
   // Where the real keys differ: the radix passes start below the bits that every real
@@ -311,40 +391,7 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
   if constexpr (LAST) {
     __syncthreads();
     if (k <= kRankSortMaxK) {  // every selected key is real, so all are distinct: rank = keys above it
-      const int k8 = (k + 7) & ~7;  // k rounded up to a multiple of 8; the slots past k hold 0 (set at the
-                                    // start), below every real key
-      // S = 8, 4 or 2 lanes share a key (as many as the threads allow): lane part p
-      // counts the keys above it among slots [p * k8 / S, (p + 1) * k8 / S), and DPP steps
-      // add the S counts.
-      const int lg = k * 8 <= NT ? 3 : (k * 4 <= NT ? 2 : (k * 2 <= NT ? 1 : 0));
-      const int S = 1 << lg;
-      const int per = k8 >> lg;
-      for (int t = tid; t < (S > 1 ? S * k8 : k); t += NT) {
-        const int i = t >> lg;
-        const uint64_t me = sel[i];  // slots in [k, k8) are padding zeros: they rank below
-        const int j0 = (t & (S - 1)) * per;
-        uint32_t rank = 0u;
-        // eight reads in flight per step (a loop with one read per step waits for each)
-        int j = j0;
-        for (; j + 8 <= j0 + per; j += 8) {
-          uint64_t x[8];
-#pragma unroll
-          for (int q = 0; q < 8; q++) x[q] = sel[j + q];
-#pragma unroll
-          for (int q = 0; q < 8; q++) rank += x[q] > me ? 1u : 0u;
-        }
-        for (; j < j0 + per; j++) rank += sel[j] > me ? 1u : 0u;
-        if (S > 1) {
-          rank += dpp_u32<0xB1>(rank);                 // quad_perm [1,0,3,2]: pairs
-          if (S > 2) rank += dpp_u32<0x4E>(rank);      // quad_perm [2,3,0,1]: quads
-          if (S > 4) rank += dpp_u32<0x141>(rank);     // row_half_mirror: the other quad of the eight
-          if ((t & (S - 1)) != 0 || i >= k) continue;
-        }
-        const int64_t idx = (int64_t)(0xffffffffu - (uint32_t)me);
-        if constexpr (FIRST) out_vals[row * k + rank] = __builtin_bit_cast(float, sel_bits[i]);
-        else out_vals[row * k + rank] = vals[row * val_stride + (idx < val_stride ? idx : val_stride - 1)];
-        out_idx[row * k + rank] = idx;
-      }
+      rank_out(k, (k + 7) & ~7);  // the slots past k hold 0 (set at the start)
       return;
     }
     int P = 1;  // bitonic sort of the k survivors, padded to a power of two

@@ -107,12 +107,13 @@ def _one_launch(Q: torch.Tensor, D: torch.Tensor, k: int):
     if not (isinstance(Q, torch.Tensor) and isinstance(D, torch.Tensor) and Q.dim() == 2 and D.dim() == 3):
         return None
     B, Nd, d = D.shape
+    # the size checks first: a call beyond them costs the two-kernel path nothing more
+    if not 1 <= B <= 1024 or not 1 <= k <= B or _one_launch_workgroups(B, Nd) > ONE_LAUNCH_MAX_WORKGROUPS:
+        return None
     Nq = Q.shape[0]
-    if (D.dtype not in (torch.float16, torch.bfloat16) or not D.is_cuda or not D.is_contiguous()
-            or Q.device != D.device or Q.shape[1] != d or d not in (32, 64, 96, 128)
-            or not 1 <= Nq <= 64 or not 1 <= B <= 1024 or not 1 <= k <= B
-            or _one_launch_workgroups(B, Nd) > ONE_LAUNCH_MAX_WORKGROUPS
-            or torch.cuda.is_current_stream_capturing()):
+    if (d not in (32, 64, 96, 128) or not 1 <= Nq <= 64 or Q.shape[1] != d
+            or D.dtype not in (torch.float16, torch.bfloat16) or not D.is_cuda or not D.is_contiguous()
+            or Q.device != D.device or torch.cuda.is_current_stream_capturing()):
         return None
     Q2, code = _check.query_for(Q, D.dtype)
     if code not in (_lib.TMS_DTYPE_F16, _lib.TMS_DTYPE_BF16) or Q2.data_ptr() % 16 or D.data_ptr() % 16:
