@@ -16,7 +16,8 @@ corpus as a ColBERTv2 residual-compressed index, fused decode + MaxSim per query
 (the same index, all queries through the batched residual kernel), prec (the
 reference's precision experiment: 1 query x 10K raw-Gaussian documents, Nd = 128,
 d = 128), copy (counter calibration), readprobe (a read-only streaming kernel over a
-C2-sized 46 GB buffer: the read rate any streaming kernel reaches on this part).
+C2-sized 46 GB buffer: the read rate any streaming kernel reaches on this part), topk
+(top-100 of each row of C2's (64, 1M) score matrix, plus other row shapes).
 ``--dtype fp16|bf16|fp32`` sets the embedding dtype of c1, rerank, c2, c4 and prec.
 
 Prints ONE JSON line on stdout. ``value`` is (query, document) pairs scored per second
@@ -56,7 +57,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=None, help="untimed steps first (default 1; 20 for c1 and rerank)")
     p.add_argument("--config", default="c2",
                    choices=["c1", "rerank", "c2", "c2b", "c3", "c3b", "c4", "c5", "c5b", "c6", "c6b", "prec", "copy",
-                            "readprobe", "ldsprobe", "mfmaprobe"])
+                            "readprobe", "ldsprobe", "mfmaprobe", "topk"])
     p.add_argument("--d", type=int, default=512, help="embedding width for --config c4")
     p.add_argument("--dtype", default="fp16", choices=["fp16", "bf16", "fp32"],
                    help="embedding dtype for --config c1, rerank, c2, c2b, c4 and prec")
@@ -718,6 +719,66 @@ class Copy:
         return None
 
 
+class TopK:
+    """Top-100 of every row of C2's score matrix (64 queries x 1M documents, MaxSim-like
+    scores 10 + 0.5 N(0, 1), fp32) with tms_topk: the step the reference takes with
+    torch.topk after scoring (src/cycle3_experiments.py:215). HIP events time each whole
+    call (every level of the tournament); the extra rows time other row shapes the same
+    way, each checked against torch.topk on the GPU."""
+    kernel = "topk_level_kernel"
+    dtype = "fp32"
+    SHAPES = [(32, 5_000_000, 100), (1, 1000, 100), (1, 256, 100), (1, 128, 100)]
+
+    def __init__(self, torch, rows=64, n=1_000_000, k=100):
+        self.torch, self.rows, self.n, self.k = torch, rows, n, k
+        self.gen = torch.Generator(device="cuda").manual_seed(7)
+        self.scores = 10 + 0.5 * torch.randn(rows, n, device="cuda", generator=self.gen)
+
+    def step(self, timer):
+        from tilemaxsim_amd import topk
+        return timer(lambda: topk(self.scores, self.k))
+
+    def bytes_per_launch(self):
+        return self.rows * self.n * 4
+
+    def pairs_per_step(self):
+        return self.rows * self.n
+
+    def config(self):
+        return {"workload": f"topk: top-{self.k} of each row of a ({self.rows}, {self.n:,}) fp32 score matrix "
+                            "(C2's scores, MaxSim-like values)", "rows": self.rows, "n": self.n, "k": self.k}
+
+    def cpu_baseline(self, seconds):
+        return None
+
+    def extra_roofline(self, k_mean):
+        from tilemaxsim_amd import topk
+        torch = self.torch
+        v, i = topk(self.scores, self.k)
+        ref = torch.topk(self.scores, self.k)
+        out = {"matches_torch_topk": bool(torch.equal(v, ref.values) and torch.equal(i, ref.indices)), "rows": []}
+        for rows, n, k in self.SHAPES:
+            s = 10 + 0.5 * torch.randn(rows, n, device="cuda", generator=self.gen)
+            reps = 200 if rows * n < 1_000_000 else 10
+            for _ in range(5):
+                v, i = topk(s, k)
+            ev = []
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                v, i = topk(s, k)
+                e1.record()
+                ev.append((e0, e1))
+            torch.cuda.synchronize()
+            ms = sorted(a.elapsed_time(b) for a, b in ev)
+            ref = torch.topk(s, k)
+            out["rows"].append({"rows": rows, "n": n, "k": k, "ms_p50": round(ms[len(ms) // 2], 4),
+                                "gbs": round(rows * n * 4 / (ms[len(ms) // 2] * 1e-3) / 1e9, 1),
+                                "matches_torch_topk": bool(torch.equal(v, ref.values) and torch.equal(i, ref.indices))})
+            del s
+        return out
+
+
 class ReadProbe:
     """A read-only streaming kernel (tms_read_probe: 8 KiB per wave-iteration, persistent
     XCD-grouped grid) over a C2-sized 46.08 GB buffer: the rate at which this part
@@ -977,6 +1038,8 @@ def main():
         wl = ResidualBatched(torch, 32, 2_000_000, 32, 300)
     elif args.config == "readprobe":
         wl = ReadProbe(torch)
+    elif args.config == "topk":
+        wl = TopK(torch)
     elif args.config == "ldsprobe":
         wl = LdsProbe(torch)
     elif args.config == "mfmaprobe":
