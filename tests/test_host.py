@@ -168,7 +168,7 @@ def test_one_launch_gate_counts_the_kernels_workgroups():
     waves per document (while B x waves < 2,048 and at most one wave per 16-token tile),
     four waves a workgroup."""
     from tilemaxsim_amd.topk import ONE_LAUNCH_MAX_WORKGROUPS, _one_launch_workgroups
-    assert ONE_LAUNCH_MAX_WORKGROUPS == 256
+    assert ONE_LAUNCH_MAX_WORKGROUPS == 384
     # (B, nd) -> workgroups: 256 x 180 = 12 tiles -> 4 waves each; 1,024 documents stop at
     # 2 waves (2,048 waves); 16 x 32 = 2 tiles -> 2 waves; 16-token documents -> 1 wave
     for (B, nd), wg in {(256, 180): 256, (1000, 128): 1000, (64, 100): 64, (1024, 300): 512, (16, 32): 8,

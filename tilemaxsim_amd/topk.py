@@ -72,11 +72,11 @@ _COUNTERS: dict = {}
 # workgroup of the launch takes one device-scope ticket on a single counter and makes its
 # scores visible device-wide (an L2 write-back of its XCD) before the last one ranks
 # them, so the launch grows slower with its workgroup count. Measured on MI355X (32-token
-# query, d = 128, 16-180-300-token documents): 11.5-15 us against 20 us for the two calls
-# up to 256 workgroups, even at 512, behind from 768. A HIP graph replays two launches
-# without host cost, where one launch never wins by more than noise: captured calls take
-# the two kernels.
-ONE_LAUNCH_MAX_WORKGROUPS = 256
+# query, d = 128, 32-300-token documents): 11.5-17 us against 20 us for the two calls up
+# to 384 workgroups; even or behind at 512 for long documents. A HIP graph replays two
+# launches without host cost, where one launch never wins by more than noise: captured
+# calls take the two kernels.
+ONE_LAUNCH_MAX_WORKGROUPS = 384
 
 
 def _one_launch_workgroups(B: int, nd: int) -> int:
