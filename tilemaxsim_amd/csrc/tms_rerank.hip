@@ -39,7 +39,8 @@ struct RerankArgs {
   int32_t mask4;           // masked: nd % 4 == 0 and a 4-byte aligned mask (word loads)
 };
 
-template <int DT, int KS, int NB, int MODE>
+// NT threads per workgroup (NT / 64 waves; NT / 64 / wpd documents).
+template <int DT, int KS, int NB, int MODE, int NT = 256>
 __device__ __forceinline__ void rerank_body(const RerankArgs& a) {
   constexpr int R = 3;  // ring of tiles: two in flight while one is scored
   const int lane = threadIdx.x & 63;
@@ -47,12 +48,13 @@ __device__ __forceinline__ void rerank_body(const RerankArgs& a) {
   const int wid = threadIdx.x >> 6;
   const float NEG_INF = -__builtin_inff();
   constexpr int NFRAG = NB * KS * 2 * 64;
-  __shared__ u32x4 qlds[NFRAG];        // query fragments, in the order the waves read them
-  __shared__ float red[4][NB][2][16];  // per-column maxima of each wave
+  constexpr int NW = NT / 64;
+  __shared__ u32x4 qlds[NFRAG];         // query fragments, in the order the waves read them
+  __shared__ float red[NW][NB][2][16];  // per-column maxima of each wave
 
   const int wpd = a.wpd;
   const int part = wid % wpd;
-  const int64_t b = (int64_t)blockIdx.x * (4 / wpd) + wid / wpd;
+  const int64_t b = (int64_t)blockIdx.x * (NW / wpd) + wid / wpd;
   const bool live = b < a.B;
 
   // query fragments: block j, half h, step s -> token 16h + rr of the block, chunk 4s + g
@@ -65,11 +67,11 @@ __device__ __forceinline__ void rerank_body(const RerankArgs& a) {
   };
   // this thread's share of the query fragments (fragment f = ((j KS + s) 2 + h) 64 + lane),
   // loaded now and stored to LDS after the first tiles are in flight
-  constexpr int QPT = (NFRAG + 255) / 256;
+  constexpr int QPT = (NFRAG + NT - 1) / NT;
   u32x4 qtmp[QPT];
 #pragma unroll
   for (int i = 0; i < QPT; i++) {
-    const int f = threadIdx.x + 256 * i;
+    const int f = threadIdx.x + NT * i;
     const int fl = f & 63, h = (f >> 6) & 1, s = (f >> 7) % KS, j = (f >> 7) / KS;
     int64_t row;
     const bool v = f < NFRAG && q_valid(j, h, fl & 15, row);
@@ -134,7 +136,7 @@ __device__ __forceinline__ void rerank_body(const RerankArgs& a) {
 
 #pragma unroll
   for (int i = 0; i < QPT; i++)
-    if (threadIdx.x + 256 * i < NFRAG) qlds[threadIdx.x + 256 * i] = qtmp[i];
+    if (threadIdx.x + NT * i < NFRAG) qlds[threadIdx.x + NT * i] = qtmp[i];
   __syncthreads();
   u32x4 qf[NB][KS][2];
 #pragma unroll
@@ -269,9 +271,14 @@ struct TopkTail {
   int64_t* indices;   // (k)
   int32_t k;
 };
+// Four waves a workgroup, as the small-batch kernel: a 256 x 180-token call then spreads
+// over 256 CUs. 16-wave workgroups take four times fewer tickets and rank with four lanes
+// per key, but leave three quarters of the CUs idle at that size (17.5 against 13.6 us
+// per eager call); they only won for short documents.
+constexpr int kTopkNT = 256;
 template <int DT, int KS, int NB>
-__global__ void __launch_bounds__(256) rerank_topk_kernel(RerankArgs a, TopkTail t) {
-  rerank_body<DT, KS, NB, RR_FIXED>(a);
+__global__ void __launch_bounds__(kTopkNT) rerank_topk_kernel(RerankArgs a, TopkTail t) {
+  rerank_body<DT, KS, NB, RR_FIXED, kTopkNT>(a);
   __shared__ uint32_t last;
   // The barrier orders every wave's score stores before thread 0's agent-scope release
   // (cumulative: on this part it writes the XCD's L2 back, once per workgroup, not per
@@ -286,8 +293,8 @@ __global__ void __launch_bounds__(256) rerank_topk_kernel(RerankArgs a, TopkTail
   }
   __syncthreads();
   if (!last) return;
-  topk_chunk<true, true, kShortThreads, kShortRow>(a.out, a.B, nullptr, a.B, a.B, nullptr, 0, t.values, t.indices,
-                                                   t.k, 0, 0);
+  topk_chunk<true, true, kTopkNT, kShortRow>(a.out, a.B, nullptr, a.B, a.B, nullptr, 0, t.values, t.indices, t.k, 0,
+                                            0);
   if (threadIdx.x == 0) *t.counter = 0u;
 }
 
@@ -413,7 +420,7 @@ extern "C" int tms_maxsim_topk(const void* Q, int64_t nq, int64_t d, const void*
   const int64_t tiles = (nd + 15) / 16;
   a.wpd = 1;
   while (a.wpd < 4 && B * a.wpd < TMS_RERANK_TARGET_WAVES && 2 * a.wpd <= tiles) a.wpd *= 2;
-  const int64_t grid = (B * a.wpd + 3) / 4;
+  const int64_t grid = (B * a.wpd + kTopkNT / 64 - 1) / (kTopkNT / 64);
   TopkTail t{counter, out_values, out_indices, (int32_t)k};
   hipStream_t st = (hipStream_t)stream;
   const bool two = a.nblk == 2;
@@ -421,11 +428,11 @@ extern "C" int tms_maxsim_topk(const void* Q, int64_t nq, int64_t d, const void*
 #define TMS_RR_TOPK(KS)                                                                                              \
   case KS:                                                                                                           \
     if (dtype == TMS_DTYPE_F16) {                                                                                    \
-      if (two) hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_F16, KS, 2>), dim3((unsigned)grid), dim3(256), 0, st, a, t); \
-      else hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_F16, KS, 1>), dim3((unsigned)grid), dim3(256), 0, st, a, t);     \
+      if (two) hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_F16, KS, 2>), dim3((unsigned)grid), dim3(kTopkNT), 0, st, a, t); \
+      else hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_F16, KS, 1>), dim3((unsigned)grid), dim3(kTopkNT), 0, st, a, t);     \
     } else {                                                                                                         \
-      if (two) hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_BF16, KS, 2>), dim3((unsigned)grid), dim3(256), 0, st, a, t); \
-      else hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_BF16, KS, 1>), dim3((unsigned)grid), dim3(256), 0, st, a, t);    \
+      if (two) hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_BF16, KS, 2>), dim3((unsigned)grid), dim3(kTopkNT), 0, st, a, t); \
+      else hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_BF16, KS, 1>), dim3((unsigned)grid), dim3(kTopkNT), 0, st, a, t);    \
     }                                                                                                                \
     break;
     TMS_RR_TOPK(1)
