@@ -179,19 +179,25 @@ def test_topk_random_rows(cuda, seed):
         assert np.array_equal(v[r][~got_nan].view(np.uint32), ev[~exp_nan].astype(np.float32).view(np.uint32)), (seed, r)
 
 
-@pytest.mark.parametrize("n,k", [(n, k) for n in (1, 31, 200, 1000, 1024, 1025, 4096)
+@pytest.mark.parametrize("n,k", [(n, k) for n in (1, 31, 64, 100, 128, 129, 200, 256, 257, 1000, 1024, 1025, 4096)
                                  for k in (1, 32, 33, 100, 128, 129, 200, 256, 257, 700, 1024) if k <= n])
 def test_topk_short_rows_every_ordering_form(cuda, n, k):
-    """Rows of at most 1,024 scores (and last levels that small) run one 1,024-key chunk over
-    four waves; longer single-chunk rows run 16 waves. The k selected keys are ordered by
-    rank with 8, 4, 2 or 1 lanes per key (k <= 32, 64, 128, 256 at four waves) or by a
-    bitonic sort (k > 256). Every form against the oracle, bit for bit, on MaxSim-like
-    values with ties, over three rows."""
+    """Rows of at most 256 scores are ranked directly, all n keys, with 8, 4, 2 or 1 lanes
+    per key (n <= 32, 64, 128, 256); rows of at most 1,024 scores (and last levels that
+    small) run the radix passes over one 1,024-key chunk on four waves; longer
+    single-chunk rows run 16 waves. The k selected keys are ordered by rank with 8, 4, 2
+    or 1 lanes per key (k <= 32, 64, 128, 256 at four waves) or by a bitonic sort
+    (k > 256). Every form against the oracle, bit for bit, on MaxSim-like values, a row
+    with many ties, and a row with NaN (either sign bit), +-inf and +-0.0 sprinkled in."""
     import torch
     from tilemaxsim_amd import topk
     rng = np.random.default_rng(n * 7 + k)
     x = (10.0 + 0.5 * rng.standard_normal((3, n))).astype(np.float32)
     x[1] = np.round(x[1], 1)  # many ties, resolved by the lower index
+    neg_nan = np.array([0xFFC00000], dtype=np.uint32).view(np.float32)[0]
+    specials = np.array([np.nan, neg_nan, np.inf, -np.inf, 0.0, -0.0, -0.0, 0.0], dtype=np.float32)
+    pos = rng.permutation(n)[:min(n, 2 * len(specials))]
+    x[2, pos] = np.resize(specials, len(pos))
     v, i = topk(torch.from_numpy(x).cuda(), k)
     v, i = v.cpu().numpy(), i.cpu().numpy()
     for r in range(3):
