@@ -147,8 +147,8 @@ def test_public_entry_point_repeated_calls(cuda, monkeypatch):
         rv, ri = tms.topk(s, k)
         _same_bits(v, rv, f"B={B} values")
         _same_bits(i, ri, f"B={B} indices")
-    counters = [c for (dev, _), c in topk_mod._COUNTERS.items() if dev == 0]
-    assert counters and all(int(c.item()) == 0 for c in counters)
+    scratch = [c for (dev, _), c in topk_mod._SCRATCH.items() if dev == 0]
+    assert scratch and all(int(c[0].item()) == 0 for c in scratch)  # the ticket counter
 
 
 def test_public_entry_point_falls_back_outside_the_one_launch_shapes(cuda):

@@ -67,7 +67,7 @@ def topk(scores: torch.Tensor, k: int):
     return vals, idx
 
 
-_COUNTERS: dict = {}
+_SCRATCH: dict = {}
 # Workgroups up to which one launch beats scoring, then ranking, for an eager call. Every
 # workgroup of the launch takes one device-scope ticket on a single counter and makes its
 # scores visible device-wide (an L2 write-back of its XCD) before the last one ranks
@@ -88,15 +88,17 @@ def _one_launch_workgroups(B: int, nd: int) -> int:
     return (B * wpd + 3) // 4
 
 
-def _counter(dev: torch.device, stream: int) -> torch.Tensor:
-    """The zeroed ticket counter of the one-launch path for this device and stream: each
-    launch leaves it zero, and launches on one stream never overlap."""
+def _scratch(dev: torch.device, stream: int) -> tuple[int, int]:
+    """Device addresses of the one-launch path's ticket counter and its B <= 1,024 scores,
+    one buffer per device and stream: a launch leaves the counter zero and uses the
+    scores only within itself, and launches on one stream never overlap."""
     key = (dev.index, stream)
-    c = _COUNTERS.get(key)
+    c = _SCRATCH.get(key)
     if c is None:
-        c = torch.zeros(1, dtype=torch.int32, device=dev)
-        _COUNTERS[key] = c
-    return c
+        c = torch.zeros(4 + 1024, dtype=torch.int32, device=dev)  # counter, then scores from byte 16
+        _SCRATCH[key] = c
+    p = c.data_ptr()
+    return p, p + 16
 
 
 def _one_launch(Q: torch.Tensor, D: torch.Tensor, k: int):
@@ -118,14 +120,14 @@ def _one_launch(Q: torch.Tensor, D: torch.Tensor, k: int):
     Q2, code = _check.query_for(Q, D.dtype)
     if code not in (_lib.TMS_DTYPE_F16, _lib.TMS_DTYPE_BF16) or Q2.data_ptr() % 16 or D.data_ptr() % 16:
         return None
-    scores = torch.empty(B, dtype=torch.float32, device=D.device)
     vals = torch.empty(k, dtype=torch.float32, device=D.device)
     idx = torch.empty(k, dtype=torch.int64, device=D.device)
     lib = _lib.load()
     with _lib.on_device(D.device):
         stream = _lib.stream_of(D)
-        _lib.check(lib.tms_maxsim_topk(Q2.data_ptr(), Nq, d, D.data_ptr(), B, Nd, code, k, scores.data_ptr(),
-                                       vals.data_ptr(), idx.data_ptr(), _counter(D.device, stream).data_ptr(), stream))
+        counter, scores = _scratch(D.device, stream)
+        _lib.check(lib.tms_maxsim_topk(Q2.data_ptr(), Nq, d, D.data_ptr(), B, Nd, code, k, scores, vals.data_ptr(),
+                                       idx.data_ptr(), counter, stream))
     return vals, idx
 
 
