@@ -25,6 +25,13 @@ int main(void) {
   if (tms_residual_decompress(NULL, NULL, 1, (const void*)out, 1, 128, (const void*)out, 3, out, NULL) !=
       TMS_ERR_UNSUPPORTED)
     return 8;
+  /* one-launch score + top-k: more than 1,024 documents, and no ticket counter */
+  if (tms_maxsim_topk((const void*)out, 32, 128, (const void*)out, 2000, 8, TMS_DTYPE_F16, 10, out, out, NULL, NULL,
+                      NULL) != TMS_ERR_UNSUPPORTED)
+    return 9;
+  if (tms_maxsim_topk((const void*)out, 32, 128, (const void*)out, 16, 8, TMS_DTYPE_F16, 10, out, out,
+                      (int64_t*)out, NULL, NULL) != TMS_ERR_INVALID)
+    return 10;
   printf("ok %s\n", tms_last_error());
   return 0;
 }
