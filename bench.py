@@ -138,6 +138,9 @@ class Dense:
 
     def step(self, timer):
         from tilemaxsim_amd import flash_maxsim_v2_multiquery
+        if self.nQ == 1:  # one query (c1, rerank, prec): rank its scores where they are
+            s = timer(lambda: flash_maxsim_v2_multiquery(self.Q[0], self.D))
+            return topk_rows(s.unsqueeze(0), min(self.k, self.B))
         for i in range(self.nQ):
             s = timer(lambda: flash_maxsim_v2_multiquery(self.Q[i], self.D))
             self.scores[i].copy_(s)
