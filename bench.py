@@ -91,18 +91,28 @@ def topk_rows(scores, k):
 
 
 class KernelTimer:
-    """HIP events around each launch of the dominant kernel, on the stream it runs on."""
+    """HIP events around each launch of the dominant kernel, on the stream it runs on. The
+    event pairs are created before the timed steps (``prepare``), so a step pays only for
+    recording them."""
 
     def __init__(self, torch):
         self.torch = torch
         self.pairs = []
+        self.pool = []
         self.enabled = False
+
+    def prepare(self, n):
+        ev = lambda: self.torch.cuda.Event(enable_timing=True)
+        self.pool = [(ev(), ev()) for _ in range(n)]
+        self.pool.reverse()
 
     def __call__(self, fn):
         if not self.enabled:
             return fn()
-        s = self.torch.cuda.Event(enable_timing=True)
-        e = self.torch.cuda.Event(enable_timing=True)
+        if self.pool:
+            s, e = self.pool.pop()
+        else:
+            s, e = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
         s.record()
         r = fn()
         e.record()
@@ -1056,6 +1066,7 @@ def main():
     for _ in range(args.warmup):
         wl.step(timer)
     torch.cuda.synchronize()
+    timer.prepare(args.steps * getattr(wl, "nQ", 1))
     timer.enabled = True
     log(f"[bench] timing {args.steps} step(s)")
     t0 = time.perf_counter()
