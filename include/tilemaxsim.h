@@ -231,12 +231,15 @@ int tms_topk_noalloc(const float* scores, int64_t nrows, int64_t n, int64_t k, f
  * finishes last selects the top k of them (values descending, ties to the lower index,
  * the same bits as tms_maxsim_dense followed by tms_topk). fp16 / bf16, 1..64 query
  * tokens, d in {32, 64, 96, 128}, 16-byte aligned Q and D, 1 <= k <= B; other shapes
- * return TMS_ERR_UNSUPPORTED (score, then tms_topk). `counter` is one device word that
- * must hold 0 before the first call; each call leaves it 0 again. Calls that share a
- * counter must not overlap (calls on one stream never do). Replaces the reference's
+ * return TMS_ERR_UNSUPPORTED (score, then tms_topk). `counter` is a device block of
+ * TMS_MAXSIM_TOPK_COUNTER_WORDS 32-bit words (the workgroups' tickets, taken in two levels
+ * on large grids, each counter on its own 64-byte line) that must hold 0 before the first
+ * call; each call leaves it 0 again. Calls that share a counter must not overlap (calls on
+ * one stream never do). Replaces the reference's
  * scoring call followed by torch.topk (src/cycle3_experiments.py:215) for the serving
  * shapes of the reference's reranking flow (src/e2e_retrieval_quality.py:267-291).
  */
+#define TMS_MAXSIM_TOPK_COUNTER_WORDS 144
 int tms_maxsim_topk(const void* Q, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype, int64_t k,
                     float* scores, float* out_values, int64_t* out_indices, uint32_t* counter, void* stream);
 

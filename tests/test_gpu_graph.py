@@ -78,7 +78,7 @@ def test_graph_one_launch_score_and_topk(cuda):
         scores = torch.empty(256, device="cuda")
         vals = torch.empty(100, device="cuda")
         idx = torch.empty(100, dtype=torch.int64, device="cuda")
-        counter = torch.zeros(1, dtype=torch.int32, device="cuda")
+        counter = torch.zeros(_lib.TMS_MAXSIM_TOPK_COUNTER_WORDS, dtype=torch.int32, device="cuda")
         rc = lib.tms_maxsim_topk(q.data_ptr(), 32, 128, D.data_ptr(), 256, 180, _lib.TMS_DTYPE_F16, 100,
                                  scores.data_ptr(), vals.data_ptr(), idx.data_ptr(), counter.data_ptr(),
                                  _lib.stream_of(D))

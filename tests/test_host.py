@@ -163,6 +163,18 @@ def test_maxsim_topk_c_abi_rejects_bad_arguments():
     assert rc == 2 and "aligned" in msg
 
 
+def test_header_constants_match_the_python_mirror():
+    """Every #define of include/tilemaxsim.h that _lib.py mirrors has the same value."""
+    import re
+    from tilemaxsim_amd import _lib
+    text = open(os.path.join(REPO, "include", "tilemaxsim.h")).read()
+    defines = dict(re.findall(r"^#define (TMS_\w+) (\S+)", text, re.M))
+    mirrored = [n for n in defines if hasattr(_lib, n)]
+    assert "TMS_MAXSIM_TOPK_COUNTER_WORDS" in mirrored and len(mirrored) >= 3
+    for n in mirrored:
+        assert int(eval(defines[n].replace("LL", ""))) == getattr(_lib, n), n
+
+
 def test_one_launch_gate_counts_the_kernels_workgroups():
     """maxsim_topk's gate counts tms_maxsim_topk's workgroups as the launch does: 1, 2 or 4
     waves per document (while B x waves < 2,048 and at most one wave per 16-token tile),

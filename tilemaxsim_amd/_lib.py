@@ -27,6 +27,7 @@ TMS_CODES_I16 = 0x200  # OR-ed into a PQ dtype: int16 codes
 TMS_CODES_I32 = 0x400  # OR-ed into a PQ dtype: int32 codes
 TMS_READ_PROBE_SINK_WORDS = 524288  # words of the sink tms_read_probe writes
 TMS_LDS_PROBE_WAVES = 4096  # waves of one tms_lds_probe launch (one cycle count each)
+TMS_MAXSIM_TOPK_COUNTER_WORDS = 144  # 32-bit words of tms_maxsim_topk's zeroed ticket block
 TMS_MFMA_PROBE_SINK_WORDS = 131072  # words of the sink tms_mfma_probe writes
 
 _c_void_p = ctypes.c_void_p

@@ -265,12 +265,20 @@ __global__ void __launch_bounds__(256) rerank_maxsim_kernel(RerankArgs a) {
 // and takes a ticket; the workgroup that takes the last one fences (acquire), selects the
 // top k of the B scores with the 1,024-key chunk of the top-k kernel, and resets the
 // counter for the next call. Nothing waits on another workgroup.
+//
+// Tickets on one address serialise, so a grid of kTicketTwoLevel workgroups or more takes
+// them in two levels: workgroup g on group counter g % kTicketGroups, the last of each
+// group (after an acquire + release, which passes its group's scores on) on the top
+// counter. Each counter has its own 64-byte line (TMS_MAXSIM_TOPK_COUNTER_WORDS words in
+// all). Every counter the launch used is zero again when it ends.
 struct TopkTail {
-  uint32_t* counter;  // zero before the launch; zero again after it
+  uint32_t* counter;  // TMS_MAXSIM_TOPK_COUNTER_WORDS words, zero before the launch and after it
   float* values;      // (k)
   int64_t* indices;   // (k)
   int32_t k;
 };
+constexpr uint32_t kTicketGroups = 8, kTicketLine = 16, kTicketTwoLevel = 64;
+static_assert(kTicketLine * (1 + kTicketGroups) == TMS_MAXSIM_TOPK_COUNTER_WORDS, "the counter block of the header");
 // Four waves a workgroup, as the small-batch kernel: a 256 x 180-token call then spreads
 // over 256 CUs. 16-wave workgroups take four times fewer tickets and rank with four lanes
 // per key, but leave three quarters of the CUs idle at that size (17.5 against 13.6 us
@@ -282,20 +290,36 @@ __global__ void __launch_bounds__(kTopkNT) rerank_topk_kernel(RerankArgs a, Topk
   __shared__ uint32_t last;
   // The barrier orders every wave's score stores before thread 0's agent-scope release
   // (cumulative: on this part it writes the XCD's L2 back, once per workgroup, not per
-  // wave); the ticket is a relaxed RMW in that release sequence; the last workgroup's
-  // thread 0 acquires before the second barrier hands the scores to its other waves.
+  // wave); a ticket is a relaxed RMW in that release sequence; the last workgroup's thread
+  // 0 acquires before the second barrier hands the scores to its other waves.
   __syncthreads();
   if (threadIdx.x == 0) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const uint32_t prev = __hip_atomic_fetch_add(t.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = prev == gridDim.x - 1 ? 1u : 0u;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const uint32_t G = gridDim.x;
+    uint32_t l;
+    if (G < kTicketTwoLevel) {
+      l = __hip_atomic_fetch_add(t.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1 ? 1u : 0u;
+    } else {
+      const uint32_t grp = blockIdx.x % kTicketGroups;
+      const uint32_t members = (G - grp + kTicketGroups - 1) / kTicketGroups;  // workgroups with this group
+      uint32_t* gc = t.counter + kTicketLine * (1 + grp);
+      l = 0u;
+      if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == members - 1) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "agent");  // the group's scores, passed on
+        __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        l = __hip_atomic_fetch_add(t.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kTicketGroups - 1
+                ? 1u
+                : 0u;
+      }
+    }
+    if (l) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    last = l;
   }
   __syncthreads();
   if (!last) return;
   topk_chunk<true, true, kTopkNT, kShortRow>(a.out, a.B, nullptr, a.B, a.B, nullptr, 0, t.values, t.indices, t.k, 0,
                                             0);
-  if (threadIdx.x == 0) *t.counter = 0u;
+  if (threadIdx.x == 0) __hip_atomic_store(t.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int DT, int KS, int NB>

@@ -89,16 +89,17 @@ def _one_launch_workgroups(B: int, nd: int) -> int:
 
 
 def _scratch(dev: torch.device, stream: int) -> tuple[int, int]:
-    """Device addresses of the one-launch path's ticket counter and its B <= 1,024 scores,
-    one buffer per device and stream: a launch leaves the counter zero and uses the
+    """Device addresses of the one-launch path's ticket counters and its B <= 1,024 scores,
+    one buffer per device and stream: a launch leaves the counters zero and uses the
     scores only within itself, and launches on one stream never overlap."""
     key = (dev.index, stream)
     c = _SCRATCH.get(key)
     if c is None:
-        c = torch.zeros(4 + 1024, dtype=torch.int32, device=dev)  # counter, then scores from byte 16
+        words = _lib.TMS_MAXSIM_TOPK_COUNTER_WORDS
+        c = torch.zeros(words + 1024, dtype=torch.int32, device=dev)  # counters, then the scores
         _SCRATCH[key] = c
     p = c.data_ptr()
-    return p, p + 16
+    return p, p + 4 * _lib.TMS_MAXSIM_TOPK_COUNTER_WORDS
 
 
 def _one_launch(Q: torch.Tensor, D: torch.Tensor, k: int):
