@@ -226,16 +226,16 @@ class Dense:
     def one_launch_line(self, torch, steps=200, warmup=20):
         """C1 and rerank only, after the timed steps: the same step through maxsim_topk, which
         scores and ranks in one launch (tms_maxsim_topk) when the call has at most
-        ONE_LAUNCH_MAX_WORKGROUPS workgroups (rerank: 256; C1's 1,000 documents take the two
-        kernels); wall clock around eager steps, as for the timed steps, and a check that
-        the results are those of the timed step."""
+        ONE_LAUNCH_MAX_TOKENS document tokens (rerank: 46K; C1: 128K); wall clock around
+        eager steps, as for the timed steps, and a check that the results are those of the
+        timed step."""
         if self.name not in ("c1", "rerank") or self.nQ != 1 or self.dtype == "fp32":
             return None
         from tilemaxsim_amd import maxsim_topk
-        from tilemaxsim_amd.topk import ONE_LAUNCH_MAX_WORKGROUPS, _one_launch_workgroups
-        wg = _one_launch_workgroups(self.B, self.Nd)
-        if wg > ONE_LAUNCH_MAX_WORKGROUPS:
+        from tilemaxsim_amd.topk import ONE_LAUNCH_MAX_TOKENS, _one_launch_workgroups
+        if self.B * self.Nd > ONE_LAUNCH_MAX_TOKENS:
             return None
+        wg = _one_launch_workgroups(self.B, self.Nd, self.d, self.Nq)
         k = min(self.k, self.B)
         q = self.Q[0]
         v, i = maxsim_topk(q, self.D, k)

@@ -118,7 +118,7 @@ def test_tied_scores_rank_by_lower_index(cuda):
 
 
 def test_public_entry_point_repeated_calls(cuda, monkeypatch):
-    """maxsim_topk takes the one launch for eager calls of at most 384 workgroups and
+    """maxsim_topk takes the one launch for eager calls of at most 160K document tokens and
     reuses one counter per stream: a sequence of calls whose grids shrink and grow must
     each give the two-call results (a counter left non-zero would leave a call's top-k
     unwritten), and larger calls take the two kernels."""
@@ -136,11 +136,11 @@ def test_public_entry_point_repeated_calls(cuda, monkeypatch):
     monkeypatch.setattr(topk_mod, "_one_launch", spy)
     g = torch.Generator(device="cuda").manual_seed(9)
     Q = torch.nn.functional.normalize(torch.randn(32, 128, device="cuda", generator=g), dim=-1).half()
-    # (B, nd, k, one launch?): 256 workgroups at 256 x 180, 300 at 300 x 64, 400 at 400 x 180,
-    # 512 at 1,024 x 32, 1,000 at 1,000 x 128
-    seq = [(256, 180, 100, True), (7, 30, 5, True), (1000, 128, 100, False), (1024, 32, 1024, False),
-           (512, 32, 512, True), (1, 16, 1, True), (300, 64, 100, True), (400, 180, 100, False),
-           (384, 64, 384, True), (64, 100, 64, True), (256, 180, 100, True)]
+    # (B, nd, k, one launch?): 4-, 8- and 16-wave workgroups (256 x 180, 1,024 x 32 with
+    # wpd 2, 1,000 x 128), and calls past 163,840 tokens (1,000 x 180, 1,024 x 300)
+    seq = [(256, 180, 100, True), (7, 30, 5, True), (1000, 128, 100, True), (1000, 180, 100, False),
+           (1024, 32, 1024, True), (512, 32, 512, True), (1, 16, 1, True), (1024, 300, 100, False),
+           (300, 64, 100, True), (768, 180, 100, True), (64, 100, 64, True), (256, 180, 100, True)]
     for B, nd, k, one in seq:
         D = torch.nn.functional.normalize(torch.randn(B, nd, 128, device="cuda", generator=g), dim=-1).half()
         v, i = tms.maxsim_topk(Q, D, k)

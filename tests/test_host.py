@@ -175,17 +175,21 @@ def test_header_constants_match_the_python_mirror():
         assert int(eval(defines[n].replace("LL", ""))) == getattr(_lib, n), n
 
 
-def test_one_launch_gate_counts_the_kernels_workgroups():
-    """maxsim_topk's gate counts tms_maxsim_topk's workgroups as the launch does: 1, 2 or 4
-    waves per document (while B x waves < 2,048 and at most one wave per 16-token tile),
-    four waves a workgroup."""
-    from tilemaxsim_amd.topk import ONE_LAUNCH_MAX_WORKGROUPS, _one_launch_workgroups
-    assert ONE_LAUNCH_MAX_WORKGROUPS == 384
-    # (B, nd) -> workgroups: 256 x 180 = 12 tiles -> 4 waves each; 1,024 documents stop at
-    # 2 waves (2,048 waves); 16 x 32 = 2 tiles -> 2 waves; 16-token documents -> 1 wave
-    for (B, nd), wg in {(256, 180): 256, (1000, 128): 1000, (64, 100): 64, (1024, 300): 512, (16, 32): 8,
-                        (1, 1): 1, (7, 16): 2, (5, 0): 2, (300, 64): 300, (512, 32): 256}.items():
+def test_one_launch_workgroups_mirror_the_launch():
+    """The workgroup count bench.py reports for tms_maxsim_topk is the launch's own: 1, 2
+    or 4 waves per document (while B x waves < 2,048 and at most one wave per 16-token
+    tile), then 4, 8 or 16 waves a workgroup (the fewest that keep the launch within 256
+    workgroups; at most 8 at d = 128 with two query blocks)."""
+    from tilemaxsim_amd.topk import ONE_LAUNCH_MAX_TOKENS, _one_launch_workgroups
+    assert ONE_LAUNCH_MAX_TOKENS == 163840
+    # (B, nd) -> workgroups: 256 x 180 = 12 tiles -> 4 waves each, 1,024 waves, 4 a group;
+    # 1,000 x 128 -> 4,000 waves, 16 a group; 1,024 documents stop at 2 waves (2,048
+    # waves, 8 a group); 16 x 32 = 2 tiles -> 2 waves; 16-token documents -> 1 wave
+    for (B, nd), wg in {(256, 180): 256, (1000, 128): 250, (64, 100): 64, (1024, 300): 256, (16, 32): 8,
+                        (1, 1): 1, (7, 16): 2, (5, 0): 2, (300, 64): 150, (512, 32): 256}.items():
         assert _one_launch_workgroups(B, nd) == wg, (B, nd)
+        assert _one_launch_workgroups(B, nd) <= 256
+    assert _one_launch_workgroups(1000, 128, d=128, nq=64) == 500  # 8 waves a group there
 
 
 def test_residual_c_abi_rejects_bad_arguments():

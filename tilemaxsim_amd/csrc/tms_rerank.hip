@@ -279,14 +279,13 @@ struct TopkTail {
 };
 constexpr uint32_t kTicketGroups = 8, kTicketLine = 16, kTicketTwoLevel = 64;
 static_assert(kTicketLine * (1 + kTicketGroups) == TMS_MAXSIM_TOPK_COUNTER_WORDS, "the counter block of the header");
-// Four waves a workgroup, as the small-batch kernel: a 256 x 180-token call then spreads
-// over 256 CUs. 16-wave workgroups take four times fewer tickets and rank with four lanes
-// per key, but leave three quarters of the CUs idle at that size (17.5 against 13.6 us
-// per eager call); they only won for short documents.
-constexpr int kTopkNT = 256;
-template <int DT, int KS, int NB>
-__global__ void __launch_bounds__(kTopkNT) rerank_topk_kernel(RerankArgs a, TopkTail t) {
-  rerank_body<DT, KS, NB, RR_FIXED, kTopkNT>(a);
+// NT threads a workgroup: four waves while the call has at most 1,024 waves (a 256 x
+// 180-token call then spreads over 256 CUs), eight or 16 above that, so that a launch
+// never has more than 256 workgroups: each one takes a ticket and writes its XCD's L2
+// back, and those costs grow with the workgroup count.
+template <int DT, int KS, int NB, int NT>
+__global__ void __launch_bounds__(NT) rerank_topk_kernel(RerankArgs a, TopkTail t) {
+  rerank_body<DT, KS, NB, RR_FIXED, NT>(a);
   __shared__ uint32_t last;
   // The barrier orders every wave's score stores before thread 0's agent-scope release
   // (cumulative: on this part it writes the XCD's L2 back, once per workgroup, not per
@@ -317,8 +316,7 @@ __global__ void __launch_bounds__(kTopkNT) rerank_topk_kernel(RerankArgs a, Topk
   }
   __syncthreads();
   if (!last) return;
-  topk_chunk<true, true, kTopkNT, kShortRow>(a.out, a.B, nullptr, a.B, a.B, nullptr, 0, t.values, t.indices, t.k, 0,
-                                            0);
+  topk_chunk<true, true, NT, kShortRow>(a.out, a.B, nullptr, a.B, a.B, nullptr, 0, t.values, t.indices, t.k, 0, 0);
   if (threadIdx.x == 0) __hip_atomic_store(t.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -406,6 +404,32 @@ int run_rerank(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, 
 
 }  // namespace tms
 
+namespace tms {
+
+template <int DTV, int KS, int NB>
+static void rerank_topk_launch(int nt, int64_t grid, hipStream_t st, const RerankArgs& a, const TopkTail& t) {
+  constexpr int kMaxNT = (KS == 4 && NB == 2) ? 512 : 1024;  // never instantiated past the cap
+  if (nt == 256)
+    hipLaunchKernelGGL((rerank_topk_kernel<DTV, KS, NB, 256>), dim3((unsigned)grid), dim3(256), 0, st, a, t);
+  else if (nt == 512)
+    hipLaunchKernelGGL((rerank_topk_kernel<DTV, KS, NB, 512>), dim3((unsigned)grid), dim3(512), 0, st, a, t);
+  else
+    hipLaunchKernelGGL((rerank_topk_kernel<DTV, KS, NB, kMaxNT>), dim3((unsigned)grid), dim3(kMaxNT), 0, st, a, t);
+}
+
+template <int DTV>
+static void rerank_topk_dispatch(int ks, bool two, int nt, int64_t grid, hipStream_t st, const RerankArgs& a,
+                                 const TopkTail& t) {
+  switch (ks) {
+    case 1: two ? rerank_topk_launch<DTV, 1, 2>(nt, grid, st, a, t) : rerank_topk_launch<DTV, 1, 1>(nt, grid, st, a, t); break;
+    case 2: two ? rerank_topk_launch<DTV, 2, 2>(nt, grid, st, a, t) : rerank_topk_launch<DTV, 2, 1>(nt, grid, st, a, t); break;
+    case 3: two ? rerank_topk_launch<DTV, 3, 2>(nt, grid, st, a, t) : rerank_topk_launch<DTV, 3, 1>(nt, grid, st, a, t); break;
+    default: two ? rerank_topk_launch<DTV, 4, 2>(nt, grid, st, a, t) : rerank_topk_launch<DTV, 4, 1>(nt, grid, st, a, t);
+  }
+}
+
+}  // namespace tms
+
 extern "C" int64_t tms_set_rerank_limit(int64_t tiles) {
   if (tiles < 0) return tms::g_rerank_tiles.load(std::memory_order_relaxed);
   return tms::g_rerank_tiles.exchange(tiles, std::memory_order_relaxed);
@@ -444,26 +468,17 @@ extern "C" int tms_maxsim_topk(const void* Q, int64_t nq, int64_t d, const void*
   const int64_t tiles = (nd + 15) / 16;
   a.wpd = 1;
   while (a.wpd < 4 && B * a.wpd < TMS_RERANK_TARGET_WAVES && 2 * a.wpd <= tiles) a.wpd *= 2;
-  const int64_t grid = (B * a.wpd + kTopkNT / 64 - 1) / (kTopkNT / 64);
+  const int64_t waves = B * a.wpd;
+  int nt = waves <= 1024 ? 256 : (waves <= 2048 ? 512 : 1024);
+  const int ks = (int)(d / 32);
+  const bool two = a.nblk == 2;
+  if (ks == 4 && two && nt > 512) nt = 512;  // 16 waves of that form spill registers
+  const int64_t grid = (waves + nt / 64 - 1) / (nt / 64);
   TopkTail t{counter, out_values, out_indices, (int32_t)k};
   hipStream_t st = (hipStream_t)stream;
-  const bool two = a.nblk == 2;
-  switch (d / 32) {
-#define TMS_RR_TOPK(KS)                                                                                              \
-  case KS:                                                                                                           \
-    if (dtype == TMS_DTYPE_F16) {                                                                                    \
-      if (two) hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_F16, KS, 2>), dim3((unsigned)grid), dim3(kTopkNT), 0, st, a, t); \
-      else hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_F16, KS, 1>), dim3((unsigned)grid), dim3(kTopkNT), 0, st, a, t);     \
-    } else {                                                                                                         \
-      if (two) hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_BF16, KS, 2>), dim3((unsigned)grid), dim3(kTopkNT), 0, st, a, t); \
-      else hipLaunchKernelGGL((rerank_topk_kernel<TMS_DTYPE_BF16, KS, 1>), dim3((unsigned)grid), dim3(kTopkNT), 0, st, a, t);    \
-    }                                                                                                                \
-    break;
-    TMS_RR_TOPK(1)
-    TMS_RR_TOPK(2)
-    TMS_RR_TOPK(3)
-    TMS_RR_TOPK(4)
-#undef TMS_RR_TOPK
-  }
+  if (dtype == TMS_DTYPE_F16)
+    rerank_topk_dispatch<TMS_DTYPE_F16>(ks, two, nt, grid, st, a, t);
+  else
+    rerank_topk_dispatch<TMS_DTYPE_BF16>(ks, two, nt, grid, st, a, t);
   return check_launch("rerank_topk_kernel");
 }

@@ -68,24 +68,30 @@ def topk(scores: torch.Tensor, k: int):
 
 
 _SCRATCH: dict = {}
-# Workgroups up to which one launch beats scoring, then ranking, for an eager call. Every
-# workgroup of the launch takes one device-scope ticket on a single counter and makes its
-# scores visible device-wide (an L2 write-back of its XCD) before the last one ranks
-# them, so the launch grows slower with its workgroup count. Measured on MI355X (32-token
-# query, d = 128, 32-300-token documents): 11.5-17 us against 20 us for the two calls up
-# to 384 workgroups; even or behind at 512 for long documents. A HIP graph replays two
-# launches without host cost, where one launch never wins by more than noise: captured
-# calls take the two kernels.
-ONE_LAUNCH_MAX_WORKGROUPS = 384
+# Documents' tokens (B x Nd) up to which one launch beats scoring, then ranking, for an
+# eager call. The launch pays a device-scope ticket and an L2 write-back per workgroup
+# (at most 256 of them) and ranks after the last one, so it saves the second call's host
+# cost (about 10 us) while the GPU time stays below it. Measured on MI355X (32-token
+# query, d = 128): every shape up to 160K tokens wins (1,000 x 128: 16.1 us against
+# 19.3; 512 x 300: 17.2 against 19.5); 1,000 x 180 (180K) loses by 0.8 us and longer
+# calls by 1-3 us. A HIP graph replays two launches without host cost, where one launch
+# never wins by more than noise: captured calls take the two kernels.
+ONE_LAUNCH_MAX_TOKENS = 160 * 1024
 
 
-def _one_launch_workgroups(B: int, nd: int) -> int:
+def _one_launch_workgroups(B: int, nd: int, d: int = 128, nq: int = 32) -> int:
     """Workgroups of tms_maxsim_topk's launch: 1, 2 or 4 waves per document (enough for
-    about 2,048 waves, at most one per 16-token tile), four waves a workgroup."""
+    about 2,048 waves, at most one per 16-token tile); 4, 8 or 16 waves a workgroup, the
+    fewest that keep the launch within 256 workgroups (at most 8 at d = 128 with two
+    32-token query blocks)."""
     tiles, wpd = (nd + 15) // 16, 1
     while wpd < 4 and B * wpd < 2048 and 2 * wpd <= tiles:
         wpd *= 2
-    return (B * wpd + 3) // 4
+    waves = B * wpd
+    per = 4 if waves <= 1024 else (8 if waves <= 2048 else 16)
+    if d == 128 and nq > 32:
+        per = min(per, 8)
+    return (waves + per - 1) // per
 
 
 def _scratch(dev: torch.device, stream: int) -> tuple[int, int]:
@@ -105,13 +111,13 @@ def _scratch(dev: torch.device, stream: int) -> tuple[int, int]:
 def _one_launch(Q: torch.Tensor, D: torch.Tensor, k: int):
     """``tms_maxsim_topk`` for the eager calls it takes (one query of at most 64 fp16 /
     bf16 tokens, d in {32, 64, 96, 128}, 1..1,024 contiguous documents, 1 <= k <= B,
-    16-byte aligned, at most ONE_LAUNCH_MAX_WORKGROUPS workgroups); None otherwise (the
+    16-byte aligned, at most ONE_LAUNCH_MAX_TOKENS document tokens); None otherwise (the
     caller scores, then ranks)."""
     if not (isinstance(Q, torch.Tensor) and isinstance(D, torch.Tensor) and Q.dim() == 2 and D.dim() == 3):
         return None
     B, Nd, d = D.shape
     # the size checks first: a call beyond them costs the two-kernel path nothing more
-    if not 1 <= B <= 1024 or not 1 <= k <= B or _one_launch_workgroups(B, Nd) > ONE_LAUNCH_MAX_WORKGROUPS:
+    if not 1 <= B <= 1024 or not 1 <= k <= B or B * Nd > ONE_LAUNCH_MAX_TOKENS:
         return None
     Nq = Q.shape[0]
     if (d not in (32, 64, 96, 128) or not 1 <= Nq <= 64 or Q.shape[1] != d
