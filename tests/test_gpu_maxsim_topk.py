@@ -76,13 +76,18 @@ def _against_two_calls(Qg, Dg, k, fused, Q=None, D=None, what=""):
 
 
 # (nq, nd, d, B, k): B sets the grid (one to 256 workgroups, the last one partly empty),
-# nd the waves per document (1-3 tiles: 1 wave; 4-7: 2; >= 8: 4), nq one or two 32-token
-# query blocks, k from 1 to B (the selection's every ordering form up to 1,024)
+# nd the waves per document (1-3 tiles: 1 wave; 4-7: 2; >= 8: 4), and the call's waves
+# the workgroup size (4 waves up to 1,024 waves, 8 up to 2,048, 16 above; 8 at most at
+# d = 128 with two query blocks); nq one or two 32-token query blocks; k from 1 to B
+# (the selection's every ordering form up to 1,024, at 256, 512 and 1,024 threads)
 CASES = [
     (32, 180, 128, 256, 100), (32, 128, 128, 1000, 100), (32, 128, 128, 1024, 1024), (1, 1, 32, 1, 1),
     (1, 16, 32, 7, 7), (33, 181, 128, 11, 3), (64, 300, 96, 100, 10), (5, 7, 96, 21, 21),
     (32, 64, 64, 513, 257), (40, 33, 128, 999, 1), (32, 0, 128, 5, 3), (64, 16, 64, 1024, 300),
     (17, 100, 32, 300, 64), (32, 1, 128, 1024, 100),
+    (32, 128, 128, 1000, 1000),  # 16-wave workgroups, bitonic ordering at 1,024 threads
+    (64, 200, 128, 700, 300),    # two query blocks at d = 128: capped at 8 waves (350 workgroups)
+    (17, 100, 96, 1024, 1024),   # 8-wave workgroups, bitonic ordering at 512 threads
 ]
 
 
