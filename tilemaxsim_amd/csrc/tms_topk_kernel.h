@@ -299,17 +299,30 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
     uint32_t(&hb)[kHistCopies][256] = hist[pass % 3];
     {
       uint32_t run_bin = 0u, run_n = 0u;  // a run of this thread's keys in one bin
-#pragma unroll
-      for (int e = 0; e < kPerThread; e++) {
-        if (shift + w == 64 || (key[e] >> (shift + w)) == prefix) {
-          const uint32_t bin = (uint32_t)(key[e] >> shift) & ((1u << w) - 1u);
-          if (run_n != 0u && bin != run_bin) {
-            atomicAdd(&hb[wid % kHistCopies][run_bin], run_n);
-            run_n = 0u;
-          }
-          run_bin = bin;
-          run_n++;
+      auto count = [&](uint32_t bin) {
+        if (run_n != 0u && bin != run_bin) {
+          atomicAdd(&hb[wid % kHistCopies][run_bin], run_n);
+          run_n = 0u;
         }
+        run_bin = bin;
+        run_n++;
+      };
+      if (shift >= 32) {
+        // The digit lies in the high word (the score's order bits, where rows of distinct
+        // scores are decided): 32-bit shifts and one bit-field extract per key instead of
+        // 64-bit shifts. top = shift + w - 32 <= 32; top == 32 is the first pass from the
+        // top, which every key takes.
+        const uint32_t sh = (uint32_t)(shift - 32), top = sh + (uint32_t)w, pre = (uint32_t)prefix;
+#pragma unroll
+        for (int e = 0; e < kPerThread; e++) {
+          const uint32_t hi = (uint32_t)(key[e] >> 32);
+          if (top == 32u || (hi >> top) == pre) count(__builtin_amdgcn_ubfe(hi, sh, (uint32_t)w));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < kPerThread; e++)
+          if (shift + w == 64 || (key[e] >> (shift + w)) == prefix)
+            count((uint32_t)(key[e] >> shift) & ((1u << w) - 1u));
       }
       if (run_n != 0u) atomicAdd(&hb[wid % kHistCopies][run_bin], run_n);
     }
