@@ -102,8 +102,8 @@ def _scratch(dev: torch.device, stream: int) -> tuple[int, int]:
     c = _SCRATCH.get(key)
     if c is None:
         words = _lib.TMS_MAXSIM_TOPK_COUNTER_WORDS
-        c = torch.zeros(words + 1024, dtype=torch.int32, device=dev)  # counters, then the scores
-        _SCRATCH[key] = c
+        # counters, then the scores; setdefault keeps one buffer when two threads race here
+        c = _SCRATCH.setdefault(key, torch.zeros(words + 1024, dtype=torch.int32, device=dev))
     p = c.data_ptr()
     return p, p + 4 * _lib.TMS_MAXSIM_TOPK_COUNTER_WORDS
 
