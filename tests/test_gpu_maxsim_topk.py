@@ -178,3 +178,45 @@ def test_public_entry_point_falls_back_outside_the_one_launch_shapes(cuda):
         rv, ri = tms.topk(tms.flash_maxsim_v2_multiquery(Q, D), k)
         _same_bits(v, rv, "values")
         _same_bits(i, ri, "indices")
+
+
+def test_threads_on_their_own_streams(cuda):
+    """Four host threads, each on its own stream (default priority), call maxsim_topk 40
+    times against their own candidates: each stream has its own counters and scratch
+    scores, so every result is the two calls' result."""
+    import threading
+    import torch
+    import tilemaxsim_amd as tms
+    g = torch.Generator(device="cuda").manual_seed(21)
+
+    def normed(*shape):
+        return torch.nn.functional.normalize(torch.randn(*shape, device="cuda", generator=g), dim=-1).half()
+
+    Q = normed(32, 128)
+    work = [(normed(B, nd, 128), k) for B, nd, k in [(256, 180, 100), (1000, 128, 50), (64, 40, 64), (513, 96, 257)]]
+    torch.cuda.synchronize()
+    results = [None] * len(work)
+    errors = []
+
+    def run(t):
+        try:
+            D, k = work[t]
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                outs = [tms.maxsim_topk(Q, D, k) for _ in range(40)]
+            s.synchronize()
+            results[t] = outs
+        except Exception as e:  # reported below, on the test's thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(t,)) for t in range(len(work))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not errors, errors
+    for t, (D, k) in enumerate(work):
+        rv, ri = tms.topk(tms.flash_maxsim_v2_multiquery(Q, D), k)
+        for v, i in results[t]:
+            _same_bits(v, rv, f"thread {t} values")
+            _same_bits(i, ri, f"thread {t} indices")
