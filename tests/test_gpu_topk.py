@@ -202,3 +202,44 @@ def test_topk_short_rows_every_ordering_form(cuda, n, k):
     v, i = v.cpu().numpy(), i.cpu().numpy()
     for r in range(3):
         _check_row(v[r], i[r], x[r], k)
+
+
+@pytest.mark.parametrize("k", [1, 2, 100, 127, 128, 129])
+@pytest.mark.parametrize("spread", [False, True])
+def test_topk_prefilter_every_candidate_count(cuda, k, spread):
+    """Chunks that pass k keys on (k <= 128) first drop the keys below a bound taken from
+    each wave's j-th largest thread maximum (j = ceil(k / 4)) and select among the rest,
+    gathered in LDS, when at most 1,024 remain (1 to 4 per thread); with more, the chunk
+    keeps its registers. A chunk's element e * 256 + t sits in thread t (wave t // 64),
+    slot e. Here the first j threads of every wave hold h high keys each, all other keys
+    low, so the candidates number 4j * h (all high keys tie when spread is False: the
+    bound then falls on them and the index decides) -- h = 1, 3, 6, 10 give 1, 2, 3 and 4
+    candidates per thread at k = 100, and h = 11 and 16 overflow the buffer. Every form
+    against the oracle, bit for bit, at the first level and at the level the chunks'
+    survivors feed."""
+    import torch
+    from tilemaxsim_amd import topk
+    rng = np.random.default_rng(500 + k + (1000 if spread else 0))
+    j = -(-k // 4)
+    hs = (1, 3, 6, 10, 11, 16)
+    n = 4096 * len(hs) * 2 + 777  # two chunks per h, and a ragged last chunk
+    rows = []
+    for r in range(2):
+        x = rng.random(n).astype(np.float32)  # low keys in [0, 1)
+        for c in range(n // 4096):
+            h = hs[c % len(hs)]
+            blk = np.zeros((16, 256), dtype=np.float32)
+            lanes = (np.arange(256) % 64) < j
+            hi = 11.0 + (rng.random((h, 256)) * 0.5 if spread else 0.0)
+            blk[:h, lanes] = np.broadcast_to(hi, (h, 256))[:, lanes]
+            sel = np.zeros((16, 256), dtype=bool)
+            sel[:h, lanes] = True
+            chunk = x[c * 4096:(c + 1) * 4096].reshape(16, 256)
+            chunk[sel] = blk[sel]
+        rows.append(x)
+    x = np.stack(rows)
+    print(f"k={k} spread={spread} n={n}", flush=True)
+    v, i = topk(torch.from_numpy(x).cuda(), k)
+    v, i = v.cpu().numpy(), i.cpu().numpy()
+    for r in range(x.shape[0]):
+        _check_row(v[r], i[r], x[r], k)

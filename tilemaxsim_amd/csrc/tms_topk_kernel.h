@@ -38,15 +38,20 @@ constexpr int kMaxK = kChunk / 4;
 constexpr int kShortRow = 1024;
 constexpr int kShortThreads = 256;
 constexpr int kRankSortMaxK = 256;  // the last level orders up to this many keys by rank, more by a bitonic sort
+// Levels that pass k keys on, at k <= kFilterMaxK, first drop the keys below a bound on
+// the chunk's k-th key and select among the rest, gathered in LDS, when at most
+// kCandCap of them remain.
+constexpr int kFilterMaxK = 128;
+constexpr int kCandCap = 1024;
 
-// Order-preserving image of a float's bits. -0.0 is taken as +0.0 (they compare equal,
-// so they tie and go by index) and every NaN as the positive quiet NaN, so that a NaN
-// with its sign bit set (x86's default NaN, or a negated one) still ranks above +inf.
+// Order-preserving image of a float's bits, never 0 (0 is the padding key). Positive
+// values map to b | 2^31 and negative ones to -b (mod 2^32), so -0.0 lands on +0.0's key
+// (they compare equal, so they tie and go by index); every NaN, either sign, maps to the
+// top key, above +inf, as torch ranks NaN.
 __device__ __forceinline__ uint32_t order_key(float f) {
-  uint32_t b = __builtin_bit_cast(uint32_t, f);
-  b = (b == 0x80000000u) ? 0u : b;
-  b = ((b & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : b;
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  const uint32_t b = __builtin_bit_cast(uint32_t, f);
+  const uint32_t o = (int32_t)b < 0 ? 0u - b : (b | 0x80000000u);
+  return (b & 0x7fffffffu) > 0x7f800000u ? 0xffffffffu : o;
 }
 
 // FIRST: input is fp32 scores (row stride in_stride), indices are positions in the row.
@@ -93,6 +98,16 @@ __device__ __forceinline__ void wave_minmax(uint64_t& lo, uint64_t& hi, uint32_t
   step(swap16_u64(lo, lane), swap16_u64(hi, lane), swap16_u32(n, lane));
   step(swap32_u64(lo, lane), swap32_u64(hi, lane), swap32_u32(n, lane));
 }
+// Wave-wide maximum of a 32-bit value; every lane gets it.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x, int lane) {
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  x = mx(x, dpp_u32<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = mx(x, dpp_u32<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = mx(x, dpp_u32<0x141>(x));  // row_half_mirror
+  x = mx(x, dpp_u32<0x140>(x));  // row_mirror
+  x = mx(x, swap16_u32(x, lane));
+  return mx(x, swap32_u32(x, lane));
+}
 // Inclusive prefix sum over the 64 lanes (lane order): row shifts, then row broadcasts.
 __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x) {
   x += dpp_u32<0x111>(x);  // row_shr:1
@@ -122,7 +137,9 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
   // cleared after pass p's barrier, when no wave can still be scanning it (its last
   // scan, in pass p - 1, ended before that barrier) -- one barrier per pass.
   __shared__ uint32_t hist[3][kHistCopies][256];
-  __shared__ uint32_t n_gt, n_eq;
+  __shared__ uint32_t n_gt, n_eq, n_cand;
+  __shared__ uint64_t cand[LAST ? 1 : kCandCap];
+  __shared__ uint32_t red_t[kTopkWaves], red_m[kTopkWaves];
   __shared__ uint64_t sel[LAST ? kMaxK : 1];
   // FIRST && LAST (a row that fits one chunk): the selected scores' own bits, kept from
   // the loads so the output needs no second read of the scores.
@@ -130,31 +147,50 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t c0 = chunk * CH;
   // All loads are issued before any key is formed (one memory round trip, not one per
-  // element); positions past the row read its last element and become padding.
+  // element). A chunk inside the row reads from one uniform base at 32-bit offsets and
+  // every key is real; in the row's last chunk, positions past the row read its last
+  // element and become padding.
   uint64_t key[kPerThread];
   float v[kPerThread];
+  const bool inside = c0 + CH <= n_in;  // uniform
   if constexpr (FIRST) {
+    if (inside) {
+      const float* __restrict__ base = vals + row * val_stride + c0;
 #pragma unroll
-    for (int e = 0; e < kPerThread; e++) {
-      const int64_t p = c0 + e * NT + tid;
-      v[e] = vals[row * val_stride + (p < n_in ? p : n_in - 1)];
-    }
+      for (int e = 0; e < kPerThread; e++) v[e] = base[e * NT + tid];
+      const uint32_t inv = 0xffffffffu - (uint32_t)c0 - (uint32_t)tid;  // inverted index of element 0
 #pragma unroll
-    for (int e = 0; e < kPerThread; e++) {
-      const int64_t p = c0 + e * NT + tid;
-      key[e] = p < n_in ? ((uint64_t)order_key(v[e]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)p)
-                        : 0ull;  // below every real element
+      for (int e = 0; e < kPerThread; e++)
+        key[e] = ((uint64_t)order_key(v[e]) << 32) | (uint64_t)(inv - (uint32_t)(e * NT));
+    } else {
+#pragma unroll
+      for (int e = 0; e < kPerThread; e++) {
+        const int64_t p = c0 + e * NT + tid;
+        v[e] = vals[row * val_stride + (p < n_in ? p : n_in - 1)];
+      }
+#pragma unroll
+      for (int e = 0; e < kPerThread; e++) {
+        const int64_t p = c0 + e * NT + tid;
+        key[e] = p < n_in ? ((uint64_t)order_key(v[e]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)p)
+                          : 0ull;  // below every real element
+      }
     }
   } else {
+    if (inside) {
+      const uint64_t* __restrict__ base = keys_in + row * in_stride + c0;
 #pragma unroll
-    for (int e = 0; e < kPerThread; e++) {
-      const int64_t p = c0 + e * NT + tid;
-      key[e] = keys_in[row * in_stride + (p < n_in ? p : n_in - 1)];
-    }
+      for (int e = 0; e < kPerThread; e++) key[e] = base[e * NT + tid];
+    } else {
 #pragma unroll
-    for (int e = 0; e < kPerThread; e++) {
-      const int64_t p = c0 + e * NT + tid;
-      key[e] = p < n_in ? key[e] : 0ull;
+      for (int e = 0; e < kPerThread; e++) {
+        const int64_t p = c0 + e * NT + tid;
+        key[e] = keys_in[row * in_stride + (p < n_in ? p : n_in - 1)];
+      }
+#pragma unroll
+      for (int e = 0; e < kPerThread; e++) {
+        const int64_t p = c0 + e * NT + tid;
+        key[e] = p < n_in ? key[e] : 0ull;
+      }
     }
   }
 
@@ -243,11 +279,93 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
   if (tid == 0) {
     n_gt = 0u;
     n_eq = 0u;
+    n_cand = 0u;
   }
   if constexpr (LAST) {
     const int k8 = (k + 7) & ~7;
     if (k <= kRankSortMaxK)
       for (int t = k + tid; t < k8 + kRankPad; t += NT) sel[t] = 0ull;
+  }
+  auto below = [&](uint64_t m) -> uint32_t {  // set bits of m in lanes below this one
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+  };
+
+  // The selection below runs over key[0, E); key[E, kPerThread) are 0 (padding). After
+  // the pre-filter, the candidates' high words lie in [fT, fM].
+  int E = kPerThread;
+  bool filtered = false;
+  uint32_t fT = 0u, fM = 0u;
+  if constexpr (!LAST) {
+    // Pre-filter. Wave w finds T_w, the j-th largest of its 64 threads' maximum high words
+    // (j = ceil(k / waves); padding counts as 0). Each of those j threads holds a key whose
+    // high word is >= T_w, so the chunk has at least waves * j >= k keys whose high word
+    // is >= T = min_w T_w, and every key below T is below all of them: the top k lie among
+    // the keys with high word >= T. On continuous scores they are a few k; they are
+    // gathered in LDS and selected from there, at most kCandCap / NT per thread. T = 0
+    // (fewer than j real keys in some wave) or more than kCandCap candidates (ties at the
+    // bound) keep the registers and the full selection.
+    if (k <= kFilterMaxK) {
+      static_assert(kFilterMaxK <= 64 * kTopkWaves, "j <= 64: the bound is taken within each wave");
+      static_assert(kCandCap % NT == 0 && kCandCap / NT <= kPerThread, "candidates per thread");
+      uint32_t tm = 0u;
+#pragma unroll
+      for (int e = 0; e < kPerThread; e++) {
+        const uint32_t h = (uint32_t)(key[e] >> 32);
+        tm = h > tm ? h : tm;
+      }
+      // the j-th largest of the wave's tm, one bit at a time from the top: the largest t
+      // that at least j lanes reach
+      const uint32_t j = (uint32_t)((k + kTopkWaves - 1) / kTopkWaves);
+      uint32_t t = 0u;
+#pragma unroll
+      for (int b = 31; b >= 0; b--) {
+        const uint32_t c = t | (1u << b);
+        t = (uint32_t)__popcll(__ballot(tm >= c)) >= j ? c : t;
+      }
+      const uint32_t wm = wave_max_u32(tm, lane);
+      if (lane == 0) {
+        red_t[wid] = t;
+        red_m[wid] = wm;
+      }
+      __syncthreads();
+      uint32_t T = red_t[0], M = red_m[0];
+#pragma unroll
+      for (int w = 1; w < kTopkWaves; w++) {
+        T = red_t[w] < T ? red_t[w] : T;
+        M = red_m[w] > M ? red_m[w] : M;
+      }
+      if (T != 0u) {  // uniform
+        uint64_t mc[kPerThread];
+        uint32_t wave_n = 0u;
+#pragma unroll
+        for (int e = 0; e < kPerThread; e++) {
+          mc[e] = __ballot((uint32_t)(key[e] >> 32) >= T);
+          wave_n += (uint32_t)__popcll(mc[e]);
+        }
+        uint32_t base = 0u;
+        if (lane == 0) base = atomicAdd(&n_cand, wave_n);
+        base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
+#pragma unroll
+        for (int e = 0; e < kPerThread; e++) {
+          const uint32_t pos = base + below(mc[e]);
+          if ((uint32_t)(key[e] >> 32) >= T && pos < (uint32_t)kCandCap) cand[pos] = key[e];
+          base += (uint32_t)__popcll(mc[e]);
+        }
+        __syncthreads();
+        const uint32_t nc = (uint32_t)__builtin_amdgcn_readfirstlane((int)n_cand);
+        if (nc <= (uint32_t)kCandCap) {
+          filtered = true;
+          fT = T;
+          fM = M;
+          E = (int)((nc + NT - 1) / NT);
+#pragma unroll
+          for (int e = 0; e < kPerThread; e++) {
+            const uint32_t p = (uint32_t)(e * NT + tid);
+            key[e] = (e < kCandCap / NT && p < nc) ? cand[e < kCandCap / NT ? p : 0] : 0ull;
+          }
+        }
+      }
+    }
   }
 
   // Where the real keys differ: the radix passes start below the bits that every real
@@ -256,12 +374,20 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
   // keys (0) are not real; a chunk with fewer than k real keys starts from the top.
   __shared__ uint64_t red_lo[kTopkWaves], red_hi[kTopkWaves];
   __shared__ uint32_t red_n[kTopkWaves];
-  {
+  uint64_t prefix = 0;  // the key bits fixed so far: candidates have key >> shift == prefix
+  int shift = 64;
+  if (filtered) {
+    // At least k candidates, all with high words in [fT, fM]: they share the bits above
+    // the highest bit at which fT and fM differ (all 32 if they are equal).
+    const uint32_t diff = fT ^ fM;
+    shift = diff == 0u ? 32 : 64 - __builtin_clz(diff);
+    prefix = shift == 64 ? 0ull : ((uint64_t)fM << 32) >> shift;
+  } else {
     uint64_t lo = ~0ull, hi = 0ull;
     uint32_t nr = 0u;
 #pragma unroll
     for (int e = 0; e < kPerThread; e++) {
-      if (key[e] != 0ull) {
+      if (e < E && key[e] != 0ull) {
         lo = key[e] < lo ? key[e] : lo;
         hi = key[e] > hi ? key[e] : hi;
         nr++;
@@ -273,14 +399,11 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
       red_hi[wid] = hi;
       red_n[wid] = nr;
     }
-  }
-  __syncthreads();
-  uint64_t prefix = 0;  // the key bits fixed so far: candidates have key >> shift == prefix
-  int shift = 64;
-  {  // lane w brings wave w's partial results; every lane gets the chunk's
-    uint64_t lo = lane < kTopkWaves ? red_lo[lane] : ~0ull;
-    uint64_t hi = lane < kTopkWaves ? red_hi[lane] : 0ull;
-    uint32_t nr = lane < kTopkWaves ? red_n[lane] : 0u;
+    __syncthreads();
+    // lane w brings wave w's partial results; every lane gets the chunk's
+    lo = lane < kTopkWaves ? red_lo[lane] : ~0ull;
+    hi = lane < kTopkWaves ? red_hi[lane] : 0ull;
+    nr = lane < kTopkWaves ? red_n[lane] : 0u;
     wave_minmax(lo, hi, nr, lane);
     if (nr >= (uint32_t)k) {
       const uint64_t diff = hi ^ lo;
@@ -315,14 +438,17 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
         const uint32_t sh = (uint32_t)(shift - 32), top = sh + (uint32_t)w, pre = (uint32_t)prefix;
 #pragma unroll
         for (int e = 0; e < kPerThread; e++) {
+          if (e >= E) break;
           const uint32_t hi = (uint32_t)(key[e] >> 32);
           if (top == 32u || (hi >> top) == pre) count(__builtin_amdgcn_ubfe(hi, sh, (uint32_t)w));
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < kPerThread; e++)
+        for (int e = 0; e < kPerThread; e++) {
+          if (e >= E) break;
           if (shift + w == 64 || (key[e] >> (shift + w)) == prefix)
             count((uint32_t)(key[e] >> shift) & ((1u << w) - 1u));
+        }
       }
       if (run_n != 0u) atomicAdd(&hb[wid % kHistCopies][run_bin], run_n);
     }
@@ -364,9 +490,6 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
     if constexpr (LAST) sel[pos] = kv;
     else keys_out[row * out_stride + chunk * k + pos] = kv;
   };
-  auto below = [&](uint64_t m) -> uint32_t {  // set bits of m in lanes below this one
-    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-  };
   // The wave's selected keys in element order: ballots first, then one atomic per wave
   // for all of them (and one for the keys equal to T, which only padding can need).
   uint64_t mg[kPerThread];
@@ -374,6 +497,8 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
   uint64_t any_eq = 0ull;
 #pragma unroll
   for (int e = 0; e < kPerThread; e++) {
+    mg[e] = 0ull;
+    if (e >= E) continue;
     mg[e] = __ballot(key[e] > T);
     wave_gt += (uint32_t)__popcll(mg[e]);
     if (need_eq > 0u) {
@@ -389,6 +514,7 @@ __device__ __forceinline__ void topk_chunk(const float* __restrict__ vals, int64
   base_eq = (uint32_t)__builtin_amdgcn_readlane((int)base_eq, 0);
 #pragma unroll
   for (int e = 0; e < kPerThread; e++) {
+    if (e >= E) break;
     if (mg[e] != 0ull) {
       const uint32_t pos = base_gt + below(mg[e]);
       if (key[e] > T && pos < (uint32_t)k - need_eq) put(pos, key[e], e);  // always below; bounds every write
