@@ -10,7 +10,9 @@
 // Tournament: a workgroup selects the best k of a chunk of kChunk keys and each level
 // shrinks a row by kChunk / k until one chunk holds it; the last level sorts its k keys
 // (a last level of at most kShortRow keys runs a chunk of that size over four waves).
-// Intermediate keys live in a caller-provided workspace. Selection is a radix select on
+// Intermediate keys live in a caller-provided workspace. Levels that pass keys on first
+// drop the keys below a bound on the chunk's k-th key taken from the threads' maxima
+// (at k <= kFilterMaxK) and select among the survivors. Selection is a radix select on
 // the 64-bit keys held in registers (4 or 16 per thread): one 256-bin LDS histogram per 8-bit
 // digit, from the highest bit at which the chunk's real keys differ, narrowed to the
 // keys that share the digits fixed so far, until the k-th largest key is known or a
