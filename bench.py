@@ -24,8 +24,10 @@ Prints ONE JSON line on stdout. ``value`` is (query, document) pairs scored per 
 over the whole step; ``roofline`` is the dominant kernel's algorithmic bandwidth from
 HIP events around each of its launches; ``cpu_baseline`` times the reference's PyTorch
 scoring path (restated in ``oracle/torch_ref.py``, fp32 on the CPU with
-``torch.set_num_threads(os.cpu_count())``) on this host over a bounded sample, with the
-numpy restatement beside it.
+``torch.set_num_threads(os.cpu_count())``) on this host, streaming 500-document chunks of
+a prefix of the corpus larger than the host's last-level cache (20,000 documents for the
+dense and variable-length configs, 100,000 for PQ) and extrapolated linearly to docs/s
+(``extrapolated``, ``prefix_docs``), with the numpy restatement beside it.
 """
 from __future__ import annotations
 
@@ -267,18 +269,18 @@ class Dense:
     def cpu_baseline(self, seconds):
         from oracle import maxsim_oracle as orc
         from oracle import torch_ref as tr
-        n = min(self.B, 4000)
+        n = min(self.B, CPU_PREFIX_DOCS)
         Qt, Dt = self.Q[0].cpu(), self.D[:n].cpu()
+        nbytes = Dt.numel() * Dt.element_size()
         # torch: the reference's own formulation; each chunk is cast .float() in the timed calls
-        base = _time_torch_cpu(lambda: tr.maxsim_naive(Qt, Dt, chunk=500), n, seconds,
-                               f"{n} docs of this corpus x query 0, torch fp32 einsum -> max -> sum "
-                               "(pytorch_maxsim_naive), 500-doc chunks, repeated")
-        Q, D = self.Q[0], self.D[:n]
+        base = _time_cpu_prefix(lambda b0, b1: tr.maxsim_naive(Qt, Dt[b0:b1], chunk=500), n, self.B, seconds,
+                                "query 0, torch fp32 einsum -> max -> sum (pytorch_maxsim_naive)", nbytes)
         if self.dtype == "bf16":  # numpy has no bfloat16: cast once, outside the timed calls
-            Q, D = Q.float(), D.float()
-        Q, D = Q.cpu().numpy(), D.cpu().numpy()
-        base["numpy_port"] = _time_cpu(lambda: orc.maxsim_naive(Q, D, chunk=500), n, seconds / 2,
-                                       f"{n} docs x query 0, numpy fp32 materialise-then-reduce, repeated")
+            Dt = Dt.float()
+        Q, D = self.Q[0].float().cpu().numpy() if self.dtype == "bf16" else Qt.numpy(), Dt.numpy()
+        base["numpy_port"] = _time_cpu_prefix(lambda b0, b1: orc.maxsim_naive(Q, D[b0:b1], chunk=500), n, self.B,
+                                              seconds / 2, "query 0, numpy fp32 materialise-then-reduce",
+                                              D.nbytes, torch_threads=False)
         return base
 
 
@@ -395,17 +397,19 @@ class Varlen(Dense):
     def cpu_baseline(self, seconds):
         from oracle import maxsim_oracle as orc
         from oracle import torch_ref as tr
-        n = 4000
+        n = min(self.B, CPU_PREFIX_DOCS)
         offs_t = self.offsets[: n + 1].cpu()
         Qt, Dt = self.Q[0].cpu(), self.D[: int(offs_t[-1])].cpu()
-        base = _time_torch_cpu(lambda: tr.maxsim_varlen_masked(Qt, Dt, offs_t, chunk=500), n, seconds,
-                               f"first {n} docs x query 0, torch fp32: 500-doc chunks padded to their longest, "
-                               "einsum -> masked_fill(-inf) -> max -> sum (pytorch_maxsim_score), repeated")
+        nbytes = Dt.numel() * Dt.element_size()
+        base = _time_cpu_prefix(lambda b0, b1: tr.maxsim_varlen_masked(Qt, Dt, offs_t[b0:b1 + 1] , chunk=500), n,
+                                self.B, seconds, "query 0, torch fp32: 500-doc chunks padded to their longest, "
+                                "einsum -> masked_fill(-inf) -> max -> sum (pytorch_maxsim_score)", nbytes)
         offs = offs_t.numpy()
         Q, Dflat = Qt.numpy(), Dt.numpy()
-        base["numpy_port"] = _time_cpu(lambda: orc.maxsim_varlen(Q, Dflat, offs), n, seconds / 2,
-                                       f"first {n} docs x query 0, numpy fp32 per-token sims + segmented max, "
-                                       "repeated")
+        base["numpy_port"] = _time_cpu_prefix(lambda b0, b1: orc.maxsim_varlen(Q, Dflat, offs[b0:b1 + 1]), n,
+                                              self.B, seconds / 2,
+                                              "query 0, numpy fp32 per-token sims + segmented max", Dflat.nbytes,
+                                              torch_threads=False)
         return base
 
 
@@ -516,15 +520,19 @@ class Residual(Varlen):
 
     def cpu_baseline(self, seconds):
         from oracle import residual_oracle as ro
-        n = 2000
+        n = min(self.B, CPU_PREFIX_DOCS)
         offs = self.offsets[: n + 1].cpu().numpy()
         t = int(offs[-1])
         Q = self.Q[0].cpu().numpy()
         codes, res = self.codes[:t].cpu().numpy(), self.res[:t].cpu().numpy()
         C, w = self.centroids.cpu().numpy(), self.weights.cpu().numpy()
-        return _time_cpu(lambda: ro.maxsim_residual_f32(Q, codes, res, C, w, self.nbits, offs), n, seconds,
-                         f"first {n} docs x query 0, numpy decompress (restated codec) then fp32 varlen MaxSim, "
-                         "repeated")
+
+        def score(b0, b1):
+            t0, t1 = int(offs[b0]), int(offs[b1])
+            return ro.maxsim_residual_f32(Q, codes[t0:t1], res[t0:t1], C, w, self.nbits, offs[b0:b1 + 1] - t0)
+
+        return _time_cpu_prefix(score, n, self.B, seconds, "query 0, numpy decompress (restated codec) then fp32 "
+                                "varlen MaxSim", codes.nbytes + res.nbytes, torch_threads=False)
 
 
 class ResidualBatched(Residual):
@@ -658,14 +666,16 @@ class PQ:
     def cpu_baseline(self, seconds):
         from oracle import maxsim_oracle as orc
         from oracle import torch_ref as tr
-        n = 2000
+        n = min(self.B, 5 * CPU_PREFIX_DOCS)  # 205 MB of codes; each chunk decodes to 33 MB of fp32
         Qt, Ct, codes_t = self.Q[0].cpu(), self.codebook.cpu(), self.codes[:n].cpu()
-        base = _time_torch_cpu(lambda: tr.pq_decompress_score(Qt, Ct, codes_t, chunk=500), n, seconds,
-                               f"{n} docs x query 0, torch fp32 decompress per subspace then einsum -> max -> sum "
-                               "(pytorch_pqsim_baseline), 500-doc chunks, repeated")
+        nbytes = codes_t.numel()
+        base = _time_cpu_prefix(lambda b0, b1: tr.pq_decompress_score(Qt, Ct, codes_t[b0:b1], chunk=500), n, self.B,
+                                seconds, "query 0, torch fp32 decompress per subspace then einsum -> max -> sum "
+                                "(pytorch_pqsim_baseline)", nbytes)
         Q, C, codes = Qt.numpy(), Ct.numpy(), codes_t.numpy()
-        base["numpy_port"] = _time_cpu(lambda: orc.pq_decompress_score(Q, C, codes, chunk=500), n, seconds / 2,
-                                       f"{n} docs x query 0, numpy decompress-then-score, repeated")
+        base["numpy_port"] = _time_cpu_prefix(lambda b0, b1: orc.pq_decompress_score(Q, C, codes[b0:b1], chunk=500),
+                                              n, self.B, seconds / 2, "query 0, numpy decompress-then-score",
+                                              nbytes, torch_threads=False)
         return base
 
 
@@ -941,6 +951,51 @@ def _cpu_model():
     except OSError:
         pass
     return platform.processor() or platform.machine()
+
+
+CPU_PREFIX_DOCS = 20_000  # documents in a dense CPU-baseline prefix (0.9 GB at C2: far above any host LLC)
+
+
+def _time_cpu_prefix(score_chunk, n_docs, total_docs, seconds, sample, prefix_bytes, torch_threads=True,
+                     chunk=500):
+    """Times ``score_chunk(b0, b1)`` over consecutive ``chunk``-document slices of a prefix
+    of ``n_docs`` documents, cycling through the prefix until ``seconds`` have passed, on
+    every host core. Each slice is scored once per pass and the prefix is larger than the
+    host's last-level cache, so every pass reads its documents from DRAM, as a full pass
+    over the corpus would; documents are independent, so the rate extrapolates linearly
+    to the full corpus (``extrapolated`` unless the prefix is the corpus)."""
+    import torch
+    threads = os.cpu_count() or 1
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    from threadpoolctl import threadpool_limits
+    try:
+        with threadpool_limits(limits=threads):
+            score_chunk(0, min(chunk, n_docs))  # warm-up
+            docs, passes, b0 = 0, 0, 0
+            t0 = time.perf_counter()
+            while True:
+                b1 = min(n_docs, b0 + chunk)
+                score_chunk(b0, b1)
+                docs += b1 - b0
+                b0 = b1
+                if b0 >= n_docs:
+                    b0, passes = 0, passes + 1
+                el = time.perf_counter() - t0
+                if el >= seconds and (passes >= 1 or el >= 4 * seconds):
+                    break
+        used = torch.get_num_threads()
+    finally:
+        torch.set_num_threads(prev)
+    out = {"value": docs / el, "unit": "docs/s (1 query)", "cores": used if torch_threads else threads,
+           "kind": "port", "extrapolated": n_docs < total_docs, "prefix_docs": n_docs,
+           "prefix_bytes": int(prefix_bytes), "corpus_docs": total_docs,
+           "os_cpu_count": os.cpu_count(), "cpu_model": _cpu_model(),
+           "sample": f"{sample}: {docs:,} documents ({passes} full passes over a {n_docs:,}-document prefix of "
+                     f"{prefix_bytes / 1e6:.0f} MB, {chunk} at a time) in {el:.1f} s"}
+    if torch_threads:
+        out.update({"impl": f"torch {torch.__version__} (CPU, fp32)", "torch_num_threads": used})
+    return out
 
 
 def _time_torch_cpu(fn, docs_per_call, seconds, sample):

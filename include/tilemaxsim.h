@@ -214,9 +214,14 @@ int64_t tms_topk_workspace_size(int64_t nrows, int64_t n, int64_t k);
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). The intermediate keys live in a fixed 32 MiB device
  * array of the library (TMS_TOPK_SCRATCH_BYTES; one copy per GPU, held until the process
- * ends), whose address is looked up on the first call on each device: the calling
- * thread's current device must be the one that holds the pointers and the stream. Sizes
- * whose tms_topk_workspace_size() exceeds that return TMS_ERR_UNSUPPORTED (split the rows
+ * ends). The array sits in a code object of its own, with no kernels: under HIP's
+ * deferred module loading (the ROCm default) a GPU reserves it at the first
+ * tms_topk_noalloc call there, and processes that only call tms_topk never do. That first
+ * call on each device loads the array and looks up its address, so it must not run under
+ * stream capture: make one call eagerly before capturing tms_topk_noalloc into a graph
+ * (later calls launch kernels only and capture like tms_topk). The calling thread's
+ * current device must be the one that holds the pointers and the stream. Sizes whose
+ * tms_topk_workspace_size() exceeds the array return TMS_ERR_UNSUPPORTED (split the rows
  * over several calls). Every call on one GPU shares its array: calls that overlap on
  * one GPU (different streams, or host threads, with no ordering between them) race, and
  * must be serialised by the caller. Results equal tms_topk's bit for bit.

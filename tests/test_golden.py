@@ -1,13 +1,16 @@
 """Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
 
 CPU: the oracle still reproduces every fixture (and the C restatement agrees).
-GPU: every HIP entry point reproduces the fixture scores to 1e-3 relative (+1e-3 absolute).
+GPU: every HIP entry point reproduces the fixture scores to 1e-3 relative (+1e-3 absolute)
+and, for the dense, variable-length, masked, packed and PQ fixtures, to the
+fp32-accumulation bar of ``accum_bar.py`` (on MaxSim(|Q|, |D|) of the fixture's inputs).
 """
 import os
 
 import numpy as np
 import pytest
 
+import accum_bar as bar
 from oracle import c_oracle
 from oracle import maxsim_oracle as orc
 from oracle import residual_oracle as ro
@@ -49,11 +52,13 @@ def test_fixtures_reproduce_on_cpu():
         np.testing.assert_allclose(got[fin], f[name][fin], rtol=1e-12)
 
 
-def _close(got, ref):
-    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
-    inf = np.isinf(ref)
-    assert np.array_equal(np.isinf(got), inf)
-    np.testing.assert_allclose(got[~inf], ref[~inf], rtol=1e-3, atol=1e-3)
+def _close(got, ref, lim=None, what=""):
+    bar.assert_scores(got, ref, lim, what)
+
+
+def _lim(fn, Q, X, *rest, **kw):
+    """The fp32-accumulation bar for a fixture's scores, from its inputs."""
+    return bar.with_bound(fn, Q, X, *rest, **kw)[1]
 
 
 @pytest.mark.gpu
@@ -63,20 +68,26 @@ def test_fixtures_on_gpu(cuda):
     g = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()
     for name in ("dense_d128.npz", "dense_d256.npz"):
         f = _load(name)
-        _close(tms.flash_maxsim_v2_multiquery(g(f["Q"]), g(f["D"])).cpu().numpy(), f["scores"])
+        _close(tms.flash_maxsim_v2_multiquery(g(f["Q"]), g(f["D"])).cpu().numpy(), f["scores"],
+               _lim(orc.maxsim_f64, f["Q"], f["D"]), name)
     f = _load("varlen_d64.npz")
-    _close(tms.flash_maxsim_multi_doc(g(f["Q"]), g(f["D_flat"]), g(f["offsets"])).cpu().numpy(), f["scores"])
+    _close(tms.flash_maxsim_multi_doc(g(f["Q"]), g(f["D_flat"]), g(f["offsets"])).cpu().numpy(), f["scores"],
+           _lim(orc.maxsim_varlen, f["Q"], f["D_flat"], f["offsets"], f64=True), "varlen_d64")
     f = _load("masked_d128.npz")
-    _close(tms.maxsim_score(g(f["Q"]), g(f["D"]), g(f["mask"])).cpu().numpy(), f["scores"])
+    _close(tms.maxsim_score(g(f["Q"]), g(f["D"]), g(f["mask"])).cpu().numpy(), f["scores"],
+           _lim(orc.maxsim_masked, f["Q"], f["D"], f["mask"], f64=True), "masked_d128")
     f = _load("pq_m16_k256.npz")
     pq = tms.TileMaxSimPQ(g(f["codebook"]))
+    lim = _lim(orc.pq_decompress_score, f["Q"], f["codebook"], f["codes"], f64=True)
     for method in ("mfma", "lut"):
-        _close(pq.score_batch(g(f["Q"]), g(f["codes"]), method=method).cpu().numpy(), f["scores"])
+        _close(pq.score_batch(g(f["Q"]), g(f["codes"]), method=method).cpu().numpy(), f["scores"], lim,
+               f"pq {method}")
     lut = pq.build_distance_table(g(f["Q"])).cpu().numpy()
     np.testing.assert_allclose(lut[:2], f["lut_q01"], rtol=1e-5, atol=1e-5)
     f = _load("packed_zeros_d128.npz")
     got = tms.flashmaxsim_score_packed(g(f["Q"]), g(f["D_packed"]), torch.from_numpy(f["lengths"]))
-    _close(got.cpu().numpy(), f["scores"])
+    _close(got.cpu().numpy(), f["scores"],
+           _lim(orc.maxsim_packed_zero_padded, f["Q"], f["D_packed"], f["lengths"]), "packed_zeros_d128")
     f = _load("residual_d128_nb2.npz")
     idx = (g(f["codes"]), g(f["residuals"]), g(f["centroids"]), g(f["bucket_weights"]), 2)
     dec = tms.decompress_residual(*idx).cpu().numpy()

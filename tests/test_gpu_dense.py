@@ -1,19 +1,22 @@
 """GPU parity of the dense / masked / variable-length MaxSim kernels against the CPU oracle.
 
-Bar: |score - oracle| <= 1e-3 relative (fp32 accumulation), and
-identical top-100 rankings except for swaps among scores within that tolerance.
+Bars: |score - oracle| <= 1e-3 relative (the north star's), and within the
+fp32-accumulation bar (d + Nq) * 2^-23 * MaxSim(|Q|, |D|) of ``accum_bar.py`` (the
+reference accumulates in fp32: ``tl.dot`` at ``src/flash_maxsim_v2.py:117``); top-100
+rankings identical except for swaps among scores within the 1e-3 tolerance.
 The oracle is the float64 restatement of ``pytorch_maxsim_naive``
 (``src/flash_maxsim_kernel.py:280-288``) on the same fp16/bf16 input values.
 """
 import numpy as np
 import pytest
 
+import accum_bar as bar
 from oracle import maxsim_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
-RTOL = 1e-3
-ATOL = 1e-3
+RTOL = bar.NORTH_STAR_RTOL
+ATOL = bar.NORTH_STAR_ATOL
 
 
 @pytest.fixture(autouse=True, params=["default", "small_batch", "streaming"])
@@ -49,15 +52,16 @@ def _to_gpu(x, torch_dtype=None):
     return t.cuda()
 
 
-def _assert_scores(got, ref, what=""):
-    got = np.asarray(got, dtype=np.float64)
-    ref = np.asarray(ref, dtype=np.float64)
-    assert got.shape == ref.shape, (what, got.shape, ref.shape)
-    inf_ref = np.isinf(ref)
-    assert np.array_equal(np.isinf(got), inf_ref), f"{what}: -inf pattern differs"
-    assert np.all(got[inf_ref] == ref[inf_ref]), f"{what}: infinite values differ"
-    fin = ~inf_ref
-    np.testing.assert_allclose(got[fin], ref[fin], rtol=RTOL, atol=ATOL, err_msg=what)
+def _oracle(fn, Q, X, *rest, what="", qsplit=None, **kw):
+    """(float64 oracle scores, what, the fp32-accumulation bar) for ``_assert_scores``."""
+    ref, lim = bar.with_bound(fn, Q, X, *rest, qsplit=qsplit, **kw)
+    return ref, what, lim
+
+
+def _assert_scores(got, ref, what="", lim=None):
+    """The 1e-3 bar, and the fp32-accumulation bar ``lim`` when the reference is the
+    float64 oracle (``bar.with_bound``); kernel-against-kernel checks pass no ``lim``."""
+    bar.assert_scores(got, ref, lim, what)
 
 
 # exp10 shape grid of the reference (src/run_all_experiments.py:617-626): (Nq, Nd, d, B)
@@ -74,7 +78,7 @@ def test_exp10_grid_unnormalised(cuda, Nq, Nd, d, B):
     Q = _randn(rng, (Nq, d))
     D = _randn(rng, (B, Nd, d))
     got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(D)).cpu().numpy()
-    _assert_scores(got, orc.maxsim_f64(Q, D), f"exp10 Nq={Nq} Nd={Nd} d={d} B={B}")
+    _assert_scores(got, *_oracle(orc.maxsim_f64, Q, D, what=f"exp10 Nq={Nq} Nd={Nd} d={d} B={B}"))
 
 
 EDGE = [
@@ -92,7 +96,7 @@ def test_dense_edge_shapes(cuda, Nq, Nd, d, B):
     Q = _randn(rng, (Nq, d), normalize=True)
     D = _randn(rng, (B, Nd, d), normalize=True)
     got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(D)).cpu().numpy()
-    _assert_scores(got, orc.maxsim_f64(Q, D), f"Nq={Nq} Nd={Nd} d={d} B={B}")
+    _assert_scores(got, *_oracle(orc.maxsim_f64, Q, D, what=f"Nq={Nq} Nd={Nd} d={d} B={B}"))
 
 
 @pytest.mark.parametrize("d", [100, 130, 6])
@@ -103,7 +107,7 @@ def test_dense_unaligned_width(cuda, d):
     Q = _randn(rng, (32, d))
     D = _randn(rng, (40, 37, d))
     got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(D)).cpu().numpy()
-    _assert_scores(got, orc.maxsim_f64(Q, D), f"d={d}")
+    _assert_scores(got, *_oracle(orc.maxsim_f64, Q, D, what=f"d={d}"))
 
 
 def test_dense_misaligned_pointer(cuda):
@@ -116,7 +120,7 @@ def test_dense_misaligned_pointer(cuda):
     Dg = _to_gpu(D)[1:].view(30, 20, 128)
     assert Dg.data_ptr() % 16 != 0
     got = flash_maxsim_v2_multiquery(_to_gpu(Q), Dg).cpu().numpy()
-    _assert_scores(got, orc.maxsim_f64(Q, D[1:].reshape(30, 20, 128)), "misaligned")
+    _assert_scores(got, *_oracle(orc.maxsim_f64, Q, D[1:].reshape(30, 20, 128), what="misaligned"))
 
 
 def test_empty_documents_and_batch(cuda):
@@ -142,11 +146,11 @@ def test_bf16_and_fp32_query(cuda):
     Qb = torch.from_numpy(Q).to(torch.bfloat16)
     Db = torch.from_numpy(D).to(torch.bfloat16)
     got = flash_maxsim_v2_multiquery(Qb.cuda(), Db.cuda()).cpu().numpy()
-    _assert_scores(got, orc.maxsim_f64(Qb.float().numpy(), Db.float().numpy()), "bf16")
+    _assert_scores(got, *_oracle(orc.maxsim_f64, Qb.float().numpy(), Db.float().numpy(), what="bf16"))
     # fp32 queries against fp16 documents are scored unrounded (split into two fp16 terms)
     Dh = D.astype(np.float16)
     got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(Dh)).cpu().numpy()
-    _assert_scores(got, orc.maxsim_f64(Q, Dh), "fp32 Q")
+    _assert_scores(got, *_oracle(orc.maxsim_f64, Q, Dh, what="fp32 Q", qsplit="fp16"))
 
 
 def test_c1_ranking_parity(cuda):
@@ -157,8 +161,8 @@ def test_c1_ranking_parity(cuda):
     Q = _randn(rng, (32, 128), normalize=True)
     D = _randn(rng, (1000, 128, 128), normalize=True)
     got = flash_maxsim_v2_multiquery(_to_gpu(Q), _to_gpu(D)).cpu().numpy()
-    ref = orc.maxsim_f64(Q, D)
-    _assert_scores(got, ref, "C1")
+    ref, lim = bar.with_bound(orc.maxsim_f64, Q, D)
+    _assert_scores(got, ref, "C1", lim)
     _assert_topk_equal(got, ref, 100)
 
 
@@ -205,8 +209,8 @@ def test_scores_do_not_depend_on_the_batch(cuda, nq, Nd, d, dtype, B):
     for b in (1000, 300, 37):
         small = flash_maxsim_v2_multiquery(Q, D[:b].contiguous()).cpu().numpy()
         assert np.array_equal(small.view(np.uint32), big[:b].view(np.uint32)), f"B={b}"
-    _assert_scores(big[:37], orc.maxsim_f64(Q.float().cpu().numpy(), D[:37].float().cpu().numpy()),
-                   "first 37 documents")
+    _assert_scores(big[:37], *_oracle(orc.maxsim_f64, Q.float().cpu().numpy(), D[:37].float().cpu().numpy(),
+                                      what="first 37 documents"))
 
 
 def test_single_and_batch_entry_points(cuda):
@@ -214,12 +218,12 @@ def test_single_and_batch_entry_points(cuda):
     rng = _rng(21)
     Q = _randn(rng, (32, 128))
     D = _randn(rng, (16, 128, 128))
-    ref = orc.maxsim_f64(Q, D)
-    _assert_scores(flash_maxsim_batch(_to_gpu(Q), _to_gpu(D)).cpu().numpy(), ref, "batch")
-    _assert_scores(flash_maxsim_v2(_to_gpu(Q), _to_gpu(D)).cpu().numpy(), ref, "v2")
+    ref, lim = bar.with_bound(orc.maxsim_f64, Q, D)
+    _assert_scores(flash_maxsim_batch(_to_gpu(Q), _to_gpu(D)).cpu().numpy(), ref, "batch", lim)
+    _assert_scores(flash_maxsim_v2(_to_gpu(Q), _to_gpu(D)).cpu().numpy(), ref, "v2", lim)
     s = flash_maxsim_single(_to_gpu(Q), _to_gpu(D[3]))
     assert s.dim() == 0
-    _assert_scores(np.array([s.item()]), ref[3:4], "single")
+    _assert_scores(np.array([s.item()]), ref[3:4], "single", lim[3:4])
 
 
 @pytest.mark.parametrize("dist", ["uniform", "with_empty"])
@@ -239,7 +243,7 @@ def test_varlen(cuda, dist):
     Q = _randn(rng, (32, 128), normalize=True)
     Dflat = _randn(rng, (T, 128), normalize=True)
     got = flash_maxsim_multi_doc(_to_gpu(Q), _to_gpu(Dflat), torch.from_numpy(offsets)).cpu().numpy()
-    _assert_scores(got, orc.maxsim_varlen(Q, Dflat, offsets, f64=True), f"varlen {dist}")
+    _assert_scores(got, *_oracle(orc.maxsim_varlen, Q, Dflat, offsets, f64=True, what=f"varlen {dist}"))
 
 
 def test_varlen_equals_fixed(cuda):
@@ -288,7 +292,8 @@ def test_varlen_batched(cuda, nQ, nq):
     got = flash_maxsim_multi_doc_batched(_to_gpu(Qs), _to_gpu(Dflat), torch.from_numpy(offsets)).cpu().numpy()
     assert got.shape == (nQ, B)
     for q in range(nQ):
-        _assert_scores(got[q], orc.maxsim_varlen(Qs[q], Dflat, offsets, f64=True), f"varlen batched q={q}")
+        _assert_scores(got[q], *_oracle(orc.maxsim_varlen, Qs[q], Dflat, offsets, f64=True,
+                                        what=f"varlen batched q={q}"))
     one = flash_maxsim_multi_doc(_to_gpu(Qs[-1]), _to_gpu(Dflat), torch.from_numpy(offsets)).cpu().numpy()
     _assert_scores(got[-1], one, "batched vs one query")
 
@@ -310,7 +315,8 @@ def test_varlen_batched_widths_bf16_and_invalid(cuda, d):
         got = flash_maxsim_multi_doc_batched(_to_gpu(Qs), D, torch.from_numpy(offsets)).cpu().numpy()
         Dr = D.float().cpu().numpy()
         for q in range(9):  # fp32 queries are scored unrounded against 16-bit documents
-            _assert_scores(got[q], orc.maxsim_varlen(Qs[q], Dr, offsets, f64=True), f"d={d} {dt} q={q}")
+            _assert_scores(got[q], *_oracle(orc.maxsim_varlen, Qs[q], Dr, offsets, f64=True, what=f"d={d} {dt} q={q}",
+                                            qsplit="bf16" if dt == torch.bfloat16 else None))
     bad = offsets.copy()
     bad[10] = bad[11] + 5  # document 9 ends after document 10 starts, document 10 is reversed
     got = flash_maxsim_multi_doc_batched(_to_gpu(Qs), _to_gpu(Dflat), torch.from_numpy(bad),
@@ -335,10 +341,10 @@ def test_packed_batched_both_paddings(cuda):
         offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
         for q in (0, 11, 19):
             if padding == "zeros":
-                ref = orc.maxsim_packed_zero_padded(Qs[q], Dp, lens)
+                ref, lim = bar.with_bound(orc.maxsim_packed_zero_padded, Qs[q], Dp, lens)
             else:
-                ref = orc.maxsim_varlen(Qs[q], Dp, offsets, f64=True)
-            _assert_scores(got[q], ref, f"packed batched {padding} q={q}")
+                ref, lim = bar.with_bound(orc.maxsim_varlen, Qs[q], Dp, offsets, f64=True)
+            _assert_scores(got[q], ref, f"packed batched {padding} q={q}", lim)
             one = flashmaxsim_score_packed(_to_gpu(Qs[q][None]), _to_gpu(Dp), torch.from_numpy(lens),
                                            padding=padding).cpu().numpy()
             _assert_scores(got[q], one, "packed batched vs one query")
@@ -357,7 +363,7 @@ def test_masked(cuda):
     mask[1, :] = False
     mask[1, -1] = True
     got = maxsim_score(_to_gpu(Q), _to_gpu(D), torch.from_numpy(mask).cuda()).cpu().numpy()
-    _assert_scores(got, orc.maxsim_masked(Q, D, mask, f64=True), "masked")
+    _assert_scores(got, *_oracle(orc.maxsim_masked, Q, D, mask, f64=True, what="masked"))
 
 
 @pytest.mark.parametrize("padding", ["zeros", "mask"])
@@ -378,11 +384,11 @@ def test_plaid_packed_dropin(cuda, padding):
     got = flashmaxsim_score_packed(torch.from_numpy(Q).cuda(), _to_gpu(flat), torch.from_numpy(lens),
                                    config=None, padding=padding).cpu().numpy()
     if padding == "zeros":
-        ref = orc.maxsim_packed_zero_padded(Q[0], flat, lens)
+        ref, lim = bar.with_bound(orc.maxsim_packed_zero_padded, Q[0], flat, lens)
         assert got[5] == 0.0
     else:
-        ref = orc.maxsim_varlen(Q[0], flat, offsets, f64=True)
-    _assert_scores(got, ref, f"packed {padding}")
+        ref, lim = bar.with_bound(orc.maxsim_varlen, Q[0], flat, offsets, f64=True)
+    _assert_scores(got, ref, f"packed {padding}", lim)
 
 
 def test_batched_queries(cuda):
@@ -399,7 +405,44 @@ def test_batched_queries(cuda):
         D = _to_gpu(_randn(rng, (400, 60, 128), normalize=True))
         got = flash_maxsim_batched_queries(Qs, D).cpu().numpy()
         for i in range(nQ):
-            ref = orc.maxsim_f64(Qs[i].cpu().numpy(), D.cpu().numpy())
-            _assert_scores(got[i], ref, f"batched nQ={nQ} Nq={Nq} q={i}")
+            ref, lim = bar.with_bound(orc.maxsim_f64, Qs[i].cpu().numpy(), D.cpu().numpy())
+            _assert_scores(got[i], ref, f"batched nQ={nQ} Nq={Nq} q={i}", lim)
             single = flash_maxsim_v2_multiquery(Qs[i], D).cpu().numpy()
             _assert_scores(got[i], single, "batched vs single")
+
+
+class _RunConfig:
+    """The one field of ColBERT's run config the reference's drop-in reads."""
+
+    def __init__(self, total_visible_gpus):
+        self.total_visible_gpus = total_visible_gpus
+
+
+def test_plaid_packed_config_moves_host_tensors(cuda):
+    """``config.total_visible_gpus > 0`` moves host Q, D_packed and D_lengths to the GPU
+    before scoring, as the reference's drop-in does (``src/plaid_integration_benchmark.py:
+    159-161``); with no GPU in the config (or no config) host tensors are refused."""
+    import os
+
+    import torch
+    from tilemaxsim_amd import flashmaxsim_score_packed, flashmaxsim_score_packed_batched
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "packed_zeros_d128.npz"),
+                allow_pickle=False)
+    Q, Dp, lens = (torch.from_numpy(f[k]) for k in ("Q", "D_packed", "lengths"))
+    ref, lim = bar.with_bound(orc.maxsim_packed_zero_padded, f["Q"], f["D_packed"], f["lengths"])
+    np.testing.assert_allclose(ref, f["scores"], rtol=1e-12)
+    got = flashmaxsim_score_packed(Q[None], Dp, lens, _RunConfig(1))
+    assert got.device.type == "cuda"
+    _assert_scores(got.cpu().numpy(), f["scores"], "config, host tensors", lim)
+    got_b = flashmaxsim_score_packed_batched(torch.stack([Q, Q.flip(0)]), Dp, lens, _RunConfig(8))
+    _assert_scores(got_b[0].cpu().numpy(), f["scores"], "config, host tensors, batched", lim)
+    _assert_scores(got_b[1].cpu().numpy(), got.cpu().numpy(), "a query's token order does not matter")
+    got_m = flashmaxsim_score_packed(Q[None], Dp, lens, _RunConfig(1), padding="mask")
+    offsets = np.concatenate([[0], np.cumsum(f["lengths"])]).astype(np.int64)
+    _assert_scores(got_m.cpu().numpy(), *_oracle(orc.maxsim_varlen, f["Q"], f["D_packed"], offsets, f64=True,
+                                                 what="config, host tensors, mask"))
+    for config in (None, _RunConfig(0)):
+        with pytest.raises(ValueError, match="GPU"):
+            flashmaxsim_score_packed(Q[None], Dp, lens, config)
+        with pytest.raises(ValueError, match="GPU"):
+            flashmaxsim_score_packed_batched(Q[None], Dp, lens, config)

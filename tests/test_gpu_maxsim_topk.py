@@ -6,13 +6,15 @@ most 1,024 documents.
 Its scores, values and indices must be the bits of the two-call path
 (``flash_maxsim_v2_multiquery`` then ``topk``): the same per-tile MFMA sums, the same
 summation order over query tokens and the same selection code. The scores are also held
-to the float64 oracle (1e-3 relative + 1e-3 absolute) and the selection to the oracle's
-top-k (value descending, ties by lower index), bit for bit. Outputs start as sentinels
-(NaN values, index -1), so a result the last workgroup failed to write cannot pass.
+to the float64 oracle (1e-3 relative + 1e-3 absolute, and the fp32-accumulation bar of
+``accum_bar.py``) and the selection to the oracle's top-k (value descending, ties by
+lower index), bit for bit. Outputs start as sentinels (NaN values, index -1), so a
+result the last workgroup failed to write cannot pass.
 """
 import numpy as np
 import pytest
 
+import accum_bar as bar
 from oracle import maxsim_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -69,10 +71,7 @@ def _against_two_calls(Qg, Dg, k, fused, Q=None, D=None, what=""):
     assert np.array_equal(i.cpu().numpy(), ei), f"{what}: indices against the oracle's top-k"
     assert np.array_equal(v.cpu().numpy().view(np.uint32), ev.astype(np.float32).view(np.uint32)), what
     if Q is not None:
-        ref = orc.maxsim_f64(Q, D)
-        fin = np.isfinite(ref)
-        assert np.array_equal(np.isneginf(sn), np.isneginf(ref)), f"{what}: -inf pattern"
-        np.testing.assert_allclose(sn[fin], ref[fin], rtol=1e-3, atol=1e-3, err_msg=what)
+        bar.assert_scores(sn, *bar.with_bound(orc.maxsim_f64, Q, D), what)
 
 
 # (nq, nd, d, B, k): B sets the grid (one to 256 workgroups, the last one partly empty),

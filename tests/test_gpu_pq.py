@@ -2,17 +2,21 @@
 
 Oracles: the reference's decompress-then-score baseline ``pytorch_pqsim_baseline``
 (``src/flash_pqsim_kernel.py:283-313``) in float64, and the table-gather form
-(``:127-173``). Bar: |score - oracle| <= 1e-3 relative; identical top-100 up to ties.
+(``:127-173``). Bars: |score - oracle| <= 1e-3 relative, and the fp32-accumulation bar
+(d + Nq) * 2^-23 * MaxSim(|Q|, |decoded tokens|) of ``accum_bar.py`` against the float64
+oracle (the reference sums fp32 table entries, ``:154-167``, and the q-sum with
+``torch.sum``, ``:250``); identical top-100 up to ties.
 """
 import numpy as np
 import pytest
 
+import accum_bar as bar
 from oracle import maxsim_oracle as orc
 
 pytestmark = pytest.mark.gpu
 
-RTOL = 1e-3
-ATOL = 1e-3
+RTOL = bar.NORTH_STAR_RTOL
+ATOL = bar.NORTH_STAR_ATOL
 
 
 def _mk(seed, M, K, dsub, Nq, B, Nd, normalize_q=True, dtype=np.float16):
@@ -31,12 +35,14 @@ def _gpu(x):
     return torch.from_numpy(np.ascontiguousarray(x)).cuda()
 
 
-def _check(got, ref, what):
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    inf = np.isinf(ref)
-    assert np.array_equal(np.isinf(got), inf), what
-    np.testing.assert_allclose(got[~inf], ref[~inf], rtol=RTOL, atol=ATOL, err_msg=what)
+def _check(got, ref, what, lim=None):
+    """The 1e-3 bar, and the fp32-accumulation bar ``lim`` against the float64 oracle."""
+    bar.assert_scores(got, ref, lim, what)
+
+
+def _pq_oracle(Q, C, codes):
+    """Float64 decompress-then-score and its fp32-accumulation bar."""
+    return bar.with_bound(orc.pq_decompress_score, Q, C, codes, f64=True)
 
 
 @pytest.mark.parametrize("method", ["mfma", "lut"])
@@ -46,7 +52,8 @@ def test_reference_selftest_shape(cuda, method):
     Q, C, codes = _mk(42, 16, 256, 8, 32, 8, 128, normalize_q=False)
     pq = TileMaxSimPQ(_gpu(C))
     got = pq.score_batch(_gpu(Q), _gpu(codes), method=method).cpu().numpy()
-    _check(got, orc.pq_decompress_score(Q, C, codes, f64=True), f"selftest {method}")
+    ref, lim = _pq_oracle(Q, C, codes)
+    _check(got, ref, f"selftest {method}", lim)
     _check(got, orc.pq_score_lut(orc.pq_build_lut(Q, C), codes), f"selftest {method} vs lut oracle")
 
 
@@ -76,7 +83,8 @@ def test_pq_shapes(cuda, M, K, dsub, Nq, B, Nd, method):
     Q, C, codes = _mk(M * 1000 + K + dsub + Nq + B + Nd, M, K, dsub, Nq, B, Nd)
     pq = TileMaxSimPQ(_gpu(C))
     got = pq.score_batch(_gpu(Q), _gpu(codes), method=method).cpu().numpy()
-    _check(got, orc.pq_decompress_score(Q, C, codes, f64=True), f"M={M} K={K} dsub={dsub} Nq={Nq} {method}")
+    ref, lim = _pq_oracle(Q, C, codes)
+    _check(got, ref, f"M={M} K={K} dsub={dsub} Nq={Nq} {method}", lim)
 
 
 @pytest.mark.parametrize("M,dsub", [(16, 3), (40, 4), (10, 8), (48, 8)])
@@ -85,7 +93,8 @@ def test_pq_generic_shapes_take_lut_path(cuda, M, dsub):
     Q, C, codes = _mk(M + dsub, M, 64, dsub, 32, 50, 30)
     pq = TileMaxSimPQ(_gpu(C))
     got = pq.score_batch(_gpu(Q), _gpu(codes)).cpu().numpy()
-    _check(got, orc.pq_decompress_score(Q, C, codes, f64=True), f"generic M={M} dsub={dsub}")
+    ref, lim = _pq_oracle(Q, C, codes)
+    _check(got, ref, f"generic M={M} dsub={dsub}", lim)
 
 
 def test_pq_bf16_int_codes_and_single(cuda):
@@ -96,13 +105,13 @@ def test_pq_bf16_int_codes_and_single(cuda):
     Q = torch.from_numpy(rng.standard_normal((32, 128), dtype=np.float32)).to(torch.bfloat16)
     codes = rng.integers(0, 256, size=(30, 64, 16)).astype(np.int32)
     pq = TileMaxSimPQ(C.cuda())
-    ref = orc.pq_decompress_score(Q.float().numpy(), C.float().numpy(), codes, f64=True)
+    ref, lim = _pq_oracle(Q.float().numpy(), C.float().numpy(), codes)
     for method in ("mfma", "lut"):
         got = pq.score_batch(Q.cuda(), _gpu(codes), method=method).cpu().numpy()
-        _check(got, ref, f"bf16 {method}")
+        _check(got, ref, f"bf16 {method}", lim)
     s = pq.score_single(Q.cuda(), _gpu(codes[4].astype(np.uint8)))
     assert s.dim() == 0
-    _check(np.array([s.item()]), ref[4:5], "single")
+    _check(np.array([s.item()]), ref[4:5], "single", lim[4:5])
 
 
 def test_pq_empty_and_invalid(cuda):
@@ -130,9 +139,9 @@ def test_pq_methods_agree_and_rank(cuda):
     pq = TileMaxSimPQ(_gpu(C))
     a = pq.score_batch(_gpu(Q), _gpu(codes), method="mfma").cpu().numpy()
     b = pq.score_batch(_gpu(Q), _gpu(codes), method="lut").cpu().numpy()
-    ref = orc.pq_decompress_score(Q, C, codes, f64=True)
-    _check(a, ref, "mfma")
-    _check(b, ref, "lut")
+    ref, lim = _pq_oracle(Q, C, codes)
+    _check(a, ref, "mfma", lim)
+    _check(b, ref, "lut", lim)
     _check(a, b, "mfma vs lut")
     kth = np.sort(ref)[::-1][99]
     for got in (a, b):
@@ -154,7 +163,8 @@ def test_pq_batched_queries_formats(cuda, M, K, dsub):
     got = pq.score_batch_queries(_gpu(Qs), _gpu(codes)).cpu().numpy()
     assert got.shape == (6, 700)
     for q in range(6):
-        _check(got[q], orc.pq_decompress_score(Qs[q], C, codes, f64=True), f"M={M} K={K} dsub={dsub} q={q}")
+        ref, lim = _pq_oracle(Qs[q], C, codes)
+        _check(got[q], ref, f"M={M} K={K} dsub={dsub} q={q}", lim)
     one = pq.score_batch(_gpu(Qs[5]), _gpu(codes)).cpu().numpy()
     _check(got[5], one, "batched vs one query")
 
@@ -170,7 +180,8 @@ def test_pq_batched_queries_shapes(cuda, nQ, nq):
     Qs = (Qs / np.linalg.norm(Qs, axis=-1, keepdims=True)).astype(np.float16)
     got = TileMaxSimPQ(_gpu(C)).score_batch_queries(_gpu(Qs), _gpu(codes)).cpu().numpy()
     for q in range(nQ):
-        _check(got[q], orc.pq_decompress_score(Qs[q], C, codes, f64=True), f"nQ={nQ} nq={nq} q={q}")
+        ref, lim = _pq_oracle(Qs[q], C, codes)
+        _check(got[q], ref, f"nQ={nQ} nq={nq} q={q}", lim)
 
 
 def test_pq_batched_queries_edges(cuda):
@@ -186,14 +197,16 @@ def test_pq_batched_queries_edges(cuda):
         pq.score_batch_queries(_gpu(Qs), _gpu(bad))
     got = pq.score_batch_queries(_gpu(Qs), _gpu(bad), validate=False).cpu().numpy()
     for q in range(3):
-        _check(got[q], orc.pq_decompress_score(Qs[q], C, np.minimum(bad, 199), f64=True), f"clamped q={q}")
+        ref, lim = _pq_oracle(Qs[q], C, np.minimum(bad, 199))
+        _check(got[q], ref, f"clamped q={q}", lim)
     # bf16 codebook and queries
     pqb = TileMaxSimPQ(_gpu(C).to(torch.bfloat16))
     got = pqb.score_batch_queries(_gpu(Qs).to(torch.bfloat16), _gpu(codes)).cpu().numpy()
     Cb = _gpu(C).to(torch.bfloat16).float().cpu().numpy()
     Qb = _gpu(Qs).to(torch.bfloat16).float().cpu().numpy()
     for q in range(3):
-        _check(got[q], orc.pq_decompress_score(Qb[q], Cb, codes, f64=True), f"bf16 q={q}")
+        ref, lim = _pq_oracle(Qb[q], Cb, codes)
+        _check(got[q], ref, f"bf16 q={q}", lim)
     # no document tokens; no query tokens; no documents; no queries
     got = pq.score_batch_queries(_gpu(Qs), _gpu(codes[:, :0])).cpu().numpy()
     assert got.shape == (3, 300) and np.all(got == -np.inf)

@@ -14,15 +14,18 @@ Paths covered (the C entry point picks them from the shape):
   larger tables (slices tiled over m, per-token partial sums in registers), and K > 16384
   (gathered from the table in memory);
 * fp32 queries (split into two 16-bit terms on MFMA; an fp32 table on the table path).
+
+Bars: 1e-3 relative, and against the float64 oracle the fp32-accumulation bar of
+``accum_bar.py`` (16-bit queries) or the split-product bar of ``test_gpu_fp32.py``
+(fp32 queries).
 """
 import numpy as np
 import pytest
 
+import accum_bar as bar
 from oracle import maxsim_oracle as orc
 
 from test_gpu_fp32 import _assert_fp32_scores, _coherent
-
-RTOL = ATOL = 1e-3
 
 
 def _gpu(x):
@@ -30,12 +33,13 @@ def _gpu(x):
     return torch.from_numpy(np.ascontiguousarray(x)).cuda()
 
 
-def _check(got, ref, what):
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    inf = np.isinf(ref)
-    assert np.array_equal(np.isinf(got), inf), what
-    np.testing.assert_allclose(got[~inf], ref[~inf], rtol=RTOL, atol=ATOL, err_msg=what)
+def _check(got, ref, what, lim=None):
+    bar.assert_scores(got, ref, lim, what)
+
+
+def _pq_oracle(Q, C, codes):
+    """Float64 decompress-then-score and its fp32-accumulation bar."""
+    return bar.with_bound(orc.pq_decompress_score, Q, C, codes, f64=True)
 
 
 def _mk(seed, M, K, dsub, Nq, B, Nd, code_dtype):
@@ -71,10 +75,10 @@ def test_pq_wide_codes_and_large_tables(cuda, M, K, dsub, cdt, methods):
     from tilemaxsim_amd import TileMaxSimPQ
     Q, C, codes = _mk(M * 7 + K + dsub, M, K, dsub, 32, 90, 41, cdt)
     pq = TileMaxSimPQ(_gpu(C))
-    ref = orc.pq_decompress_score(Q, C, codes, f64=True)
+    ref, lim = _pq_oracle(Q, C, codes)
     for method in methods:
         got = pq.score_batch(_gpu(Q), _gpu(codes), method=method).cpu().numpy()
-        _check(got, ref, f"M={M} K={K} dsub={dsub} {np.dtype(cdt).name} {method}")
+        _check(got, ref, f"M={M} K={K} dsub={dsub} {np.dtype(cdt).name} {method}", lim)
     # the reference algorithm's own sum order (table gather, ascending m)
     _check(pq.score_batch(_gpu(Q), _gpu(codes), method="lut").cpu().numpy(),
            orc.pq_score_lut(orc.pq_build_lut(Q, C), codes), "lut vs table oracle")
@@ -92,7 +96,8 @@ def test_pq_mtile_ragged_shapes(cuda, M, K, dsub):
         Q, C, codes = _mk(Nq + B + Nd, M, K, dsub, Nq, B, Nd, np.int32)
         pq = TileMaxSimPQ(_gpu(C))
         got = pq.score_batch(_gpu(Q), _gpu(codes)).cpu().numpy()
-        _check(got, orc.pq_decompress_score(Q, C, codes, f64=True), f"M={M} Nq={Nq} B={B} Nd={Nd}")
+        ref, lim = _pq_oracle(Q, C, codes)
+        _check(got, ref, f"M={M} Nq={Nq} B={B} Nd={Nd}", lim)
     empty = pq.score_batch(_gpu(Q), torch.zeros(4, 0, M, dtype=torch.int32, device="cuda")).cpu().numpy()
     assert np.all(np.isneginf(empty))
     bad = codes.copy()
@@ -102,7 +107,8 @@ def test_pq_mtile_ragged_shapes(cuda, M, K, dsub):
         pq.score_batch(_gpu(Q), _gpu(bad))
     got = pq.score_batch(_gpu(Q), _gpu(bad), validate=False).cpu().numpy()
     clamped = np.where((bad < 0) | (bad >= K), K - 1, bad)  # negative int32 codes read as large unsigned
-    _check(got, orc.pq_decompress_score(Q, C, clamped, f64=True), "clamped")
+    ref, lim = _pq_oracle(Q, C, clamped)
+    _check(got, ref, "clamped", lim)
 
 
 @pytest.mark.gpu
@@ -116,9 +122,11 @@ def test_pq_wide_batched_queries_and_int64(cuda):
     pq = TileMaxSimPQ(_gpu(C))
     got = pq.score_batch_queries(_gpu(Qs), _gpu(codes)).cpu().numpy()
     for q in range(4):
-        _check(got[q], orc.pq_decompress_score(Qs[q], C, codes, f64=True), f"batched int32 K=512 q={q}")
+        ref, lim = _pq_oracle(Qs[q], C, codes)
+        _check(got[q], ref, f"batched int32 K=512 q={q}", lim)
     got = pq.score_batch(_gpu(Q), _gpu(codes.astype(np.int64))).cpu().numpy()
-    _check(got, orc.pq_decompress_score(Q, C, codes, f64=True), "int64 codes")
+    ref, lim = _pq_oracle(Q, C, codes)
+    _check(got, ref, "int64 codes", lim)
 
 
 @pytest.mark.gpu

@@ -4,15 +4,16 @@ Each case draws (from its own seed) the number of query tokens, documents, docum
 lengths (fixed, or ragged with empty documents), the embedding width (aligned widths
 that take the register paths, widths that take the LDS path, and widths that are not
 a multiple of 8), the dtype, whether the embeddings are L2-normalised, and the entry
-point. The bar is the one of the other parity tests: 1e-3 relative (+1e-3 absolute)
-for fp16 / bf16 inputs scored against the oracle on the same rounded values, and the
-split-product bound of ``test_gpu_fp32.py`` for fp32 inputs (and for fp32 queries against
-fp16 / bf16 documents, which are split, not rounded); -inf exactly where the
-oracle has it.
+point. The bars are those of the other parity tests: for fp16 / bf16 inputs scored
+against the oracle on the same rounded values, 1e-3 relative (+1e-3 absolute) and the
+fp32-accumulation bar of ``accum_bar.py``; for fp32 inputs (and for fp32 queries against
+fp16 / bf16 documents, which are split, not rounded) the split-product bound of
+``test_gpu_fp32.py``; -inf exactly where the oracle has it.
 """
 import numpy as np
 import pytest
 
+import accum_bar as bar
 from oracle import maxsim_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -47,7 +48,10 @@ def _round(x, dtype):
     return t, t.float().numpy()
 
 
-def _check(got, ref, absref, dtype, d, what):
+def _check(got, ref, absref, dtype, d, what, nq=None):
+    """fp32 embeddings: the split-product bar. 16-bit embeddings (and PQ, whose table
+    path rounds fp32 products): 1e-3 relative and the fp32-accumulation bar for ``nq``
+    query tokens."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     inf = np.isinf(ref)
@@ -58,7 +62,7 @@ def _check(got, ref, absref, dtype, d, what):
         lim = (4 * 2.0 ** -16 + d * 2.0 ** -24) * np.asarray(absref, np.float64)[fin] + 1e-6
         assert np.all(np.abs(got[fin] - ref[fin]) <= lim), what
     else:
-        np.testing.assert_allclose(got[fin], ref[fin], rtol=1e-3, atol=1e-3, err_msg=what)
+        bar.assert_scores(got, ref, bar.bound(absref, d, nq), what)
 
 
 def _emb(rng, shape, norm):
@@ -90,19 +94,19 @@ def _random_case(seed):
         D_t, D = _round(_emb(rng, (B, nd, d), c["norm"]), dt)
         if entry == "dense":
             got = tms.flash_maxsim_v2_multiquery(Q_t.to(dev), D_t.to(dev)).cpu().numpy()
-            _check(got, orc.maxsim_f64(Q, D), orc.maxsim_f64(np.abs(Q), np.abs(D)), dt, d, what)
+            _check(got, orc.maxsim_f64(Q, D), orc.maxsim_f64(np.abs(Q), np.abs(D)), dt, d, what, nq)
         elif entry == "masked":
             mask = rng.random((B, nd)) < 0.7
             mask[0] = False  # a fully masked document scores -inf
             got = tms.maxsim_score(Q_t.to(dev), D_t.to(dev), torch.from_numpy(mask).to(dev)).cpu().numpy()
             _check(got, orc.maxsim_masked(Q, D, mask, f64=True),
-                   orc.maxsim_masked(np.abs(Q), np.abs(D), mask, f64=True), dt, d, what)
+                   orc.maxsim_masked(np.abs(Q), np.abs(D), mask, f64=True), dt, d, what, nq)
         else:
             Qs_t, Qs = _round(_emb(rng, (c["nQ"], nq, d), c["norm"]), dt)
             got = tms.flash_maxsim_batched_queries(Qs_t.to(dev), D_t.to(dev)).cpu().numpy()
             for q in range(c["nQ"]):
                 _check(got[q], orc.maxsim_f64(Qs[q], D), orc.maxsim_f64(np.abs(Qs[q]), np.abs(D)), dt, d,
-                       f"{what} q={q}")
+                       f"{what} q={q}", nq)
         return
     lens = rng.integers(0, nd + 1, B)
     lens[rng.random(B) < 0.1] = 0
@@ -113,19 +117,20 @@ def _random_case(seed):
     if entry == "varlen":
         got = tms.flash_maxsim_multi_doc(Q_t.to(dev), Df_t.to(dev), off_t).cpu().numpy()
         _check(got, orc.maxsim_varlen(Q, Df, offsets, f64=True),
-               orc.maxsim_varlen(np.abs(Q), np.abs(Df), offsets, f64=True), dt, d, what)
+               orc.maxsim_varlen(np.abs(Q), np.abs(Df), offsets, f64=True), dt, d, what, nq)
     elif entry == "batched_varlen":
         Qs_t, Qs = _round(_emb(rng, (c["nQ"], nq, d), c["norm"]), dt)
         got = tms.flash_maxsim_multi_doc_batched(Qs_t.to(dev), Df_t.to(dev), off_t).cpu().numpy()
         for q in range(c["nQ"]):
             _check(got[q], orc.maxsim_varlen(Qs[q], Df, offsets, f64=True),
-                   orc.maxsim_varlen(np.abs(Qs[q]), np.abs(Df), offsets, f64=True), dt, d, f"{what} q={q}")
+                   orc.maxsim_varlen(np.abs(Qs[q]), np.abs(Df), offsets, f64=True), dt, d, f"{what} q={q}", nq)
     else:  # PLAID packed, zero padding: scores the fp16 copies, as the reference does
         Qh = torch.from_numpy(Q).half()
         Dh = torch.from_numpy(Df).half()
         got = tms.flashmaxsim_score_packed(Q_t.to(dev), Df_t.to(dev), torch.from_numpy(lens).to(dev)).cpu().numpy()
-        ref = orc.maxsim_packed_zero_padded(Qh.float().numpy(), Dh.float().numpy()[:T], lens)
-        _check(got, ref, None, "fp16", d, what)
+        Qx, Dx = Qh.float().numpy(), Dh.float().numpy()[:T]
+        ref = orc.maxsim_packed_zero_padded(Qx, Dx, lens)
+        _check(got, ref, orc.maxsim_packed_zero_padded(np.abs(Qx), np.abs(Dx), lens), "fp16", d, what, nq)
 
 
 @pytest.mark.parametrize("seed", range(60))
@@ -188,7 +193,9 @@ def test_random_pq_case(cuda, seed):
     dev = torch.device("cuda")
     pq = TileMaxSimPQ(C_t.to(dev))
     ref = orc.pq_decompress_score(Q, C, codes, f64=True)
+    absref = orc.pq_decompress_score(np.abs(Q), np.abs(C), codes, f64=True)
     for method in ("auto", "lut"):
         got = pq.score_batch(Q_t.to(dev), torch.from_numpy(codes).to(dev), method=method).cpu().numpy()
-        # the table path rounds each table entry to fp32 and sums M of them per token
-        _check(got, ref, None, "fp16", M * dsub, f"{what} {method}")
+        # the table path rounds each fp32 product and table entry and sums M entries per
+        # token: within the same (d + Nq) operations' bar as the MFMA path
+        _check(got, ref, absref, "pq", M * dsub, f"{what} {method}", nq)

@@ -6,11 +6,13 @@ once with the small-batch kernel forced on (``tms_set_rerank_limit`` above the c
 tiles) and once forced off (limit 0: the streaming kernels). Both must give the same
 bits (the kernels form the same per-tile MFMA sums, maxima are exact, and both sum
 over query tokens in the same order), and both must match the float64 oracle within
-1e-3 relative (+1e-3 absolute), with -inf and NaN exactly where the oracle has them.
+1e-3 relative (+1e-3 absolute) and within the fp32-accumulation bar of ``accum_bar.py``,
+with -inf and NaN exactly where the oracle has them.
 """
 import numpy as np
 import pytest
 
+import accum_bar as bar
 from oracle import maxsim_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -44,17 +46,19 @@ def _both(fn):
     return small
 
 
-def _check(got, ref, what):
+def _check(got, ref, what, lim=None):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape, what
     nan = np.isnan(ref)
     assert np.array_equal(np.isnan(got), nan), f"{what}: NaN pattern"
-    inf = np.isinf(ref)
-    assert np.array_equal(np.isinf(got), inf), f"{what}: -inf pattern"
-    assert np.all(got[inf] == ref[inf]), what
-    fin = ~(inf | nan)
-    np.testing.assert_allclose(got[fin], ref[fin], rtol=1e-3, atol=1e-3, err_msg=what)
+    keep = ~nan
+    bar.assert_scores(got[keep], ref[keep], None if lim is None else np.broadcast_to(lim, ref.shape)[keep], what)
+
+
+def _oracle(fn, Q, X, *rest, **kw):
+    """(float64 oracle scores, their fp32-accumulation bar)."""
+    return bar.with_bound(fn, Q, X, *rest, **kw)
 
 
 # (nq, nd, d, B): nd sets the waves per document (1-3 tiles: 1 wave; 4-7: 2; >= 8: 4), B
@@ -76,7 +80,8 @@ def test_fixed(cuda, nq, nd, d, B, dt):
     Dt, D = _rounded(_emb(rng, (B, nd, d)), dt)
     Qg, Dg = Qt.cuda(), Dt.cuda()
     got = _both(lambda: tms.flash_maxsim_v2_multiquery(Qg, Dg))
-    _check(got, orc.maxsim_f64(Q, D), f"fixed nq={nq} nd={nd} d={d} B={B} {dt}")
+    ref, lim = _oracle(orc.maxsim_f64, Q, D)
+    _check(got, ref, f"fixed nq={nq} nd={nd} d={d} B={B} {dt}", lim)
 
 
 @pytest.mark.parametrize("nq,nd,d,B,mdt,shift", [
@@ -111,7 +116,8 @@ def test_masked(cuda, nq, nd, d, B, mdt, shift):
         mg = m.cuda()
     Qg, Dg = Qt.cuda(), Dt.cuda()
     got = _both(lambda: tms.maxsim_score(Qg, Dg, mg))
-    _check(got, orc.maxsim_masked(Q, D, mask, f64=True), f"masked nq={nq} nd={nd} d={d} B={B} {mdt}")
+    ref, lim = _oracle(orc.maxsim_masked, Q, D, mask, f64=True)
+    _check(got, ref, f"masked nq={nq} nd={nd} d={d} B={B} {mdt}", lim)
 
 
 @pytest.mark.parametrize("nq,d,B,maxlen", [(32, 128, 300, 300), (32, 64, 41, 20), (70, 128, 23, 200),
@@ -129,14 +135,15 @@ def test_varlen(cuda, nq, d, B, maxlen):
     Dt, D = _rounded(_emb(rng, (max(T, 1), d)), "bf16")
     Qg, Dg, og = Qt.cuda(), Dt.cuda(), torch.from_numpy(offsets).cuda()
     got = _both(lambda: tms.flash_maxsim_multi_doc(Qg, Dg, og))
-    _check(got, orc.maxsim_varlen(Q, D, offsets, f64=True), f"varlen nq={nq} d={d} B={B}")
+    ref, lim = _oracle(orc.maxsim_varlen, Q, D, offsets, f64=True)
+    _check(got, ref, f"varlen nq={nq} d={d} B={B}", lim)
     # PLAID's zero-padding semantics: documents shorter than the longest score max(., 0)
     Ql = torch.from_numpy(Q).half()
     Dl = torch.from_numpy(D).half()
     lg = torch.from_numpy(lens).cuda()
     got = _both(lambda: tms.flashmaxsim_score_packed(Ql.cuda(), Dl.cuda(), lg))
-    _check(got, orc.maxsim_packed_zero_padded(Ql.float().numpy(), Dl.float().numpy()[:T], lens),
-           f"packed zeros nq={nq} d={d} B={B}")
+    ref, lim = _oracle(orc.maxsim_packed_zero_padded, Ql.float().numpy(), Dl.float().numpy()[:T], lens)
+    _check(got, ref, f"packed zeros nq={nq} d={d} B={B}", lim)
 
 
 def test_varlen_invalid_offsets_score_nan(cuda):
@@ -153,8 +160,8 @@ def test_varlen_invalid_offsets_score_nan(cuda):
     assert np.isneginf(got[[3, 7]]).all()
     Qn, Dn = Q.float().cpu().numpy(), D.float().cpu().numpy()
     for b in (0, 2, 6):
-        ref = orc.maxsim_f64(Qn, Dn[offs[b]:offs[b + 1]][None])
-        _check(got[b:b + 1], ref, f"valid document {b} beside invalid ones")
+        ref, lim = _oracle(orc.maxsim_f64, Qn, Dn[offs[b]:offs[b + 1]][None])
+        _check(got[b:b + 1], ref, f"valid document {b} beside invalid ones", lim)
 
 
 @pytest.mark.parametrize("nQ,nq", [(2, 32), (3, 32), (1, 96), (1, 40)])
@@ -168,12 +175,13 @@ def test_batched_entry_points_with_few_blocks(cuda, nQ, nq):
     Dt, D = _rounded(_emb(rng, (120, 150, 128)), "fp16")
     Qg, Dg = Qt.cuda(), Dt.cuda()
     got = _both(lambda: tms.flash_maxsim_batched_queries(Qg, Dg))
+    refs = [_oracle(orc.maxsim_f64, Q[q], D) for q in range(nQ)]
     for q in range(nQ):
-        _check(got[q], orc.maxsim_f64(Q[q], D), f"dense batched q={q}")
+        _check(got[q], refs[q][0], f"dense batched q={q}", refs[q][1])
     offs = torch.arange(0, 121 * 150, 150, dtype=torch.int64).cuda()
     got = _both(lambda: tms.flash_maxsim_multi_doc_batched(Qg, Dg.view(-1, 128), offs))
     for q in range(nQ):
-        _check(got[q], orc.maxsim_f64(Q[q], D), f"varlen batched q={q}")
+        _check(got[q], refs[q][0], f"varlen batched q={q}", refs[q][1])
 
 
 def test_default_limit_takes_the_small_kernel_for_c1_and_not_for_large_calls(cuda):

@@ -8,18 +8,35 @@ oracles, computed on the CPU:
 * ``pytorch_pqsim_baseline`` (``src/flash_pqsim_kernel.py:283-313``): decompress the codes
   through the codebook to fp32, then the same MaxSim.
 
-Bar: |score - reference| <= 1e-3 relative (+1e-3 absolute), and top-100 lists equal
-except for swaps among scores within that tolerance of the 100th. The float64 numpy
-oracle (``oracle/``) is the primary checker; this file pins the same kernels to the
-reference's own arithmetic (fp32 products and sums in torch's order).
+Bars: |score - reference| <= 1e-3 relative (+1e-3 absolute); for 16-bit inputs also the
+fp32-accumulation bar of ``accum_bar.py`` with the fp32 restatement's own error added
+(``restated=True``); and top-100 lists equal except for swaps among scores within the
+1e-3 tolerance of the 100th. The float64 numpy oracle (``oracle/``) is the primary
+checker; this file pins the same kernels to the reference's own arithmetic (fp32
+products and sums in torch's order).
 """
 import numpy as np
 import pytest
 
+import accum_bar as bar
+
 pytestmark = pytest.mark.gpu
 
-RTOL = 1e-3
-ATOL = 1e-3
+RTOL = bar.NORTH_STAR_RTOL
+ATOL = bar.NORTH_STAR_ATOL
+
+
+def _close(got, ref, lim=None, what=""):
+    """The 1e-3 bar (torch's check), and the accumulation bar ``lim`` when given."""
+    import torch
+    torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
+    bar.assert_scores(got.numpy(), ref.numpy(), lim, what)
+
+
+def _lim(fn, Q, X, *rest):
+    """The accumulation bar against an fp32 restatement: ``fn`` on |Q| and |X|."""
+    absref = fn(Q.abs(), X.abs(), *rest).double().numpy()
+    return bar.bound(absref, Q.shape[-1], Q.shape[-2], restated=True)
 
 
 def _naive(Q, D):
@@ -64,7 +81,7 @@ def test_dense_vs_torch_naive(cuda, nq, d, nd):
     Q, D = _normed(g, (nq, d)), _normed(g, (600, nd, d))
     got = flash_maxsim_v2_multiquery(Q.cuda(), D.cuda()).cpu()
     ref = _naive(Q, D)
-    torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
+    _close(got, ref, _lim(_naive, Q, D), f"nq={nq} d={d} nd={nd}")
     _check_topk(got, ref)
 
 
@@ -77,13 +94,14 @@ def test_varlen_and_masked_vs_torch(cuda):
     Q, D = _normed(g, (32, d)), _normed(g, (B, Nmax, d))
     mask = torch.arange(Nmax)[None, :] < lens[:, None]
     ref = _masked(Q, D, mask)
+    lim = _lim(_masked, Q, D, mask)
     got = maxsim_score(Q.cuda(), D.cuda(), mask.cuda()).cpu()
-    torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
+    _close(got, ref, lim, "masked")
     flat = torch.cat([D[b, : lens[b]] for b in range(B)])
     offsets = torch.zeros(B + 1, dtype=torch.int64)
     offsets[1:] = torch.cumsum(lens, 0)
     got_v = flash_maxsim_multi_doc(Q.cuda(), flat.cuda(), offsets).cpu()
-    torch.testing.assert_close(got_v, ref, rtol=RTOL, atol=ATOL)
+    _close(got_v, ref, lim, "varlen")
     _check_topk(got_v, ref)
 
 
@@ -97,14 +115,15 @@ def test_pq_vs_torch_baseline(cuda, M, dsub):
     codes = torch.randint(0, K, (B, Nd, M), generator=g, dtype=torch.int64).to(torch.uint8)
     Q = _normed(g, (32, M * dsub))
     ref = _pq_baseline(Q, C, codes)
+    lim = _lim(_pq_baseline, Q, C, codes)
     pq = TileMaxSimPQ(C.cuda())
     for method in ("auto", "lut"):
         got = pq.score_batch(Q.cuda(), codes.cuda(), method=method).cpu()
-        torch.testing.assert_close(got, ref, rtol=RTOL, atol=ATOL)
+        _close(got, ref, lim, f"pq {method}")
     Qs = torch.stack([Q, _normed(g, (32, M * dsub))])
     got_b = pq.score_batch_queries(Qs.cuda(), codes.cuda()).cpu()
-    torch.testing.assert_close(got_b[0], ref, rtol=RTOL, atol=ATOL)
-    torch.testing.assert_close(got_b[1], _pq_baseline(Qs[1], C, codes), rtol=RTOL, atol=ATOL)
+    _close(got_b[0], ref, lim, "pq batched q=0")
+    _close(got_b[1], _pq_baseline(Qs[1], C, codes), _lim(_pq_baseline, Qs[1], C, codes), "pq batched q=1")
     _check_topk(got_b[0], ref)
 
 
@@ -116,7 +135,7 @@ def test_batched_queries_vs_torch_naive(cuda):
     got = flash_maxsim_batched_queries(Qs.cuda(), D.cuda()).cpu()
     for q in range(6):
         ref = _naive(Qs[q], D)
-        torch.testing.assert_close(got[q], ref, rtol=RTOL, atol=ATOL)
+        _close(got[q], ref, _lim(_naive, Qs[q], D), f"batched q={q}")
         _check_topk(got[q], ref)
 
 

@@ -31,6 +31,44 @@ def test_library_exports_every_declared_symbol():
     assert lib.tms_version() >= 100
 
 
+def _prototypes():
+    """name -> (return type, [parameter types]) of every prototype in the header, each
+    type reduced to what ctypes passes: 'ptr' for any pointer, else the C type name."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    text = re.sub(r"^\s*#.*$", "", text, flags=re.M)  # preprocessor lines
+    protos = {}
+    for ret, name, params in re.findall(r"([A-Za-z_][\w\s\*]*?)\s*\b(tms_\w+)\s*\(([^)]*)\)\s*;", text):
+        def kind(decl):
+            decl = " ".join(decl.split())
+            if "*" in decl:
+                return "ptr"
+            words = [w for w in decl.split() if w != "const"]
+            return words[0] if len(words) == 1 else " ".join(words[:-1])
+        plist = [p for p in (x.strip() for x in params.split(",")) if p and p != "void"]
+        protos[name] = (kind(ret), [kind(p) for p in plist])
+    return protos
+
+
+def test_ctypes_signatures_match_header_prototypes():
+    """Arity and integer widths of every ctypes binding equal the header's prototype:
+    pointers as c_void_p, int64_t as c_int64, int as c_int, and the return type."""
+    from tilemaxsim_amd import _lib
+    ctype_of = {"ptr": ctypes.c_void_p, "int64_t": ctypes.c_int64, "int": ctypes.c_int}
+    protos = _prototypes()
+    assert set(protos) == set(_lib.SIGNATURES) | {"tms_last_error"}
+    assert protos["tms_last_error"] == ("ptr", [])
+    for name, argtypes in _lib.SIGNATURES.items():
+        ret, params = protos[name]
+        want = [ctype_of[p] for p in params]
+        assert argtypes == want, f"{name}: ctypes {argtypes} != header {params}"
+        assert _lib.RESTYPES.get(name, ctypes.c_int) == ctype_of[ret], f"{name}: return type {ret}"
+    lib = _lib.load()
+    for name, argtypes in _lib.SIGNATURES.items():
+        fn = getattr(lib, name)
+        assert fn.argtypes == argtypes and fn.restype == _lib.RESTYPES.get(name, ctypes.c_int), name
+
+
 def test_rerank_limit_sets_and_restores():
     from tilemaxsim_amd import _lib
     lib = _lib.load()
@@ -369,3 +407,22 @@ def test_c_consumer_links_and_gets_error_statuses(tmp_path):
     run = subprocess.run([exe], capture_output=True, text=True, timeout=60)
     assert run.returncode == 0, (run.returncode, run.stdout, run.stderr)
     assert run.stdout.startswith("ok ")
+
+
+def test_plaid_config_without_gpus_keeps_host_tensors_and_refuses_them():
+    """``config.total_visible_gpus == 0`` (or no config) leaves host tensors where they
+    are, and the GPU check refuses them before any HIP call, as without a config."""
+    from tilemaxsim_amd import flashmaxsim_score_packed, flashmaxsim_score_packed_batched
+    from tilemaxsim_amd.plaid import _to_configured_gpu
+
+    class Config:
+        total_visible_gpus = 0
+
+    Q, D, lens = torch.zeros(1, 32, 128), torch.zeros(10, 128), torch.tensor([4, 6])
+    assert all(a is b for a, b in zip(_to_configured_gpu(Config(), Q, D, lens), (Q, D, lens)))
+    assert all(a is b for a, b in zip(_to_configured_gpu(None, Q, D, lens), (Q, D, lens)))
+    for config in (None, Config()):
+        with pytest.raises(ValueError, match="GPU"):
+            flashmaxsim_score_packed(Q, D, lens, config)
+        with pytest.raises(ValueError, match="GPU"):
+            flashmaxsim_score_packed_batched(Q, D, lens, config)

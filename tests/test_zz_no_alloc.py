@@ -1,9 +1,12 @@
 """tms_topk_noalloc (the allocation-free top-k: intermediate keys in the library's fixed
 device scratch array) against tms_topk with a caller workspace, through the C ABI.
 
-Three calls in a row, each smaller than the one before, must each equal tms_topk bit
+Four calls in a row, each smaller than the one before, must each equal tms_topk bit
 for bit: the scratch array keeps the previous call's keys, which must not leak into the
-next result.
+next result. The first fills the array to its documented limit (top-100 over (32, 5M)
+scores: 32.0 MB of 32 MiB); every call takes at least one intermediate level, so every
+call goes through the scratch array. A graph captured after one eager call replays
+with the eager result.
 """
 import ctypes
 
@@ -39,9 +42,13 @@ def test_topk_noalloc_matches_workspace_entry(cuda):
     from tilemaxsim_amd import _lib
     lib = _lib.load()
     g = torch.Generator(device="cuda").manual_seed(91)
-    # first call: C2's top-100 shape, (64, 1M) scores, 12.9 MB of scratch; second: smaller
-    # rows and a different k, so stale keys of the first call sit past what it writes
-    for rows, n, k in [(64, 1_000_000, 100), (5, 300_000, 37), (3, 4096, 100)]:
+    # (32, 5M): C5's top-100 shape at the array's limit; (64, 1M): C2's, 12.9 MB; then
+    # smaller rows and another k, so stale keys of earlier calls sit past what each writes
+    cases = [(32, 5_000_000, 100), (64, 1_000_000, 100), (5, 300_000, 37), (2, 50_000, 100)]
+    need = [int(lib.tms_topk_workspace_size(r, n, k)) for r, n, k in cases]
+    assert need[0] <= (32 << 20) < int(lib.tms_topk_workspace_size(34, 5_000_000, 100))
+    assert all(a > b > 0 for a, b in zip(need, need[1:])), need
+    for rows, n, k in cases:
         s = torch.randn(rows, n, device="cuda", generator=g)
         print(f"tms_topk_noalloc rows={rows} n={n} k={k}", flush=True)
         v0, i0 = _topk_ws(lib, torch, s, k)
@@ -66,3 +73,29 @@ def test_topk_noalloc_rejects_oversized(cuda):
     rc = lib.tms_topk_noalloc(ctypes.c_void_p(16), 64, 50_000_000, 100, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
     assert rc == _lib.TMS_ERR_UNSUPPORTED
     assert b"scratch" in lib.tms_last_error()
+
+
+def test_topk_noalloc_in_a_captured_graph(cuda):
+    """One eager call (which loads the array and looks up its address on this device),
+    then the call captured into a graph: every replay, with new scores and eager work and
+    synchronisations between replays, equals tms_topk on the same scores."""
+    import torch
+    from tilemaxsim_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator(device="cuda").manual_seed(17)
+    rows, n, k = 8, 300_000, 100
+    s = torch.randn(rows, n, device="cuda", generator=g)
+    _topk_noalloc(lib, torch, s, k)  # the eager first call on this device
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        v, i = _topk_noalloc(lib, torch, s, k)
+    for rep in range(4):
+        s.copy_(torch.randn(rows, n, device="cuda", generator=g))
+        graph.replay()
+        torch.cuda.synchronize()
+        ev, ei = _topk_ws(lib, torch, s, k)  # eager work between replays
+        torch.cuda.synchronize()
+        print(f"graph replay {rep}", flush=True)
+        assert torch.equal(i, ei), rep
+        assert torch.equal(v.view(torch.int32), ev.view(torch.int32)), rep

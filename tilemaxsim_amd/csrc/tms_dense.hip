@@ -124,8 +124,6 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   a.mask4 = (nd % 4 == 0 && ((uintptr_t)mask & 3) == 0) ? 1 : 0;
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);
   const bool qreg = aligned && d > 0 && d <= 128 && d % 32 == 0;
-  // fp32 documents, several query blocks: the shared-tile kernel (one pass for up to 16
-  // blocks, three bf16 MFMAs per product) instead of one pass per two blocks
   // fp32 documents or fp32 queries, several query blocks: the shared-tile kernel (one pass
   // for up to 16 blocks; three or two MFMAs per product) instead of one pass per one or
   // two blocks

@@ -280,9 +280,10 @@ struct TopkTail {
 constexpr uint32_t kTicketGroups = 8, kTicketLine = 16, kTicketTwoLevel = 64;
 static_assert(kTicketLine * (1 + kTicketGroups) == TMS_MAXSIM_TOPK_COUNTER_WORDS, "the counter block of the header");
 // NT threads a workgroup: four waves while the call has at most 1,024 waves (a 256 x
-// 180-token call then spreads over 256 CUs), eight or 16 above that, so that a launch
-// never has more than 256 workgroups: each one takes a ticket and writes its XCD's L2
-// back, and those costs grow with the workgroup count.
+// 180-token call then spreads over 256 CUs), eight or 16 above that, so that a launch has
+// at most 256 workgroups -- or 512 at d = 128 with two query blocks, where workgroups
+// stop at eight waves -- since each one takes a ticket and writes its XCD's L2 back, and
+// those costs grow with the workgroup count.
 template <int DT, int KS, int NB, int NT>
 __global__ void __launch_bounds__(NT) rerank_topk_kernel(RerankArgs a, TopkTail t) {
   rerank_body<DT, KS, NB, RR_FIXED, NT>(a);

@@ -26,6 +26,17 @@ def lengths_to_offsets(D_lengths: torch.Tensor, device: torch.device) -> torch.T
     return offsets
 
 
+def _to_configured_gpu(config, *tensors: torch.Tensor) -> tuple:
+    """The reference's device step (``src/plaid_integration_benchmark.py:159-161``): with
+    ``config.total_visible_gpus > 0`` every input is moved with ``.cuda()`` (to the
+    current device; a no-op for a tensor already there). With no config, or a config
+    that sees no GPU, the tensors stay where they are and the GPU check that follows
+    rejects host tensors, since there is no CPU path."""
+    if config is not None and getattr(config, "total_visible_gpus", 0) > 0:
+        return tuple(t.cuda() for t in tensors)
+    return tensors
+
+
 def flashmaxsim_score_packed(Q: torch.Tensor, D_packed: torch.Tensor, D_lengths: torch.Tensor, config=None,
                              padding: str = "zeros") -> torch.Tensor:
     """Score one query against packed variable-length documents.
@@ -34,20 +45,21 @@ def flashmaxsim_score_packed(Q: torch.Tensor, D_packed: torch.Tensor, D_lengths:
         Q: (1, Nq, d) or (Nq, d) query embeddings (cast to half like the reference).
         D_packed: (T, d) all document tokens back to back.
         D_lengths: (B,) tokens per document; they must sum to at most T.
-        config: accepted for signature compatibility with the reference (ColBERT's
-            run config); unused, the tensors' device decides where scoring runs.
+        config: ColBERT's run config, read as the reference reads it: when
+            ``config.total_visible_gpus > 0``, host tensors are moved to the current GPU
+            first. ``None`` leaves the tensors where they are (they must then be on the GPU).
         padding: "zeros" -- score as the reference does after zero-padding every
             document to the longest one; "mask" -- padding is -inf (ColBERT semantics).
 
     Returns:
         (B,) float32 scores on the GPU.
     """
-    del config
     if padding not in ("zeros", "mask"):
         raise ValueError(f"padding must be 'zeros' or 'mask', got {padding!r}")
     _check.tensor("Q", Q)
     _check.tensor("D_packed", D_packed)
     _check.tensor("D_lengths", D_lengths)
+    Q, D_packed, D_lengths = _to_configured_gpu(config, Q, D_packed, D_lengths)
     Q2 = Q.squeeze(0) if Q.dim() == 3 else Q
     if Q2.dim() != 2 or D_packed.dim() != 2 or D_lengths.dim() != 1:
         raise ValueError("flashmaxsim_score_packed: Q (1, Nq, d), D_packed (T, d), D_lengths (B,)")
@@ -80,15 +92,16 @@ def flashmaxsim_score_packed(Q: torch.Tensor, D_packed: torch.Tensor, D_lengths:
 
 
 def flashmaxsim_score_packed_batched(Qs: torch.Tensor, D_packed: torch.Tensor, D_lengths: torch.Tensor,
-                                     padding: str = "zeros") -> torch.Tensor:
+                                     config=None, padding: str = "zeros") -> torch.Tensor:
     """:func:`flashmaxsim_score_packed` for ``nQ`` queries over the same packed documents:
     ``Qs`` (nQ, Nq, d) -> (nQ, B) float32, one pass over the tokens for up to 32 query
-    blocks. ``padding`` as in :func:`flashmaxsim_score_packed`."""
+    blocks. ``config`` and ``padding`` as in :func:`flashmaxsim_score_packed`."""
     if padding not in ("zeros", "mask"):
         raise ValueError(f"padding must be 'zeros' or 'mask', got {padding!r}")
     _check.tensor("Qs", Qs)
     _check.tensor("D_packed", D_packed)
     _check.tensor("D_lengths", D_lengths)
+    Qs, D_packed, D_lengths = _to_configured_gpu(config, Qs, D_packed, D_lengths)
     if D_lengths.dim() != 1 or D_lengths.dtype.is_floating_point or D_lengths.dtype == torch.bool:
         raise TypeError("flashmaxsim_score_packed_batched: D_lengths must be a 1-D integer tensor")
     if D_packed.dtype != torch.float16:
