@@ -65,6 +65,10 @@ def parse():
                    help="embedding dtype for --config c1, rerank, c2, c2b, c4 and prec")
     p.add_argument("--qdtype", default=None, choices=["fp32"],
                    help="--config c2b: fp32 queries against the --dtype documents (split, never rounded)")
+    p.add_argument("--ncent", type=int, default=1 << 18,
+                   help="--config c6 / c6b: centroids in the index (2^18, ColBERT's choice for ~332M tokens)")
+    p.add_argument("--lds-pattern", type=int, default=None, choices=range(8),
+                   help="--config ldsprobe: time this pattern alone (default: pattern 1 timed, all eight reported)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
@@ -840,14 +844,20 @@ class LdsProbe:
     16 consecutive lanes hit 16 different bank groups (pattern 0), when they read random
     rows of one codebook subspace as the PQ kernel's gathers do (pattern 1, the timed
     one), when they all hit one bank group (pattern 2), and when each bank group gets
-    four lanes of every 16 (pattern 3). LDS bytes, not HBM bytes."""
+    four lanes of every 16 (pattern 3); patterns 4 to 7 repeat them at the PQ kernel's
+    occupancy and footprint (two 8-wave workgroups per CU, 64 KiB each). ``--lds-pattern``
+    times one pattern alone (for counter runs). LDS bytes, not HBM bytes."""
     kernel = "lds_probe_kernel"
-    PATTERNS = {0: "conflict-free (lane l -> bank group l % 16, random rows)",
-                1: "PQ codebook gather (one subspace per 16-lane group, random codes)",
-                2: "one bank group per 16-lane group, random rows",
-                3: "lane l -> bank group (l / 4) % 16: balanced over the wave, 4-way within 16 lanes"}
+    _P = {0: "conflict-free (lane l -> bank group l % 16, random rows)",
+          1: "PQ codebook gather (one subspace per 16-lane group, random codes)",
+          2: "one bank group per 16-lane group, random rows",
+          3: "lane l -> bank group (l / 4) % 16: balanced over the wave, 4-way within 16 lanes"}
+    PATTERNS = {**{p: f"{w}; one 16-wave workgroup per CU, 128 KiB" for p, w in _P.items()},
+                **{p + 4: f"{w}; two 8-wave workgroups per CU, 64 KiB each (the PQ kernel's shape)"
+                   for p, w in _P.items()}}
 
-    def __init__(self, torch):
+    def __init__(self, torch, pattern=None):
+        self.pattern = pattern
         from tilemaxsim_amd import _lib
         self.torch, self.lib, self.check = torch, _lib.load(), _lib.check
         self.nw = _lib.TMS_LDS_PROBE_WAVES
@@ -861,7 +871,7 @@ class LdsProbe:
                                           self.sink.numel(), stream))
 
     def step(self, timer):
-        timer(lambda: self.run(1))
+        timer(lambda: self.run(1 if self.pattern is None else self.pattern))
 
     def bytes_per_launch(self):
         return self.nw * self.instr_per_wave * 1024  # LDS bytes read by all waves
@@ -870,8 +880,9 @@ class LdsProbe:
         return 0
 
     def config(self):
-        return {"workload": "ldsprobe: 256 workgroups x 16 waves x 65,536 ds_read_b128 per wave over 128 KiB "
-                            "of LDS, four lane -> address patterns"}
+        return {"workload": "ldsprobe: 4,096 waves x 65,536 ds_read_b128 per wave, 16 waves per CU (one "
+                            "workgroup over 128 KiB, or two over 64 KiB each), four lane -> address patterns",
+                "pattern": self.pattern}
 
     def cpu_baseline(self, seconds):
         return None
@@ -880,6 +891,8 @@ class LdsProbe:
         torch = self.torch
         out = {}
         for p, what in self.PATTERNS.items():
+            if self.pattern is not None and p != self.pattern:
+                continue
             self.run(p)
             ms = []
             for _ in range(5):
@@ -1101,15 +1114,15 @@ def main():
     elif args.config == "c5b":
         wl = PQBatched(torch, 32, 5_000_000, 128)
     elif args.config == "c6":
-        wl = Residual(torch, 32, 2_000_000, 32, 300)
+        wl = Residual(torch, 32, 2_000_000, 32, 300, ncent=args.ncent)
     elif args.config == "c6b":
-        wl = ResidualBatched(torch, 32, 2_000_000, 32, 300)
+        wl = ResidualBatched(torch, 32, 2_000_000, 32, 300, ncent=args.ncent)
     elif args.config == "readprobe":
         wl = ReadProbe(torch)
     elif args.config == "topk":
         wl = TopK(torch)
     elif args.config == "ldsprobe":
-        wl = LdsProbe(torch)
+        wl = LdsProbe(torch, args.lds_pattern)
     elif args.config == "mfmaprobe":
         wl = MfmaProbe(torch)
     else:

@@ -317,10 +317,11 @@ int tms_read_probe(const void* buf, int64_t bytes, uint32_t* sink, int64_t sink_
  * reference: times 16 x 4096 x 16 ds_read_b128 wave-instructions per CU (256 workgroups
  * of 16 waves, 128 KiB of LDS each) for one lane -> address pattern (0: conflict-free,
  * 1: the PQ kernel's codebook gather, 2: every lane group on one bank group, 3: four
- * lanes of each 16-lane group per bank group) and writes
- * each wave's elapsed s_memtime cycles to `cycles` (TMS_LDS_PROBE_WAVES words) and one
- * XOR word per thread to `sink` (64 x TMS_LDS_PROBE_WAVES words). `bench.py --config
- * ldsprobe` runs the four patterns.
+ * lanes of each 16-lane group per bank group); patterns 4 to 7 are 0 to 3 at the PQ
+ * kernel's occupancy and footprint (512 workgroups of 8 waves, two per CU, 64 KiB of
+ * LDS each). Writes each wave's elapsed s_memtime cycles to `cycles`
+ * (TMS_LDS_PROBE_WAVES words) and one XOR word per thread to `sink` (64 x
+ * TMS_LDS_PROBE_WAVES words). `bench.py --config ldsprobe` runs the eight patterns.
  */
 #define TMS_LDS_PROBE_WAVES 4096
 int tms_lds_probe(int pattern, int64_t* cycles, int64_t cycle_words, uint32_t* sink, int64_t sink_words,

@@ -12,8 +12,43 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+#ifndef TMS_STREAM_NT
+#define TMS_STREAM_NT 1
+#endif
+// A load of streamed document data (tokens, codes: read once per pass). WHOLE: the
+// wave's load covers whole 128-byte lines, and is then non-temporal, so the caches treat
+// the lines as a stream. A read-only pass over 46 GB measured 6.74-6.78 TB/s with such
+// loads against 6.01-6.32 TB/s with plain ones; non-temporal loads that cover half of each
+// line (the other half read by a later load) measured 5.53 TB/s, so those stay plain.
+template <class T, bool WHOLE>
+__device__ __forceinline__ T ld_stream(const void* p) {
+#if TMS_STREAM_NT
+  if constexpr (WHOLE) return __builtin_nontemporal_load((const T*)p);
+#endif
+  return *(const T*)p;
+}
+
+// Whole-line tile loads. A 16-row tile of 256- (or 128-) byte rows is read as loads of
+// eight rows x one 128-byte line: lane 16 g + 8 s + t reads row t (first load) or 8 + t
+// (second load), bytes 64 s + 16 g of the line. The line's two MFMA A-operand fragments
+// (lane 16 g + r: row r, 16-byte chunk 4 k + g of the line, k = 0, 1) follow with one
+// rotate by eight lanes within each row: rows 0-7 of chunk g sit in place in the first
+// load, rows 8-15 eight lanes down in the second, and chunk 4 + g the other way round.
+// Each word is one DPP move (row_ror:8) whose bank mask writes only the lanes that take
+// the rotated value (lanes 8-15 of a row for k0, 0-7 for k1); the others keep the
+// unrotated word. The move runs with the whole wave active (no select that could become
+// a branch, under which the rotate would read inactive lanes).
+__device__ __forceinline__ void line_frags(const u32x4& first8, const u32x4& last8, u32x4& k0, u32x4& k1) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    k0[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)first8[i], (int)last8[i], 0x128, 0xf, 0xc, false);
+    k1[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)last8[i], (int)first8[i], 0x128, 0xf, 0x3, false);
+  }
+}
 
 // Eight consecutive elements of an embedding row as loaded from memory: 16 bytes for
 // fp16 / bf16, 32 bytes for fp32.

@@ -326,6 +326,13 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
     uint32_t m[NSUB];  // masked mode: validity bits of this lane's 4 output rows
     QRaw q[QGLB ? NQB : 1][QGLB ? KS : 1][2];  // memory-resident Q: the k-group's query chunks
   };
+  // LINES (16-bit rows, every 64-dimension pair of k-steps whole, d % 64 == 0): each load
+  // covers whole 128-byte lines of eight rows, non-temporal; line_frags turns a line's two
+  // loads into its two k-steps' fragments when the tile is scored. Lane 16 g + 8 s + t
+  // reads bytes 64 s + 16 g of a line of row t or 8 + t.
+  constexpr bool LINES = FULL && ALIGNED && !F32 && KS % 2 == 0;
+  const int t8 = lane & 7;
+  const int64_t line_off = 64 * ((lane >> 3) & 1) + 16 * g;
   auto load_tile = [&](Buf& buf, const Cursor& c) {
     if constexpr (QGLB) {  // issued with the tile's loads, so waiting for them never drains the prefetch
 #pragma unroll
@@ -344,18 +351,35 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
     }
 #pragma unroll
     for (int sub = 0; sub < NSUB; sub++) {
-      int64_t tok = c.t0 + 16 * sub + r;
-      if (tok > c.len - 1) tok = c.len - 1;
-      const int64_t row = c.base + tok;
+      if constexpr (LINES) {  // f[sub][2i], f[sub][2i+1]: line i of the k-group, rows t and 8 + t
+        int64_t t0 = c.t0 + 16 * sub + t8, t1 = t0 + 8;
+        if (t0 > c.len - 1) t0 = c.len - 1;
+        if (t1 > c.len - 1) t1 = c.len - 1;
+        const uint8_t* p0 = a.D + (c.base + t0) * a.d * 2 + (int64_t)c.kg * 256 + line_off;
+        const uint8_t* p1 = a.D + (c.base + t1) * a.d * 2 + (int64_t)c.kg * 256 + line_off;
 #pragma unroll
-      for (int s = 0; s < KS; s++) {
-        const int S = c.kg * KS + s;
-        if (!QREG && S >= a.nstep) {
-          buf.f[sub][s] = Raw{};
-        } else if constexpr (FULL && ALIGNED && !F32) {
-          buf.f[sub][s] = *(const u32x4*)(a.D + (row * a.d + 8 * (int64_t)(4 * S + g)) * 2);
-        } else {
-          buf.f[sub][s] = load_chunk<DT, ALIGNED>(a.D, row, 4 * S + g, a.d, a.nchunk);
+        for (int i = 0; i < KS / 2; i++) {
+          if (!QREG && c.kg * KS + 2 * i >= a.nstep) {  // nstep is even: both k-steps past the end
+            buf.f[sub][2 * i] = buf.f[sub][2 * i + 1] = Raw{};
+          } else {
+            buf.f[sub][2 * i] = ld_stream<u32x4, true>(p0 + 128 * i);
+            buf.f[sub][2 * i + 1] = ld_stream<u32x4, true>(p1 + 128 * i);
+          }
+        }
+      } else {
+        int64_t tok = c.t0 + 16 * sub + r;
+        if (tok > c.len - 1) tok = c.len - 1;
+        const int64_t row = c.base + tok;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+          const int S = c.kg * KS + s;
+          if (!QREG && S >= a.nstep) {
+            buf.f[sub][s] = Raw{};
+          } else if constexpr (FULL && ALIGNED && !F32) {
+            buf.f[sub][s] = *(const u32x4*)(a.D + (row * a.d + 8 * (int64_t)(4 * S + g)) * 2);
+          } else {
+            buf.f[sub][s] = load_chunk<DT, ALIGNED>(a.D, row, 4 * S + g, a.d, a.nchunk);
+          }
         }
       }
       if constexpr (MODE == MODE_MASKED) {
@@ -430,6 +454,18 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
   };
 
   auto compute_tile = [&](const Buf& buf, const Cursor& c) {
+    Raw lf[LINES ? NSUB : 1][LINES ? KS : 1];  // LINES: the fragments of the tile's loads
+    if constexpr (LINES) {
+#pragma unroll
+      for (int sub = 0; sub < NSUB; sub++)
+#pragma unroll
+        for (int i = 0; i < KS / 2; i++)
+          line_frags(buf.f[sub][2 * i], buf.f[sub][2 * i + 1], lf[sub][2 * i], lf[sub][2 * i + 1]);
+    }
+    auto F = [&](int sub, int s) -> const Raw& {  // chunk 4 s + g of row r of subtile sub
+      if constexpr (LINES) return lf[sub][s];
+      else return buf.f[sub][s];
+    };
     if constexpr (QREG) {
       // One k-group: each query block is finished before the next, so only one
       // block's accumulators are live (what lets a wave hold several blocks).
@@ -445,7 +481,7 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
 #pragma unroll
             for (int sub = 0; sub < NSUB; sub++) {
               u32x4 dh, dl;
-              split_bf16(buf.f[sub][s], dh, dl);
+              split_bf16(F(sub, s), dh, dl);
 #pragma unroll
               for (int h = 0; h < 2; h++) {
                 acc1[sub][h] = mfma16x16x32<MDT>(dl, qf[j][s][h], acc1[sub][h]);
@@ -458,15 +494,15 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
             for (int h = 0; h < 2; h++)
 #pragma unroll
               for (int sub = 0; sub < NSUB; sub++) {
-                acc1[sub][h] = mfma16x16x32<MDT>(buf.f[sub][s], qfl[j][s][h], acc1[sub][h]);
-                acc1[sub][h] = mfma16x16x32<MDT>(buf.f[sub][s], qf[j][s][h], acc1[sub][h]);
+                acc1[sub][h] = mfma16x16x32<MDT>(F(sub, s), qfl[j][s][h], acc1[sub][h]);
+                acc1[sub][h] = mfma16x16x32<MDT>(F(sub, s), qf[j][s][h], acc1[sub][h]);
               }
           } else {
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
               for (int sub = 0; sub < NSUB; sub++)
-                acc1[sub][h] = mfma16x16x32<MDT>(buf.f[sub][s], qf[j][s][h], acc1[sub][h]);
+                acc1[sub][h] = mfma16x16x32<MDT>(F(sub, s), qf[j][s][h], acc1[sub][h]);
           }
         }
 #pragma unroll
@@ -484,8 +520,8 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
       u32x4 dh[NSUB], dl[F32 ? NSUB : 1];
 #pragma unroll
       for (int sub = 0; sub < NSUB; sub++) {
-        if constexpr (F32) split_bf16(buf.f[sub][s], dh[sub], dl[sub]);
-        else dh[sub] = buf.f[sub][s];
+        if constexpr (F32) split_bf16(F(sub, s), dh[sub], dl[sub]);
+        else dh[sub] = F(sub, s);
       }
 #pragma unroll
       for (int j = 0; j < NQB; j++)
@@ -637,7 +673,9 @@ static int launch_one(const DenseArgs& a, int64_t waves, size_t lds, hipStream_t
 
 template <int DT, int QDT, int MODE, int NQB>
 static int launch_nqb(const DenseArgs& a, bool aligned, int64_t waves, hipStream_t st) {
-  const bool full = aligned && (a.d % 32 == 0);
+  // every pair of k-steps whole (the tiles' whole-line loads): d % 64 == 0; d % 64 == 32
+  // takes the bounds-checked loads
+  const bool full = aligned && (a.d % 64 == 0);
   if (aligned && a.d > 0 && a.d <= 128 && a.d % 32 == 0) {
     switch (a.d / 32) {
       case 1: return launch_one<DT, QDT, MODE, NQB, 1, true, true>(a, waves, 0, st);

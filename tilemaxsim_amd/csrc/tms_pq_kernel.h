@@ -180,31 +180,31 @@ __global__ void __launch_bounds__(kPqThreads) pq_mfma_score_kernel(PqArgs a) {
       if constexpr (LU == 16) {
 #pragma unroll
         for (int i = 0; i < LB / 16; i++) {
-          const uint4 v = ((const uint4*)p)[i];
-          c.w[u][4 * i] = v.x;
-          c.w[u][4 * i + 1] = v.y;
-          c.w[u][4 * i + 2] = v.z;
-          c.w[u][4 * i + 3] = v.w;
+          const u32x4 v = ld_stream<u32x4, true>(p + 16 * i);
+          c.w[u][4 * i] = v[0];
+          c.w[u][4 * i + 1] = v[1];
+          c.w[u][4 * i + 2] = v[2];
+          c.w[u][4 * i + 3] = v[3];
         }
       } else if constexpr (LU == 8) {
 #pragma unroll
         for (int i = 0; i < LB / 8; i++) {
-          const uint2 v = ((const uint2*)p)[i];
-          c.w[u][2 * i] = v.x;
-          c.w[u][2 * i + 1] = v.y;
+          const u32x2 v = ld_stream<u32x2, true>(p + 8 * i);
+          c.w[u][2 * i] = v[0];
+          c.w[u][2 * i + 1] = v[1];
         }
       } else if constexpr (LU == 4) {
 #pragma unroll
-        for (int i = 0; i < LB / 4; i++) c.w[u][i] = ((const uint32_t*)p)[i];
+        for (int i = 0; i < LB / 4; i++) c.w[u][i] = ld_stream<uint32_t, true>(p + 4 * i);
       } else {
 #pragma unroll
         for (int i = 0; i < CW; i++) c.w[u][i] = 0;
         if constexpr (LU == 2) {
 #pragma unroll
-          for (int i = 0; i < LB / 2; i++) c.w[u][i / 2] |= (uint32_t)((const uint16_t*)p)[i] << (16 * (i % 2));
+          for (int i = 0; i < LB / 2; i++) c.w[u][i / 2] |= (uint32_t)ld_stream<uint16_t, true>(p + 2 * i) << (16 * (i % 2));
         } else {
 #pragma unroll
-          for (int i = 0; i < LB; i++) c.w[u][i / 4] |= (uint32_t)p[i] << (8 * (i % 4));
+          for (int i = 0; i < LB; i++) c.w[u][i / 4] |= (uint32_t)ld_stream<uint8_t, true>(p + i) << (8 * (i % 4));
         }
       }
     }

@@ -4,7 +4,8 @@
 // `bench.py --config readprobe`. Not part of the scoring path; no reference counterpart.
 //
 // Persistent grid (8 workgroups of 4 waves per CU) striding over 8 KiB chunks, each
-// wave-iteration 8 independent 16-byte loads per lane (64 lanes x 16 B x 8 contiguous);
+// wave-iteration 8 independent 16-byte loads per lane (64 lanes x 16 B x 8 contiguous,
+// non-temporal: each load covers whole 128-byte lines);
 // the workgroups dispatched to one XCD (blockIdx % 8) take a contiguous range of block
 // ids, which was the fastest of the mappings tried (contiguous runs per wave, grid-stride
 // at 1x and 2x the resident grid, 4 / 8 / 16 KiB per iteration: 6.10-6.30 TB/s over a
@@ -30,7 +31,7 @@ __global__ void __launch_bounds__(256) read_probe_kernel(const uint8_t* __restri
     const uint8_t* p = base + c * kProbeChunk + lane * 16;  // < (c + 1) * kProbeChunk
     u32x4 v[kProbeDepth];
 #pragma unroll
-    for (int j = 0; j < kProbeDepth; j++) v[j] = *(const u32x4*)(p + j * 1024);
+    for (int j = 0; j < kProbeDepth; j++) v[j] = ld_stream<u32x4, true>(p + j * 1024);  // whole lines
 #pragma unroll
     for (int j = 0; j < kProbeDepth; j++) acc ^= v[j];
   }
@@ -55,10 +56,12 @@ extern "C" int tms_read_probe(const void* buf, int64_t bytes, uint32_t* sink, in
 }
 
 // ---------------------------------------------------------------------------------
-// LDS gather probe: the cost of one ds_read_b128 wave-instruction for three lane ->
+// LDS gather probe: the cost of one ds_read_b128 wave-instruction for four lane ->
 // address patterns over a 128 KiB LDS buffer (one 16-wave workgroup per CU, every
-// offset masked into the buffer). It backs the PQ kernel's floor: its codebook gathers
-// are pattern 1. Not part of the scoring path; no reference counterpart.
+// offset masked into the buffer), and the same four patterns (4 to 7) at the PQ
+// kernel's occupancy and footprint: two 8-wave workgroups per CU, each over its own
+// 64 KiB buffer (a codebook's size). It backs the PQ kernel's floor: its codebook
+// gathers are pattern 1 (5). Not part of the scoring path; no reference counterpart.
 //   0: 16 consecutive lanes read 16 different 16-byte bank groups of random 256-byte
 //      rows (lane l -> group l % 16): conflict-free;
 //   1: the PQ gather: the 16 lanes of an MFMA lane group read random 16-byte rows of one
@@ -81,21 +84,26 @@ __device__ __forceinline__ uint32_t probe_hash(uint32_t x) {
   return x;
 }
 
-__global__ void __launch_bounds__(1024) lds_probe_kernel(int pattern, int64_t* __restrict__ cycles,
-                                                         uint32_t* __restrict__ sink) {
+// NT threads a workgroup over UNITS 16-byte units of LDS; waves are numbered across the
+// grid (blockIdx.x * NT / 64 + wave), so every launch shape has TMS_LDS_PROBE_WAVES waves.
+template <int NT, int UNITS>
+__global__ void __launch_bounds__(NT) lds_probe_kernel(int pattern, int64_t* __restrict__ cycles,
+                                                       uint32_t* __restrict__ sink) {
   extern __shared__ u32x4 probe_lds[];
-  for (int i = threadIdx.x; i < kLdsProbeUnits; i += 1024) probe_lds[i] = u32x4{(uint32_t)i, 1u, 2u, 3u};
+  for (int i = threadIdx.x; i < UNITS; i += NT) probe_lds[i] = u32x4{(uint32_t)i, 1u, 2u, 3u};
+  constexpr int kWaves = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int gw = blockIdx.x * kWaves + wave;  // < TMS_LDS_PROBE_WAVES
   uint32_t o[kLdsProbeOffs];
 #pragma unroll
   for (int j = 0; j < kLdsProbeOffs; j++) {
-    const uint32_t h = probe_hash((uint32_t)(((blockIdx.x * 16 + wave) * 64 + lane) * kLdsProbeOffs + j));
+    const uint32_t h = probe_hash((uint32_t)((gw * 64 + lane) * kLdsProbeOffs + j));
     uint32_t u;
     if (pattern == 0) u = (h % 512u) * 16u + (uint32_t)(lane & 15);
     else if (pattern == 1) u = (uint32_t)((j + 4 * (lane >> 4)) & 15) * 256u + (h % 256u);
     else if (pattern == 2) u = (h % 512u) * 16u + (uint32_t)(lane >> 4);
     else u = (h % 512u) * 16u + (uint32_t)((lane >> 2) & 15);
-    o[j] = u & (kLdsProbeUnits - 1);
+    o[j] = u & (UNITS - 1);
   }
   __syncthreads();
   u32x4 acc = {0u, 0u, 0u, 0u};
@@ -107,8 +115,8 @@ __global__ void __launch_bounds__(1024) lds_probe_kernel(int pattern, int64_t* _
     for (int j = 0; j < kLdsProbeOffs; j++) asm volatile("" : "+v"(o[j]));  // keeps the loads in the loop
   }
   const uint64_t t1 = __builtin_readcyclecounter();
-  if (lane == 0) cycles[blockIdx.x * 16 + wave] = (int64_t)(t1 - t0);
-  sink[blockIdx.x * 1024 + threadIdx.x] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  if (lane == 0) cycles[gw] = (int64_t)(t1 - t0);
+  sink[gw * 64 + lane] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
 }  // namespace tms
@@ -116,13 +124,17 @@ __global__ void __launch_bounds__(1024) lds_probe_kernel(int pattern, int64_t* _
 extern "C" int tms_lds_probe(int pattern, int64_t* cycles, int64_t cycle_words, uint32_t* sink, int64_t sink_words,
                              void* stream) {
   const char* fn = "tms_lds_probe";
-  if (pattern < 0 || pattern > 3) return fail(TMS_ERR_INVALID, "%s: pattern=%d must be 0 to 3", fn, pattern);
+  if (pattern < 0 || pattern > 7) return fail(TMS_ERR_INVALID, "%s: pattern=%d must be 0 to 7", fn, pattern);
   if (!cycles || cycle_words < TMS_LDS_PROBE_WAVES)
     return fail(TMS_ERR_INVALID, "%s: cycles needs %d words", fn, TMS_LDS_PROBE_WAVES);
   if (!sink || sink_words < TMS_LDS_PROBE_WAVES * 64)
     return fail(TMS_ERR_INVALID, "%s: the sink needs %d words", fn, TMS_LDS_PROBE_WAVES * 64);
-  hipLaunchKernelGGL(lds_probe_kernel, dim3(TMS_LDS_PROBE_WAVES / 16), dim3(1024), kLdsProbeUnits * 16,
-                     (hipStream_t)stream, pattern, cycles, sink);
+  if (pattern < 4)  // one 16-wave workgroup per CU over 128 KiB
+    hipLaunchKernelGGL((lds_probe_kernel<1024, kLdsProbeUnits>), dim3(TMS_LDS_PROBE_WAVES / 16), dim3(1024),
+                       kLdsProbeUnits * 16, (hipStream_t)stream, pattern, cycles, sink);
+  else  // the PQ kernel's shape: two 8-wave workgroups per CU, 64 KiB each
+    hipLaunchKernelGGL((lds_probe_kernel<512, kLdsProbeUnits / 2>), dim3(TMS_LDS_PROBE_WAVES / 8), dim3(512),
+                       kLdsProbeUnits * 8, (hipStream_t)stream, pattern - 4, cycles, sink);
   return check_launch("lds_probe_kernel");
 }
 

@@ -84,11 +84,17 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
     const int64_t tpd = (tiles + R - 1) / R * R;  // tiles per document, padded to a multiple of R
     const int64_t total = ndocs * tpd;
     const int64_t row_bytes = (int64_t)a.d * 2;
-    const uint8_t* base = a.D + b_begin * a.nd * row_bytes + (int64_t)(8 * g) * 2;
+    // LINES (rows of 128 or 256 bytes): each load covers whole 128-byte lines of eight rows
+    // (line_frags); lane 16 g + 8 s + t reads bytes 64 s + 16 g of a line of row t or 8 + t.
+    // Otherwise lane (r, g) reads chunk 4 s + g of row r, a quarter line per load.
+    constexpr bool LINES = KS % 2 == 0;
+    const int t8 = lane & 7;
+    const uint8_t* base = a.D + b_begin * a.nd * row_bytes +
+                          (LINES ? (int64_t)(64 * ((lane >> 3) & 1) + 16 * g) : (int64_t)(8 * g) * 2);
 
-    // Address of this lane's token row for tile (doc offset dd, tile t).
-    auto tile_ptr = [&](int64_t dd, int64_t t) -> const uint8_t* {
-      int64_t tok = t * 16 + r;
+    // Address of a token row of tile (doc offset dd, tile t): row i of the tile, clamped.
+    auto tile_ptr = [&](int64_t dd, int64_t t, int i) -> const uint8_t* {
+      int64_t tok = t * 16 + i;
       if (tok > a.nd - 1) tok = a.nd - 1;
       return base + (dd * a.nd + tok) * row_bytes;
     };
@@ -106,9 +112,19 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
 
     u32x4 ring[R][KS];
     auto load = [&](u32x4 (&buf)[KS]) {
-      const uint8_t* p = tile_ptr(pd, pt);
+      if constexpr (LINES) {  // buf[2i], buf[2i+1]: line i of rows t and 8 + t
+        const uint8_t* p0 = tile_ptr(pd, pt, t8);
+        const uint8_t* p1 = tile_ptr(pd, pt, 8 + t8);
 #pragma unroll
-      for (int s = 0; s < KS; s++) buf[s] = *(const u32x4*)(p + 64 * s);
+        for (int i = 0; i < KS / 2; i++) {
+          buf[2 * i] = ld_stream<u32x4, true>(p0 + 128 * i);
+          buf[2 * i + 1] = ld_stream<u32x4, true>(p1 + 128 * i);
+        }
+      } else {
+        const uint8_t* p = tile_ptr(pd, pt, r);
+#pragma unroll
+        for (int s = 0; s < KS; s++) buf[s] = ld_stream<u32x4, false>(p + 64 * s);
+      }
     };
 #pragma unroll
     for (int k = 0; k < PFD; k++) {
@@ -117,7 +133,15 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
     }
 
     float rmax[NB][2];
-    auto score = [&](const u32x4 (&buf)[KS]) {
+    auto score = [&](const u32x4 (&raw)[KS]) {
+      u32x4 buf[KS];  // A-operand fragments: chunk 4 s + g of row r
+      if constexpr (LINES) {
+#pragma unroll
+        for (int i = 0; i < KS / 2; i++) line_frags(raw[2 * i], raw[2 * i + 1], buf[2 * i], buf[2 * i + 1]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; s++) buf[s] = raw[s];
+      }
       f32x4 acc[NB][2];
 #pragma unroll
       for (int j = 0; j < NB; j++) acc[j][0] = acc[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -208,7 +232,9 @@ static int stream_launch(const StreamArgs& a, int64_t grid, hipStream_t st) {
   return check_launch("stream_maxsim_kernel");
 }
 
-#define TMS_BATCHED_WAVES 8        // waves per workgroup (one workgroup per CU) in the batched kernel
+#ifndef TMS_BATCHED_WAVES
+#define TMS_BATCHED_WAVES 8  // waves per workgroup (one workgroup per CU) in the batched kernel
+#endif
 constexpr int kMaxBlocksPerWave = 4;  // query blocks held in VGPRs per wave there: 1, 2 or 4
 
 template <int DT, int NB>
@@ -327,7 +353,7 @@ struct PqTiles {
 };
 
 template <int DT, int KS, int NB, class SRC>
-__global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 1) batched_tile_kernel(BatchedArgs a) {
+__global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 2) batched_tile_kernel(BatchedArgs a) {
   constexpr int NS = 4;  // LDS ring slots and load lead, in tiles
   constexpr int NP = SRC::kParts;
   constexpr bool SPLIT = NP == 2;        // fp32 rows and queries: DT is the MFMA type, bf16
