@@ -12,9 +12,10 @@
 
 namespace tms {
 
-// Fixed-length documents with d in {32, 64, 96, 128} (tms_stream.hip).
-int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype,
-               float* out, hipStream_t st);
+// Fixed-length documents (offsets null) or documents at offsets into T >= 1 rows, d in
+// {32, 64, 96, 128} (tms_stream.hip).
+int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd,
+               const int64_t* offsets, int64_t T, int64_t pad_len, int dtype, float* out, hipStream_t st);
 // Variable-length documents, d in {32, 64, 96, 128}, several query blocks (tms_stream.hip).
 int run_varlen_batched(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t T,
                        const int64_t* offsets, int64_t nd, int64_t B, int64_t pad_len, int dtype, float* out,
@@ -137,9 +138,13 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   // over up to four waves, so that small calls still fill the chip
   if (qreg && nQ * a.nbq <= 3 && rerank_fits(B, hint))
     return run_rerank(Q, nQ, nq, d, D, B, nd, total_tokens, offsets, mask, pad_len, mode, dtype, out, st);
-  if (mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, dtype, out, st);
+  if (mode == MODE_FIXED && qreg) return run_stream(Q, nQ, nq, d, D, B, nd, nullptr, 0, 0, dtype, out, st);
   if (mode == MODE_VARLEN && qreg && a.nbq <= 4 && nQ * a.nbq >= 4)  // one pass for up to 32 blocks
     return run_varlen_batched(Q, nQ, nq, d, D, total_tokens, offsets, 0, B, pad_len, dtype, out, st, false);
+  // variable-length documents against one or two query blocks per pass: the stream kernel,
+  // whose walk reads each wave's document bounds from its lanes (no rows: the general kernel)
+  if (mode == MODE_VARLEN && qreg && total_tokens > 0)
+    return run_stream(Q, nQ, nq, d, D, B, 0, offsets, total_tokens, pad_len, dtype, out, st);
   if (dtype == TMS_DTYPE_F16) return run_dense<TMS_DTYPE_F16, TMS_DTYPE_F16>(a, nQ, mode, aligned, st);
   return run_dense<TMS_DTYPE_BF16, TMS_DTYPE_BF16>(a, nQ, mode, aligned, st);
 }

@@ -1,11 +1,13 @@
-// Fixed-length dense MaxSim, d <= 128, query fragments in VGPRs: the streaming kernel
-// with a control-flow shape the compiler's memory-counter tracking follows exactly.
+// Dense MaxSim, d <= 128, query fragments in VGPRs, over fixed-length documents or
+// documents at offsets: the streaming kernel with a control-flow shape the compiler's
+// memory-counter tracking follows exactly.
 //
 // The general kernel (tms_dense.hip) walks documents with a cursor whose branches make
 // the compiler drain every outstanding load before each tile. Here:
-//  * documents are fixed length, so a wave's tiles are a flat sequence; each document
-//    is padded to a multiple of R = PFD + 1 tiles with clamped duplicates of its last
-//    token (a duplicate cannot change a max), so every document starts at ring slot 0;
+//  * a wave's tiles are a flat sequence; each document is padded to a multiple of
+//    R = PFD + 1 tiles with clamped duplicates of its last token (a duplicate cannot
+//    change a max), so every document starts at ring slot 0; with offsets, lane j holds
+//    document j's first row and length and the walk reads them with readlane;
 //  * the inner loop body is straight-line and unrolled R times: it issues the loads of
 //    tile g + PFD (index clamped to the last tile, so the count never varies) and scores
 //    tile g from the ring; the per-document reduction sits between inner loops;
@@ -24,19 +26,25 @@
 namespace tms {
 
 struct StreamArgs {
-  const uint8_t* Q;  // (nQ * nq, d)
-  const uint8_t* D;  // (B, nd, d)
-  float* out;        // (nQ, B)
-  int64_t B, nd;
-  int32_t nq, nbq;   // tokens per query, 32-token blocks per query
-  int32_t blk0;      // first global query block of this launch
-  int32_t blk_end;   // one past the last block of this launch
-  int32_t nblk;      // blocks per wave
-  int32_t d;         // 32 * KS
-  int32_t docs_per_wave;  // documents per wave; <= 64
+  const uint8_t* Q;          // (nQ * nq, d)
+  const uint8_t* D;          // fixed length: (B, nd, d); variable length: (T, d)
+  const int64_t* offsets;    // variable length: (B + 1)
+  float* out;                // (nQ, B)
+  int64_t B, nd, T, pad_len;  // pad_len > 0 (variable length): score as if zero-padded to it
+  int32_t nq, nbq;           // tokens per query, 32-token blocks per query
+  int32_t blk0;              // first global query block of this launch
+  int32_t blk_end;           // one past the last block of this launch
+  int32_t nblk;              // blocks per wave
+  int32_t d;                 // 32 * KS
+  int32_t docs_per_wave;     // documents per wave; <= 64
 };
 
-template <int DT, int KS, int NB, int PFD>
+// VARLEN: documents at offsets (T >= 1 rows). Lane j of a wave holds its document j's first
+// row and length, which the walk reads with readlane, so the tile sequence stays
+// straight-line as for fixed lengths. An empty document, or one with invalid offsets,
+// takes R tiles of row 0 whose maxima are dropped: its score is -inf (0 when padded),
+// or NaN for invalid offsets.
+template <int DT, int KS, int NB, int PFD, bool VARLEN>
 __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
   constexpr int R = PFD + 1;
   const int lane = threadIdx.x & 63;
@@ -75,53 +83,103 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
         qf[j][s][h] = v ? *(const u32x4*)(a.Q + (row * a.d + 8 * (4 * s + g)) * 2) : u32x4{0u, 0u, 0u, 0u};
     }
 
+  // VARLEN: lane j holds document b_begin + j's first row (0 if it has no rows) and its
+  // length (-1: invalid offsets).
+  int64_t dbase = 0;
+  int32_t dlen = 0;
+  if constexpr (VARLEN) {
+    dlen = -1;
+    if (lane < ndocs) {
+      const int64_t b = b_begin + lane;
+      const int64_t s0 = a.offsets[b], e0 = a.offsets[b + 1];
+      if (s0 >= 0 && e0 >= s0 && e0 <= a.T && e0 - s0 <= 0x7fffffff) {
+        dlen = (int32_t)(e0 - s0);
+        dbase = dlen > 0 ? s0 : 0;
+      }
+    }
+  }
+  auto doc_len = [&](int64_t dd) -> int64_t {
+    if constexpr (VARLEN) return (int32_t)__builtin_amdgcn_readlane((uint32_t)dlen, (int)dd);
+    else return a.nd;
+  };
+  auto doc_base = [&](int64_t dd) -> int64_t {
+    if constexpr (VARLEN) {
+      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)dbase, (int)dd);
+      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)dbase >> 32), (int)dd);
+      return (int64_t)(((uint64_t)hi << 32) | lo);
+    } else {
+      return (b_begin + dd) * a.nd;
+    }
+  };
+  // tiles of a document of `len` rows, padded to a multiple of R (at least R)
+  auto doc_tiles = [&](int64_t len) -> int64_t {
+    const int64_t t = len > 0 ? (len + 15) / 16 : 1;
+    return (t + R - 1) / R * R;
+  };
+
   float pend[NB];
 #pragma unroll
   for (int j = 0; j < NB; j++) pend[j] = NEG_INF;
 
-  if (a.nd > 0) {
-    const int64_t tiles = (a.nd + 15) / 16;
-    const int64_t tpd = (tiles + R - 1) / R * R;  // tiles per document, padded to a multiple of R
-    const int64_t total = ndocs * tpd;
+  if (VARLEN || a.nd > 0) {
+    const int64_t tpd = doc_tiles(a.nd);  // fixed length: tiles per document
+    int64_t total;                        // tiles of the wave's documents
+    if constexpr (VARLEN) {
+      int32_t n = lane < ndocs ? (int32_t)doc_tiles(dlen) : 0;
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o);
+      total = (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)n);
+    } else {
+      total = ndocs * tpd;
+    }
     const int64_t row_bytes = (int64_t)a.d * 2;
     // LINES (rows of 128 or 256 bytes): each load covers whole 128-byte lines of eight rows
     // (line_frags); lane 16 g + 8 s + t reads bytes 64 s + 16 g of a line of row t or 8 + t.
     // Otherwise lane (r, g) reads chunk 4 s + g of row r, a quarter line per load.
     constexpr bool LINES = KS % 2 == 0;
     const int t8 = lane & 7;
-    const uint8_t* base = a.D + b_begin * a.nd * row_bytes +
-                          (LINES ? (int64_t)(64 * ((lane >> 3) & 1) + 16 * g) : (int64_t)(8 * g) * 2);
+    const uint8_t* base = a.D + (LINES ? (int64_t)(64 * ((lane >> 3) & 1) + 16 * g) : (int64_t)(8 * g) * 2);
 
-    // Address of a token row of tile (doc offset dd, tile t): row i of the tile, clamped.
-    auto tile_ptr = [&](int64_t dd, int64_t t, int i) -> const uint8_t* {
+    // Address of a token row of tile (document dd of the wave, tile t): row i of the
+    // tile, clamped to the document's last row (row 0 for a document without rows).
+    int64_t c_base = doc_base(0), c_len = doc_len(0);  // the prefetch cursor's document
+    auto tile_ptr = [&](int64_t t, int i) -> const uint8_t* {
       int64_t tok = t * 16 + i;
-      if (tok > a.nd - 1) tok = a.nd - 1;
-      return base + (dd * a.nd + tok) * row_bytes;
+      const int64_t last = c_len > 0 ? c_len - 1 : 0;
+      if (tok > last) tok = last;
+      return base + (c_base + tok) * row_bytes;
     };
-    // Prefetch cursor: tile index pf = pd * tpd + pt, saturating at the last tile (the
-    // prefetches past the end re-read it, L1-resident, so each iteration issues KS loads).
-    int64_t pd = 0, pt = 0, pf = 0;
+    // Prefetch cursor: tile index pf (tile pt of document pd), saturating at the last tile
+    // (the prefetches past the end re-read it, so each iteration issues KS loads).
+    int64_t pd = 0, pt = 0, pf = 0, c_tiles = VARLEN ? doc_tiles(c_len) : tpd;
     auto pf_next = [&]() {
       const bool more = pf < total - 1;
       pf += more ? 1 : 0;
       pt += more ? 1 : 0;
-      const bool wrap = pt == tpd;
+      const bool wrap = pt == c_tiles;
       pt = wrap ? 0 : pt;
       pd += wrap ? 1 : 0;
+      if constexpr (VARLEN) {  // pd < ndocs: the cursor stops at the last tile
+        c_base = doc_base(pd);
+        c_len = doc_len(pd);
+        c_tiles = doc_tiles(c_len);
+      } else {
+        c_base = (b_begin + pd) * a.nd;
+      }
     };
 
     u32x4 ring[R][KS];
     auto load = [&](u32x4 (&buf)[KS]) {
       if constexpr (LINES) {  // buf[2i], buf[2i+1]: line i of rows t and 8 + t
-        const uint8_t* p0 = tile_ptr(pd, pt, t8);
-        const uint8_t* p1 = tile_ptr(pd, pt, 8 + t8);
+        const uint8_t* p0 = tile_ptr(pt, t8);
+        const uint8_t* p1 = tile_ptr(pt, 8 + t8);
 #pragma unroll
         for (int i = 0; i < KS / 2; i++) {
           buf[2 * i] = ld_stream<u32x4, true>(p0 + 128 * i);
           buf[2 * i + 1] = ld_stream<u32x4, true>(p1 + 128 * i);
         }
       } else {
-        const uint8_t* p = tile_ptr(pd, pt, r);
+        const uint8_t* p = tile_ptr(pt, r);
 #pragma unroll
         for (int s = 0; s < KS; s++) buf[s] = ld_stream<u32x4, false>(p + 64 * s);
       }
@@ -161,7 +219,9 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
     for (int64_t dd = 0; dd < ndocs; dd++) {
 #pragma unroll
       for (int j = 0; j < NB; j++) rmax[j][0] = rmax[j][1] = NEG_INF;
-      for (int64_t t = 0; t < tpd; t += R) {
+      const int64_t len = doc_len(dd);
+      const int64_t nt = VARLEN ? doc_tiles(len) : tpd;
+      for (int64_t t = 0; t < nt; t += R) {
 #pragma unroll
         for (int k = 0; k < R; k++) {
           load(ring[(k + PFD) % R]);
@@ -170,6 +230,7 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
         }
       }
       // document done: max over the 64 rows of each column, sum over query tokens
+      const bool padded = VARLEN && len < a.pad_len;  // zero padding adds dot products of 0
       float blk[NB];
 #pragma unroll
       for (int j = 0; j < NB; j++) {
@@ -179,6 +240,7 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
           float m = rmax[j][h];
           m = fmaxf(m, __shfl_xor(m, 16));
           m = fmaxf(m, __shfl_xor(m, 32));
+          if (padded) m = fmaxf(m, 0.f);
           int64_t row;
           s += q_valid(j, h, row) ? m : 0.f;
         }
@@ -186,6 +248,7 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
         s += __shfl_xor(s, 4);
         s += __shfl_xor(s, 2);
         s += __shfl_xor(s, 1);
+        if (VARLEN && len <= 0) s = a.pad_len > 0 ? 0.f : NEG_INF;  // no rows (the tiles read row 0)
         blk[j] = s;
       }
       const bool mine = lane == (int)dd;
@@ -207,7 +270,8 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
       s += pend[j];
       if (j == my_nblk - 1 || (jb + 1) / a.nbq != qi) {
         float* o = a.out + (int64_t)qi * a.B + b;
-        *o = (qi * a.nbq < my_blk0) ? *o + s : s;
+        if (VARLEN && dlen < 0) store_nan_score(o);  // invalid offsets
+        else *o = (qi * a.nbq < my_blk0) ? *o + s : s;
         s = 0.f;
       }
     }
@@ -228,7 +292,12 @@ struct RingSlotS {
 
 template <int DT, int KS, int NB>
 static int stream_launch(const StreamArgs& a, int64_t grid, hipStream_t st) {
-  hipLaunchKernelGGL((stream_maxsim_kernel<DT, KS, NB, TMS_STREAM_PFD>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  if (a.offsets)
+    hipLaunchKernelGGL((stream_maxsim_kernel<DT, KS, NB, TMS_STREAM_PFD, true>), dim3((unsigned)grid), dim3(256), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL((stream_maxsim_kernel<DT, KS, NB, TMS_STREAM_PFD, false>), dim3((unsigned)grid), dim3(256), 0,
+                       st, a);
   return check_launch("stream_maxsim_kernel");
 }
 
@@ -761,23 +830,30 @@ int run_pq_batched(const void* Q, int64_t nQ, int64_t nq, const void* codebook, 
   });
 }
 
-// Entry used by tms_dense.hip for fixed-length documents with d in {32, 64, 96, 128},
-// 16-byte aligned Q and D. nQ queries of nq tokens; out is (nQ, B).
-int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd, int dtype,
-               float* out, hipStream_t st) {
+// Entry used by tms_dense.hip for d in {32, 64, 96, 128}, 16-byte aligned Q and D:
+// fixed-length documents (offsets null), or documents at offsets into T >= 1 rows
+// (pad_len > 0: scored as if zero-padded to pad_len tokens). nQ queries of nq tokens;
+// out is (nQ, B).
+int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, int64_t B, int64_t nd,
+               const int64_t* offsets, int64_t T, int64_t pad_len, int dtype, float* out, hipStream_t st) {
   StreamArgs a;
+  memset(&a, 0, sizeof(a));
   a.Q = (const uint8_t*)Q;
   a.D = (const uint8_t*)D;
+  a.offsets = offsets;
   a.out = out;
   a.B = B;
-  a.nd = nd;
+  a.nd = offsets ? 0 : nd;
+  a.T = T;
+  a.pad_len = pad_len;
   a.nq = (int32_t)nq;
   a.nbq = (int32_t)((nq + 31) / 32);
   a.d = (int32_t)d;
   const int64_t nblocks = nQ * (int64_t)a.nbq;
-  if (a.nbq <= kMaxBlocksPerWave && nblocks >= 4)  // batched: documents at implicit offsets b * nd
+  if (!offsets && a.nbq <= kMaxBlocksPerWave && nblocks >= 4)  // batched: documents at implicit offsets b * nd
     return run_varlen_batched(Q, nQ, nq, d, D, B * nd, nullptr, nd, B, 0, dtype, out, st, false);
-  int64_t dpw = nd > 0 ? TMS_STREAM_TOKENS_PER_WAVE / nd : 1;
+  const int64_t hint = offsets ? (B > 0 ? T / B : 1) : nd;  // tokens per document
+  int64_t dpw = hint > 0 ? TMS_STREAM_TOKENS_PER_WAVE / hint : 1;
   const int64_t min_waves = (int64_t)256 * 16 * 2;
   if (dpw > 1 && B / dpw < min_waves) dpw = B / min_waves;
   if (dpw < 1) dpw = 1;
