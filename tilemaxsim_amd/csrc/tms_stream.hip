@@ -287,7 +287,7 @@ struct RingSlotS {
 #define TMS_STREAM_PFD 2  // tiles in flight ahead of the one being scored (single-query path)
 #endif
 #ifndef TMS_STREAM_TOKENS_PER_WAVE
-#define TMS_STREAM_TOKENS_PER_WAVE 192
+#define TMS_STREAM_TOKENS_PER_WAVE 768  // document tokens one wave streams (rounded to whole documents)
 #endif
 
 template <int DT, int KS, int NB>
