@@ -373,6 +373,11 @@ class Varlen(Dense):
         offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
         self.T = int(offs[-1])
         self.lo, self.hi = lo, hi
+        # 16-bit documents with d in {32, 64, 96, 128} stream through the variable-length
+        # instantiation of the streaming kernel (queries held in registers); subclasses
+        # that run other kernels name them as class attributes
+        if self.kernel == "dense_maxsim_kernel" and d <= 128 and d % 32 == 0:
+            self.kernel = "stream_maxsim_kernel"
         gen = torch.Generator(device="cuda").manual_seed(4321)
         log(f"[bench] generating {B} varlen docs, {self.T} tokens x {d} fp16 ({self.T * d * 2 / 1e9:.2f} GB)")
         self.D = normalized_fp16(torch, (self.T, d), gen)
