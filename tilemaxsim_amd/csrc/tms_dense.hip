@@ -64,13 +64,25 @@ static int fill(float* out, int64_t n, float v, hipStream_t st) {
   return check_launch("fill");
 }
 
+#ifndef TMS_DENSE_F32_TOKENS_PER_WAVE
+#define TMS_DENSE_F32_TOKENS_PER_WAVE 768  // fp32 documents, d <= 128 (query in VGPRs)
+#endif
+#ifndef TMS_DENSE_F32_LDS_TOKENS_PER_WAVE
+#define TMS_DENSE_F32_LDS_TOKENS_PER_WAVE 384  // fp32 documents, wider rows
+#endif
+
 // Documents per wave: short waves (about TMS_DENSE_TOKENS_PER_WAVE tokens, i.e. one
 // document at typical ColBERT lengths) keep every CU's load pipeline full until the
 // end of the launch and let the dispatcher balance ragged documents; the grid still
 // spans at least two rounds of the chip's resident waves, and a wave never carries
-// fewer tokens than it spends loading its query fragments.
-static int pick_docs_per_wave(int64_t B, int64_t tokens_per_doc_hint) {
-  int64_t dpw = tokens_per_doc_hint > 0 ? TMS_DENSE_TOKENS_PER_WAVE / tokens_per_doc_hint : 1;
+// fewer tokens than it spends loading its query fragments. fp32 documents stream best
+// with longer waves (measured per query, 192 / 384 / 768 tokens: C2 in fp32 14.3 / 13.7
+// / 13.4 ms, C4 d = 768 in fp32 11.9 / 11.75 / 12.0 ms); 16-bit ones measured slower
+// with 384 or 768.
+static int pick_docs_per_wave(int64_t B, int64_t tokens_per_doc_hint, bool f32, int64_t d) {
+  const int64_t tpw = !f32 ? TMS_DENSE_TOKENS_PER_WAVE
+                           : (d <= 128 ? TMS_DENSE_F32_TOKENS_PER_WAVE : TMS_DENSE_F32_LDS_TOKENS_PER_WAVE);
+  int64_t dpw = tokens_per_doc_hint > 0 ? tpw / tokens_per_doc_hint : 1;
   const int64_t min_waves = (int64_t)256 * 16 * 2;
   if (dpw > 1 && B / dpw < min_waves) dpw = B / min_waves;
   if (dpw < 1) dpw = 1;
@@ -120,7 +132,7 @@ static int dense_entry(const char* fn, const void* Q, int64_t nQ, int64_t nq, in
   a.nkg = (int32_t)((a.nstep + 3) / 4);
   if (a.nkg < 1) a.nkg = 1;
   int64_t hint = (mode == MODE_VARLEN) ? (B > 0 ? total_tokens / B : 0) : nd;
-  a.docs_per_wave = pick_docs_per_wave(B, hint);
+  a.docs_per_wave = pick_docs_per_wave(B, hint, dtype == TMS_DTYPE_F32, d);
   a.pad_len = pad_len;
   a.mask4 = (nd % 4 == 0 && ((uintptr_t)mask & 3) == 0) ? 1 : 0;
   const bool aligned = (d % 8 == 0) && (((uintptr_t)Q & 15) == 0) && (((uintptr_t)D & 15) == 0);

@@ -16,17 +16,22 @@
 //    against one pass over D.
 //  * Each document token is read from HBM exactly once, straight into MFMA A-operand
 //    registers: lane (r = l%16, g = l/16) loads the 16-byte chunk 4*s + g of token
-//    r at k-step s. Four lanes cover 64 contiguous bytes of a token per instruction,
-//    which streams at the same rate as a fully coalesced copy on this part.
+//    r at k-step s. Four lanes cover 64 contiguous bytes of a token per instruction.
+//    Full, aligned tiles (16-bit d % 64 == 0, fp32 d % 32 == 0) instead read whole
+//    128-byte lines of eight rows per instruction with non-temporal loads, which stream
+//    faster on this part (about 7.0 against 6.3 TB/s), and rebuild the fragments with
+//    a DPP row rotate (line_frags).
 //  * A tile is 16*NSUB tokens x 128 dims; the next tile's loads are issued before the
 //    current tile's MFMAs (register double buffer). Tokens past the end of a
 //    document are clamped to its last token: a duplicate cannot change a max, so
 //    no -inf masking is needed and nothing outside the document is fetched.
 //  * The per-(query token, row) running max lives in the MFMA accumulator layout; the
 //    cross-lane max and the sum over query tokens happen once per document.
-//  * fp32 embeddings: a lane's 8-element chunk is 32 bytes (two 16-byte loads), split
-//    into bf16 hi and lo terms before the MFMAs, and each product is formed from three
-//    bf16 MFMAs (split_bf16 in tms_common.h); tiles are one 16-token block.
+//  * fp32 embeddings: a lane's 8 elements are 32 bytes (two 16-byte loads), split into
+//    bf16 hi and lo terms before the MFMAs, and each product is formed from three bf16
+//    MFMAs (split_bf16 in tms_common.h); tiles are one 16-token block with Q in VGPRs.
+//    Under whole-line loads a lane holds elements 4g..4g+3 and 16+4g..16+4g+3 of a
+//    32-dimension step, and the query fragments take the same elements.
 //  * fp32 queries against 16-bit documents: the query alone is split, into two terms of
 //    the document type, and a product takes two MFMAs.
 #pragma once
@@ -88,6 +93,16 @@ __device__ __forceinline__ typename Raw8<DT>::T load_chunk(const uint8_t* base, 
   return v;
 }
 
+// fp32 rows read as whole lines (LINES32 below): a k-step is one 128-byte line per row,
+// and line_frags leaves lane (r, g) with elements 4g .. 4g+3 and 16+4g .. 16+4g+3 of the
+// step's 32. The query fragments take the same elements, so each MFMA sums the same
+// products in another order over k. `step` < d / 32; d % 32 == 0, 16-byte aligned base.
+__device__ __forceinline__ u32x8 load_chunk_f32_lines(const uint8_t* base, int64_t row, int step, int g, int d) {
+  const uint32_t* p = (const uint32_t*)base + row * d + 32 * (int64_t)step + 4 * g;
+  const u32x4 a0 = *(const u32x4*)p, a1 = *(const u32x4*)(p + 16);
+  return u32x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+}
+
 struct Cursor {
   int64_t b;     // document index
   int64_t base;  // first token row of the document
@@ -128,6 +143,20 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g = lane >> 4;
   const int wid = threadIdx.x >> 6;
+  // LINES (16-bit rows, every 64-dimension pair of k-steps whole, d % 64 == 0) and LINES32
+  // (fp32 rows, every 32-dimension k-step whole; not with the query read from memory,
+  // whose extra loads spill there): each document load covers whole 128-byte lines of
+  // eight rows, non-temporal; line_frags turns two such loads into MFMA fragments when
+  // the tile is scored. Lane 16 g + 8 s + t reads bytes 64 s + 16 g of a line of row t
+  // or 8 + t.
+  constexpr bool LINES = FULL && ALIGNED && !F32 && KS % 2 == 0;
+  constexpr bool LINES32 = FULL && ALIGNED && F32 && !QGLB;
+  // query elements of fragment (row, step S, lane group gg): chunk 4 S + gg, or under
+  // LINES32 the elements its line_frags gives the documents' fragment
+  auto q_chunk = [&](int64_t row, int S, int gg) -> QRaw {
+    if constexpr (LINES32) return load_chunk_f32_lines(a.Q, row, S, gg, a.d);
+    else return load_chunk<QDT, ALIGNED>(a.Q, row, 4 * S + gg, a.d, a.nchunk);
+  };
 
   // Query blocks of this launch: [my_blk0, my_blk0 + my_nblk).
   const int my_blk0 = a.blk0, my_nblk = a.nblk;
@@ -168,7 +197,7 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
         float am = 0.f;
 #pragma unroll
         for (int s = 0; s < KS; s++) {
-          raw[s] = valid ? load_chunk<QDT, true>(a.Q, row, 4 * s + g, a.d, a.nchunk) : QRaw{};
+          raw[s] = valid ? q_chunk(row, s, g) : QRaw{};
           if constexpr (QSCALE) am = fmaxf(am, absmax8(raw[s]));
         }
         float sc = 1.f;
@@ -206,7 +235,7 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
         int S = rest % a.nstep, j = rest / a.nstep;
         bool valid;
         int64_t row = q_row(j, h, fl & 15, valid);
-        const QRaw raw = valid ? load_chunk<QDT, ALIGNED>(a.Q, row, 4 * S + (fl >> 4), a.d, a.nchunk) : QRaw{};
+        const QRaw raw = valid ? q_chunk(row, S, fl >> 4) : QRaw{};
         float sc = 1.f;
         if constexpr (QSCALE) {
           float unused;
@@ -326,11 +355,6 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
     uint32_t m[NSUB];  // masked mode: validity bits of this lane's 4 output rows
     QRaw q[QGLB ? NQB : 1][QGLB ? KS : 1][2];  // memory-resident Q: the k-group's query chunks
   };
-  // LINES (16-bit rows, every 64-dimension pair of k-steps whole, d % 64 == 0): each load
-  // covers whole 128-byte lines of eight rows, non-temporal; line_frags turns a line's two
-  // loads into its two k-steps' fragments when the tile is scored. Lane 16 g + 8 s + t
-  // reads bytes 64 s + 16 g of a line of row t or 8 + t.
-  constexpr bool LINES = FULL && ALIGNED && !F32 && KS % 2 == 0;
   const int t8 = lane & 7;
   const int64_t line_off = 64 * ((lane >> 3) & 1) + 16 * g;
   auto load_tile = [&](Buf& buf, const Cursor& c) {
@@ -344,8 +368,7 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
 #pragma unroll
           for (int s = 0; s < KS; s++) {
             const int S = c.kg * KS + s;
-            buf.q[j][s][h] = (valid && S < a.nstep) ? load_chunk<QDT, ALIGNED>(a.Q, row, 4 * S + g, a.d, a.nchunk)
-                                                    : QRaw{};
+            buf.q[j][s][h] = (valid && S < a.nstep) ? q_chunk(row, S, g) : QRaw{};
           }
         }
     }
@@ -364,6 +387,23 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
           } else {
             buf.f[sub][2 * i] = ld_stream<u32x4, true>(p0 + 128 * i);
             buf.f[sub][2 * i + 1] = ld_stream<u32x4, true>(p1 + 128 * i);
+          }
+        }
+      } else if constexpr (LINES32) {  // f[sub][s]: line S of rows t (elements 0-3) and 8 + t (4-7)
+        int64_t t0 = c.t0 + 16 * sub + t8, t1 = t0 + 8;
+        if (t0 > c.len - 1) t0 = c.len - 1;
+        if (t1 > c.len - 1) t1 = c.len - 1;
+        const uint8_t* p0 = a.D + (c.base + t0) * a.d * 4 + line_off;
+        const uint8_t* p1 = a.D + (c.base + t1) * a.d * 4 + line_off;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+          const int S = c.kg * KS + s;
+          if (!QREG && S >= a.nstep) {
+            buf.f[sub][s] = Raw{};
+          } else {
+            const u32x4 x0 = ld_stream<u32x4, true>(p0 + 128 * (int64_t)S);
+            const u32x4 x1 = ld_stream<u32x4, true>(p1 + 128 * (int64_t)S);
+            buf.f[sub][s] = Raw{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
           }
         }
       } else {
@@ -466,6 +506,18 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
       if constexpr (LINES) return lf[sub][s];
       else return buf.f[sub][s];
     };
+    // fp32: the 8 elements of row r this lane scores at step s (LINES32: rebuilt from the
+    // two row halves' whole-line loads)
+    auto F32frag = [&](int sub, int s) -> Raw {
+      if constexpr (LINES32) {
+        const Raw& x = buf.f[sub][s];
+        u32x4 k0, k1;
+        line_frags(u32x4{x[0], x[1], x[2], x[3]}, u32x4{x[4], x[5], x[6], x[7]}, k0, k1);
+        return Raw{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+      } else {
+        return buf.f[sub][s];
+      }
+    };
     if constexpr (QREG) {
       // One k-group: each query block is finished before the next, so only one
       // block's accumulators are live (what lets a wave hold several blocks).
@@ -481,7 +533,7 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
 #pragma unroll
             for (int sub = 0; sub < NSUB; sub++) {
               u32x4 dh, dl;
-              split_bf16(F(sub, s), dh, dl);
+              split_bf16(F32frag(sub, s), dh, dl);
 #pragma unroll
               for (int h = 0; h < 2; h++) {
                 acc1[sub][h] = mfma16x16x32<MDT>(dl, qf[j][s][h], acc1[sub][h]);
@@ -520,7 +572,7 @@ __global__ void __launch_bounds__(NT, 1) dense_maxsim_kernel(DenseArgs a) {
       u32x4 dh[NSUB], dl[F32 ? NSUB : 1];
 #pragma unroll
       for (int sub = 0; sub < NSUB; sub++) {
-        if constexpr (F32) split_bf16(F(sub, s), dh[sub], dl[sub]);
+        if constexpr (F32) split_bf16(F32frag(sub, s), dh[sub], dl[sub]);
         else dh[sub] = F(sub, s);
       }
 #pragma unroll

@@ -286,6 +286,9 @@ struct RingSlotS {
 #ifndef TMS_STREAM_PFD
 #define TMS_STREAM_PFD 2  // tiles in flight ahead of the one being scored (single-query path)
 #endif
+#ifndef TMS_STREAM_MIN_WAVES
+#define TMS_STREAM_MIN_WAVES (256 * 16 * 2)  // fewer documents per wave below this many waves
+#endif
 #ifndef TMS_STREAM_TOKENS_PER_WAVE
 #define TMS_STREAM_TOKENS_PER_WAVE 768  // document tokens one wave streams (rounded to whole documents)
 #endif
@@ -854,7 +857,7 @@ int run_stream(const void* Q, int64_t nQ, int64_t nq, int64_t d, const void* D, 
     return run_varlen_batched(Q, nQ, nq, d, D, B * nd, nullptr, nd, B, 0, dtype, out, st, false);
   const int64_t hint = offsets ? (B > 0 ? T / B : 1) : nd;  // tokens per document
   int64_t dpw = hint > 0 ? TMS_STREAM_TOKENS_PER_WAVE / hint : 1;
-  const int64_t min_waves = (int64_t)256 * 16 * 2;
+  const int64_t min_waves = TMS_STREAM_MIN_WAVES;
   if (dpw > 1 && B / dpw < min_waves) dpw = B / min_waves;
   if (dpw < 1) dpw = 1;
   if (dpw > 64) dpw = 64;
