@@ -110,6 +110,52 @@ def test_dense_unaligned_width(cuda, d):
     _assert_scores(got, *_oracle(orc.maxsim_f64, Q, D, what=f"d={d}"))
 
 
+@pytest.mark.parametrize("dt,d,mode", [("fp16", 128, "fixed"), ("bf16", 64, "fixed"), ("fp16", 256, "fixed"),
+                                       ("fp16", 128, "varlen"), ("fp32", 128, "fixed"), ("fp32", 256, "fixed"),
+                                       ("fp32", 128, "varlen")])
+def test_whole_line_loads_at_16_byte_offsets(cuda, dt, d, mode):
+    """The whole-line document loads (16-bit rows at d % 64 == 0, fp32 rows at
+    d % 32 == 0) from documents that start 16 bytes past a 128-byte line, so that every
+    load straddles two lines: the scores equal, bit for bit, those of the same documents
+    at an aligned address, and the oracle's within the bar."""
+    import torch
+    from tilemaxsim_amd import flash_maxsim_multi_doc, flash_maxsim_v2_multiquery
+    tdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dt]
+    rng = _rng(d + len(mode) + len(dt))
+    Q = _randn(rng, (32, d), True, np.float32)
+    if mode == "fixed":
+        D = _randn(rng, (40, 45, d), True, np.float32)
+        lens = None
+    else:
+        lens = rng.integers(0, 70, size=40)
+        lens[3] = 0
+        D = _randn(rng, (int(lens.sum()), d), True, np.float32)
+    # the values each dtype holds, so that the oracle sees what the kernel reads
+    Qt = torch.from_numpy(Q).to(tdt)
+    Dt = torch.from_numpy(D).to(tdt)
+    Qn, Dn = Qt.float().numpy(), Dt.float().numpy()
+    pad = 16 // Dt.element_size()
+    buf = torch.empty(Dt.numel() + pad, dtype=tdt, device="cuda")
+    Dv = buf[pad:].view(Dt.shape)
+    Dv.copy_(Dt)
+    Da = Dt.cuda()
+    assert Dv.data_ptr() % 128 == 16 and Da.data_ptr() % 128 == 0
+    Qg = Qt.cuda()
+    if mode == "fixed":
+        got, ref_al = flash_maxsim_v2_multiquery(Qg, Dv), flash_maxsim_v2_multiquery(Qg, Da)
+        fn = orc.maxsim_f64
+    else:
+        offs = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int64))
+        got, ref_al = flash_maxsim_multi_doc(Qg, Dv, offs), flash_maxsim_multi_doc(Qg, Da, offs)
+        fn = lambda q, x: orc.maxsim_varlen(q, x, offs.numpy(), f64=True)  # noqa: E731
+    assert torch.equal(got.view(torch.int32), ref_al.view(torch.int32)), f"{dt} d={d} {mode}"
+    ref, absref = fn(Qn, Dn), fn(np.abs(Qn), np.abs(Dn))
+    absref = np.where(np.isfinite(absref), absref, 0.0)
+    # fp32: products of bf16 hi + lo terms, the fp32 bar of test_gpu_fp32.py
+    lim = (4 * 2.0 ** -16 + d * 2.0 ** -24) * absref + 1e-6 if dt == "fp32" else bar.rel(d, 32) * absref + 1e-30
+    _assert_scores(got.cpu().numpy(), ref, what=f"{dt} d={d} {mode}", lim=lim)
+
+
 def test_dense_misaligned_pointer(cuda):
     """A contiguous view that starts 2 bytes into its storage (not 16-byte aligned)."""
     import torch
