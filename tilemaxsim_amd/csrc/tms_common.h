@@ -21,9 +21,10 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 #endif
 // A load of streamed document data (tokens, codes: read once per pass). WHOLE: the
 // wave's load covers whole 128-byte lines, and is then non-temporal, so the caches treat
-// the lines as a stream. A read-only pass over 46 GB measured 6.74-6.78 TB/s with such
-// loads against 6.01-6.32 TB/s with plain ones; non-temporal loads that cover half of each
-// line (the other half read by a later load) measured 5.53 TB/s, so those stay plain.
+// the lines as a stream. A read-only pass over 46 GB measured 6.74-7.08 TB/s with such
+// loads against 6.01-6.34 TB/s with plain ones (the cache-coherence bits sc0 / sc1 change
+// neither); non-temporal loads that cover half of each line (the other half read by a
+// later load) measured 5.53 TB/s, so those stay plain.
 template <class T, bool WHOLE>
 __device__ __forceinline__ T ld_stream(const void* p) {
 #if TMS_STREAM_NT

@@ -7,9 +7,10 @@
 // wave-iteration 8 independent 16-byte loads per lane (64 lanes x 16 B x 8 contiguous,
 // non-temporal: each load covers whole 128-byte lines);
 // the workgroups dispatched to one XCD (blockIdx % 8) take a contiguous range of block
-// ids, which was the fastest of the mappings tried (contiguous runs per wave, grid-stride
-// at 1x and 2x the resident grid, 4 / 8 / 16 KiB per iteration: 6.10-6.30 TB/s over a
-// 46 GB buffer).
+// ids. With plain loads this was the fastest of the mappings tried (contiguous runs per
+// wave, grid-stride at 1x and 2x the resident grid, 4 / 8 / 16 KiB per iteration:
+// 6.10-6.30 TB/s over a 46 GB buffer); with non-temporal loads every such shape, and a
+// one-shot grid of one chunk per wave, reads 6.9-7.1 TB/s.
 #include "tms_common.h"
 
 namespace tms {
