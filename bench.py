@@ -67,8 +67,8 @@ def parse():
                    help="--config c2b: fp32 queries against the --dtype documents (split, never rounded)")
     p.add_argument("--ncent", type=int, default=1 << 18,
                    help="--config c6 / c6b: centroids in the index (2^18, ColBERT's choice for ~332M tokens)")
-    p.add_argument("--lds-pattern", type=int, default=None, choices=range(8),
-                   help="--config ldsprobe: time this pattern alone (default: pattern 1 timed, all eight reported)")
+    p.add_argument("--lds-pattern", type=int, default=None, choices=range(10),
+                   help="--config ldsprobe: time this pattern alone (default: pattern 1 timed, all ten reported)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     return p.parse_args()
@@ -850,8 +850,10 @@ class LdsProbe:
     rows of one codebook subspace as the PQ kernel's gathers do (pattern 1, the timed
     one), when they all hit one bank group (pattern 2), and when each bank group gets
     four lanes of every 16 (pattern 3); patterns 4 to 7 repeat them at the PQ kernel's
-    occupancy and footprint (two 8-wave workgroups per CU, 64 KiB each). ``--lds-pattern``
-    times one pattern alone (for counter runs). LDS bytes, not HBM bytes."""
+    occupancy and footprint (two 8-wave workgroups per CU, 64 KiB each), and patterns 8
+    and 9 repeat 5 and 4 with the PQ kernel's matrix work beside the gathers (two MFMAs
+    per gathered fragment, random fp16 data). ``--lds-pattern`` times one pattern alone
+    (for counter runs). LDS bytes, not HBM bytes."""
     kernel = "lds_probe_kernel"
     _P = {0: "conflict-free (lane l -> bank group l % 16, random rows)",
           1: "PQ codebook gather (one subspace per 16-lane group, random codes)",
@@ -859,7 +861,9 @@ class LdsProbe:
           3: "lane l -> bank group (l / 4) % 16: balanced over the wave, 4-way within 16 lanes"}
     PATTERNS = {**{p: f"{w}; one 16-wave workgroup per CU, 128 KiB" for p, w in _P.items()},
                 **{p + 4: f"{w}; two 8-wave workgroups per CU, 64 KiB each (the PQ kernel's shape)"
-                   for p, w in _P.items()}}
+                   for p, w in _P.items()},
+                8: f"{_P[1]}; the PQ kernel's shape, two MFMAs per gathered fragment",
+                9: f"{_P[0]}; the PQ kernel's shape, two MFMAs per gathered fragment"}
 
     def __init__(self, torch, pattern=None):
         self.pattern = pattern
@@ -886,7 +890,8 @@ class LdsProbe:
 
     def config(self):
         return {"workload": "ldsprobe: 4,096 waves x 65,536 ds_read_b128 per wave, 16 waves per CU (one "
-                            "workgroup over 128 KiB, or two over 64 KiB each), four lane -> address patterns",
+                            "workgroup over 128 KiB, or two over 64 KiB each), four lane -> address patterns, "
+                            "and two of them with MFMAs beside the gathers",
                 "pattern": self.pattern}
 
     def cpu_baseline(self, seconds):

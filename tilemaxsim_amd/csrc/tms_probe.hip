@@ -70,6 +70,9 @@ extern "C" int tms_read_probe(const void* buf, int64_t bytes, uint32_t* sink, in
 //   2: the 16 lanes of a lane group all read one bank group at random rows;
 //   3: lane l -> bank group (l / 4) % 16 at random rows: every bank group gets exactly
 //      four lanes of the wave, but four lanes of each 16-lane group share one.
+// Patterns 8 and 9 run patterns 1 and 0 at the PQ kernel's shape with the PQ kernel's
+// matrix work beside the gathers (two MFMAs per gathered fragment, random fp16 data):
+// the gather rate this part holds under that mix, with no HBM traffic.
 namespace tms {
 
 constexpr int kLdsProbeUnits = 8192;  // 16-byte units (128 KiB)
@@ -85,13 +88,27 @@ __device__ __forceinline__ uint32_t probe_hash(uint32_t x) {
   return x;
 }
 
+// fp16 bits of a value in +-[0.5, 1) with random sign and mantissa, two per word
+__device__ __forceinline__ uint32_t probe_halves(uint32_t h) {
+  return (h & 0x83ff83ffu) | 0x38003800u;
+}
+
 // NT threads a workgroup over UNITS 16-byte units of LDS; waves are numbered across the
 // grid (blockIdx.x * NT / 64 + wave), so every launch shape has TMS_LDS_PROBE_WAVES waves.
-template <int NT, int UNITS>
+// MIX: the LDS holds random fp16 values, and every gathered fragment feeds two
+// v_mfma_f32_16x16x32_f16 against random fp16 fragments held in registers (the PQ
+// kernel's 64 MFMAs per 32 gathers, on data of the same kind), eight accumulators per wave.
+template <int NT, int UNITS, bool MIX>
 __global__ void __launch_bounds__(NT) lds_probe_kernel(int pattern, int64_t* __restrict__ cycles,
                                                        uint32_t* __restrict__ sink) {
   extern __shared__ u32x4 probe_lds[];
-  for (int i = threadIdx.x; i < UNITS; i += NT) probe_lds[i] = u32x4{(uint32_t)i, 1u, 2u, 3u};
+  for (int i = threadIdx.x; i < UNITS; i += NT) {
+    if constexpr (MIX)
+      probe_lds[i] = u32x4{probe_halves(probe_hash(4u * i)), probe_halves(probe_hash(4u * i + 1u)),
+                           probe_halves(probe_hash(4u * i + 2u)), probe_halves(probe_hash(4u * i + 3u))};
+    else
+      probe_lds[i] = u32x4{(uint32_t)i, 1u, 2u, 3u};
+  }
   constexpr int kWaves = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int gw = blockIdx.x * kWaves + wave;  // < TMS_LDS_PROBE_WAVES
@@ -108,15 +125,41 @@ __global__ void __launch_bounds__(NT) lds_probe_kernel(int pattern, int64_t* __r
   }
   __syncthreads();
   u32x4 acc = {0u, 0u, 0u, 0u};
+  f32x4 macc[MIX ? 8 : 1];
+  u32x4 qb[MIX ? 2 : 1];
+  if constexpr (MIX) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) macc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const uint32_t s0 = (uint32_t)(gw * 64 + lane) * 8u + 4u * h;
+      qb[h] = u32x4{probe_halves(probe_hash(s0)), probe_halves(probe_hash(s0 + 1u)), probe_halves(probe_hash(s0 + 2u)),
+                    probe_halves(probe_hash(s0 + 3u))};
+    }
+  }
   const uint64_t t0 = __builtin_readcyclecounter();
   for (int it = 0; it < kLdsProbeIters; it++) {
 #pragma unroll
-    for (int j = 0; j < kLdsProbeOffs; j++) acc ^= probe_lds[o[j]];
+    for (int j = 0; j < kLdsProbeOffs; j++) {
+      if constexpr (MIX) {
+        const u32x4 f = probe_lds[o[j]];
+        macc[2 * (j & 3)] = mfma16x16x32<TMS_DTYPE_F16>(f, qb[0], macc[2 * (j & 3)]);
+        macc[2 * (j & 3) + 1] = mfma16x16x32<TMS_DTYPE_F16>(f, qb[1], macc[2 * (j & 3) + 1]);
+      } else {
+        acc ^= probe_lds[o[j]];
+      }
+    }
 #pragma unroll
     for (int j = 0; j < kLdsProbeOffs; j++) asm volatile("" : "+v"(o[j]));  // keeps the loads in the loop
   }
   const uint64_t t1 = __builtin_readcyclecounter();
   if (lane == 0) cycles[gw] = (int64_t)(t1 - t0);
+  if constexpr (MIX) {
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) sum += macc[i][0] + macc[i][1] + macc[i][2] + macc[i][3];
+    acc[0] = __builtin_bit_cast(uint32_t, sum);
+  }
   sink[gw * 64 + lane] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
@@ -125,17 +168,20 @@ __global__ void __launch_bounds__(NT) lds_probe_kernel(int pattern, int64_t* __r
 extern "C" int tms_lds_probe(int pattern, int64_t* cycles, int64_t cycle_words, uint32_t* sink, int64_t sink_words,
                              void* stream) {
   const char* fn = "tms_lds_probe";
-  if (pattern < 0 || pattern > 7) return fail(TMS_ERR_INVALID, "%s: pattern=%d must be 0 to 7", fn, pattern);
+  if (pattern < 0 || pattern > 9) return fail(TMS_ERR_INVALID, "%s: pattern=%d must be 0 to 9", fn, pattern);
   if (!cycles || cycle_words < TMS_LDS_PROBE_WAVES)
     return fail(TMS_ERR_INVALID, "%s: cycles needs %d words", fn, TMS_LDS_PROBE_WAVES);
   if (!sink || sink_words < TMS_LDS_PROBE_WAVES * 64)
     return fail(TMS_ERR_INVALID, "%s: the sink needs %d words", fn, TMS_LDS_PROBE_WAVES * 64);
   if (pattern < 4)  // one 16-wave workgroup per CU over 128 KiB
-    hipLaunchKernelGGL((lds_probe_kernel<1024, kLdsProbeUnits>), dim3(TMS_LDS_PROBE_WAVES / 16), dim3(1024),
+    hipLaunchKernelGGL((lds_probe_kernel<1024, kLdsProbeUnits, false>), dim3(TMS_LDS_PROBE_WAVES / 16), dim3(1024),
                        kLdsProbeUnits * 16, (hipStream_t)stream, pattern, cycles, sink);
-  else  // the PQ kernel's shape: two 8-wave workgroups per CU, 64 KiB each
-    hipLaunchKernelGGL((lds_probe_kernel<512, kLdsProbeUnits / 2>), dim3(TMS_LDS_PROBE_WAVES / 8), dim3(512),
+  else if (pattern < 8)  // the PQ kernel's shape: two 8-wave workgroups per CU, 64 KiB each
+    hipLaunchKernelGGL((lds_probe_kernel<512, kLdsProbeUnits / 2, false>), dim3(TMS_LDS_PROBE_WAVES / 8), dim3(512),
                        kLdsProbeUnits * 8, (hipStream_t)stream, pattern - 4, cycles, sink);
+  else  // 8: the PQ gather (1), 9: conflict-free (0), each with two MFMAs per gathered fragment
+    hipLaunchKernelGGL((lds_probe_kernel<512, kLdsProbeUnits / 2, true>), dim3(TMS_LDS_PROBE_WAVES / 8), dim3(512),
+                       kLdsProbeUnits * 8, (hipStream_t)stream, pattern == 8 ? 1 : 0, cycles, sink);
   return check_launch("lds_probe_kernel");
 }
 
