@@ -124,11 +124,13 @@ __global__ void __launch_bounds__(256, 1) stream_maxsim_kernel(StreamArgs a) {
   if (VARLEN || a.nd > 0) {
     const int64_t tpd = doc_tiles(a.nd);  // fixed length: tiles per document
     int64_t total;                        // tiles of the wave's documents
-    if constexpr (VARLEN) {
-      int32_t n = lane < ndocs ? (int32_t)doc_tiles(dlen) : 0;
+    if constexpr (VARLEN) {  // 64-bit: documents may overlap, each up to 2^31 rows
+      int64_t n = lane < ndocs ? doc_tiles(dlen) : 0;
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o);
-      total = (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)n);
+      const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)n);
+      const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)n >> 32));
+      total = (int64_t)(((uint64_t)hi << 32) | lo);
     } else {
       total = ndocs * tpd;
     }
