@@ -1,5 +1,5 @@
-"""Parity at the benchmark workloads' full sizes (C2-C5 with c2b/c3b/c5b, c6/c6b, top-k
-over C2's score matrix).
+"""Parity at the benchmark workloads' full sizes (C2-C5 with c2b/c3b/c5b, C2 in fp32,
+c6/c6b, top-k over C2's score matrix).
 
 Every score of C2 (64 queries x 1M docs), C3 (32 queries x 2M varlen docs), C4 (16
 queries x 200K docs at d = 256, 512 and 768) and C5 (32 queries x 5M PQ docs) is
@@ -175,6 +175,48 @@ def test_c2_dense_and_batched_fullsize(cuda):
         bar.assert_scores(single[q].cpu().numpy()[idx], *bar.with_bound(orc.maxsim_f64, Qs[q].cpu().numpy(), Dcpu),
                           f"C2 sample q={q}")
     del D, single, batched, ref, absref
+    _release(torch)
+
+
+def _normal_fp32(torch, shape, seed, chunk=1 << 21):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    out = torch.empty(shape, dtype=torch.float32, device="cuda")
+    flat = out.view(-1, shape[-1])
+    for s in range(0, flat.shape[0], chunk):
+        e = min(flat.shape[0], s + chunk)
+        flat[s:e] = torch.nn.functional.normalize(torch.randn(e - s, shape[-1], device="cuda", generator=g), dim=-1)
+    return out
+
+
+def test_c2_fp32_fullsize(cuda):
+    """C2 in fp32 (1M docs x Nd=180 x d=128: 92 GB, `bench.py --config c2 --dtype fp32`):
+    16 queries, each through the per-query kernel (fp32 documents read as whole lines,
+    split into bf16 hi + lo terms, three MFMAs per product), every score against the
+    fp32 restatement to the fp32 bar of test_gpu_fp32.py, (4 * 2^-16 + d * 2^-24) *
+    MaxSim(|Q|, |D|), plus the restatement's own fp32-accumulation error."""
+    import torch
+    from tilemaxsim_amd import flash_maxsim_v2_multiquery
+    D = _normal_fp32(torch, (1_000_000, 180, 128), 13)
+    Qs = _normal_fp32(torch, (16, 32, 128), 14)
+    got = torch.stack([flash_maxsim_v2_multiquery(Qs[q], D) for q in range(16)])
+    ref = _ref_fixed(torch, Qs, D)
+    absref = _ref_fixed(torch, Qs.abs(), D, absolute=True)
+    err = (got - ref).abs()
+    lim = (4 * 2.0 ** -16 + 128 * 2.0 ** -24 + bar.rel(128, 32)) * absref
+    print(f"C2 fp32: {got.numel()} scores, max |delta| {err.max().item():.3e}, "
+          f"max |delta| / bar {(err / lim).max().item():.3f}", flush=True)
+    bad = int((err > lim).sum().item())
+    assert bad == 0, f"C2 fp32: {bad} scores outside the fp32 bar"
+    _check_top100(torch, got, ref, "C2 fp32 per-query")
+    idx = _sample(1_000_000, 60, 3)
+    Dcpu = D[torch.from_numpy(idx).cuda()].cpu().numpy()
+    for q in (0, 15):
+        Q = Qs[q].cpu().numpy()
+        ref64 = orc.maxsim_f64(Q, Dcpu)
+        abs64 = orc.maxsim_f64(np.abs(Q), np.abs(Dcpu))
+        g = got[q].cpu().numpy()[idx].astype(np.float64)
+        assert np.all(np.abs(g - ref64) <= (4 * 2.0 ** -16 + 128 * 2.0 ** -24) * abs64 + 1e-6), f"C2 fp32 sample q={q}"
+    del D, got, ref, absref
     _release(torch)
 
 
