@@ -1,5 +1,5 @@
-"""Parity at the benchmark workloads' full sizes (C2-C5 with c2b/c3b/c5b, C2 in fp32,
-c6/c6b, top-k over C2's score matrix).
+"""Parity at the benchmark workloads' full sizes (C2-C5 with c2b/c3b/c5b, C2 in fp32, C3
+in bf16, c6/c6b, top-k over C2's score matrix).
 
 Every score of C2 (64 queries x 1M docs), C3 (32 queries x 2M varlen docs), C4 (16
 queries x 200K docs at d = 256, 512 and 768) and C5 (32 queries x 5M PQ docs) is
@@ -248,6 +248,28 @@ def test_c3_varlen_fullsize(cuda):
                           *bar.with_bound(orc.maxsim_varlen, Qs[q].cpu().numpy(), sub, sub_offs, f64=True),
                           f"C3 sample q={q}")
     del D, single, batched, ref, absref
+    _release(torch)
+
+
+def test_c3_bf16_fullsize(cuda):
+    """C3's 332M-token corpus in bf16 (85 GB), 8 queries through the variable-length
+    stream kernel (bf16 rows read as whole lines): every score against the fp32
+    restatement, to the fp32-accumulation bar and the north star's 1e-3."""
+    import torch
+    from tilemaxsim_amd import flash_maxsim_multi_doc
+    rng = np.random.default_rng(78)
+    lens = rng.integers(32, 301, size=2_000_000)
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    D = _normal_fp16(torch, (int(offs[-1]), 128), 23).to(torch.bfloat16)
+    _release(torch)
+    Qs = _normal_fp16(torch, (8, 32, 128), 24).to(torch.bfloat16)
+    offs_t = torch.from_numpy(offs).cuda()
+    got = torch.stack([flash_maxsim_multi_doc(Qs[q], D, offs_t, validate=False) for q in range(8)])
+    ref = _ref_varlen(torch, Qs, D, offs_t)
+    absref = _ref_varlen(torch, Qs.abs(), D, offs_t, absolute=True)
+    _check_all(torch, got, ref, "C3 bf16 per-query varlen stream kernel", absref, 128, 32)
+    _check_top100(torch, got, ref, "C3 bf16 per-query")
+    del D, got, ref, absref
     _release(torch)
 
 
