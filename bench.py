@@ -620,10 +620,13 @@ class PQ:
 
     def extra_roofline(self, launch_ms):
         """Beside the code-bytes roofline: the reference's own PQ IO formula
-        (src/benchmark.py:226: table + codes + output), the LDS roof of this kernel's
-        codebook gather (16 B per code per token, against 128 B/clk/CU x 256 CUs at
-        2.4 GHz = 78.6 TB/s), and the MFMA rate of scoring the decoded tokens beside an
-        fp16 GEMM measured in the same process."""
+        (src/benchmark.py:226: table + codes + output), the LDS rate of this kernel's
+        codebook gather (16 B per code per token) against the LDS peak for
+        ds_read_b128 (256 B/clk/CU x 256 CUs at 2.4 GHz = 157.3 TB/s: a conflict-free
+        wave-instruction of 1 KiB takes 4 LDS cycles, tms_lds_probe pattern 0) and
+        against the PQ gather pattern's own ceiling at that clock (12 LDS cycles per
+        wave-instruction, pattern 1: 52.4 TB/s), and the MFMA rate of scoring the decoded
+        tokens beside an fp16 GEMM measured in the same process."""
         ref_bytes = self.Nq * self.M * self.K * 4 + self.B * self.Nd * self.M + self.B * self.Nq * 4
         lds_bytes = self.B * self.Nd * self.M * 16
         lds_tbs = lds_bytes / (launch_ms * 1e-3) / 1e12
@@ -633,7 +636,8 @@ class PQ:
         out = {"bytes_reference_formula": ref_bytes,
                "gbs_reference_formula": round(ref_bytes / (launch_ms * 1e-3) / 1e9, 1),
                "lds_gather_bytes_per_launch": lds_bytes, "lds_gather_tbs": round(lds_tbs, 2),
-               "lds_peak_tbs": 78.6, "lds_frac": round(lds_tbs / 78.6, 4),
+               "lds_peak_tbs": 157.3, "lds_frac": round(lds_tbs / 157.3, 4),
+               "lds_pq_pattern_ceiling_tbs": 52.4, "lds_frac_of_pattern_ceiling": round(lds_tbs / 52.4, 4),
                "mfma_flops_per_launch": flops, "mfma_tflops": round(mfma_tf, 1)}
         out.update(gemm_ceiling(self.torch, mfma_tf))
         out.update(self.table_gather_line())
