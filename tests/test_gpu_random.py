@@ -9,12 +9,19 @@ against the oracle on the same rounded values, 1e-3 relative (+1e-3 absolute) an
 fp32-accumulation bar of ``accum_bar.py``; for fp32 inputs (and for fp32 queries against
 fp16 / bf16 documents, which are split, not rounded) the split-product bound of
 ``test_gpu_fp32.py``; -inf exactly where the oracle has it.
+
+``TMS_RANDOM_SEEDS=N`` (default 160) widens the sweep: N seeds of the main case, 3N/8 of
+the split-query case and 9N/40 of the PQ case.
 """
+import os
+
 import numpy as np
 import pytest
 
 import accum_bar as bar
 from oracle import maxsim_oracle as orc
+
+N_SEEDS = int(os.environ.get("TMS_RANDOM_SEEDS", "160"))
 
 pytestmark = pytest.mark.gpu
 
@@ -73,7 +80,7 @@ def _emb(rng, shape, norm):
 
 
 @pytest.mark.parametrize("path", ["small_batch", "streaming"])
-@pytest.mark.parametrize("seed", range(160))
+@pytest.mark.parametrize("seed", range(N_SEEDS))
 def test_random_case(cuda, seed, path):
     """Each case with the small-batch kernel taking every call it can, and with it off."""
     from tilemaxsim_amd import _lib
@@ -133,7 +140,7 @@ def _random_case(seed):
         _check(got, ref, orc.maxsim_packed_zero_padded(np.abs(Qx), np.abs(Dx), lens), "fp16", d, what, nq)
 
 
-@pytest.mark.parametrize("seed", range(60))
+@pytest.mark.parametrize("seed", range(N_SEEDS * 3 // 8))
 def test_random_split_query_case(cuda, seed):
     """fp32 queries against fp16 / bf16 documents (never rounded: split into two terms of
     the documents' type), one and several queries, fixed-length and variable-length
@@ -173,7 +180,7 @@ PQ_SHAPES = [  # (M, K, dsub)
 ]
 
 
-@pytest.mark.parametrize("seed", range(36))
+@pytest.mark.parametrize("seed", range(N_SEEDS * 9 // 40))
 def test_random_pq_case(cuda, seed):
     """PQ: shapes that take the MFMA kernel and shapes that take the table path, every
     codebook dtype, both methods where the shape allows, against decompress-then-score
