@@ -57,6 +57,18 @@ against it.
 ``b`` is index rows ``[offsets[p], offsets[p+1])`` with ``p = pids[b]``. It follows the
 PLAID drop-in's semantics (``maxsim_oracle.maxsim_packed_zero_padded`` for
 ``pad_len > 0``, plain varlen MaxSim otherwise).
+
+:func:`maxsim_residual_kernel_envelope` restates, with the same semantics, the
+arithmetic of this build's two residual MaxSim kernels, which do not round ``v / n`` to
+fp16 the way the codec's decompression does (the single-query kernel scales
+``<q, v>`` by ``1 / n``; the batched kernel rounds ``fp16(v * (1 / n))``), as an
+interval that holds both fp16 norms a kernel's fp32 sum of squares can round to
+(:func:`norm_candidates`). It is pinned in ``tests/test_oracle_residual.py`` by closed
+forms (a (3, 4, 0, ...) token in both forms), by fp32 simulations of both kernels with
+the squares summed in random orders (each inside the envelope and its accumulation
+bar; 24 orders over 6,000 tokens always land on one of the two norms, and a zero-width
+envelope is caught), and by the fused form differing from the codec's scores by more
+than that bar.
 """
 from __future__ import annotations
 
@@ -182,6 +194,69 @@ def maxsim_residual(Q, codes, residuals, centroids, bucket_weights, nbits: int, 
             m = np.maximum(m, 0.0)
         out[i] = m.sum()
     return out
+
+
+def norm_candidates(V: np.ndarray):
+    """The fp16 norms a kernel can form from fp16 rows ``V`` (T, d): ``fp16(sqrt(n2))``
+    with ``n2`` an fp32 sum of the squares in any order and the square root rounded to
+    fp32, so ``sqrt(n2)`` lies within ``(d + 8) * 2^-24`` (relative) of the exact norm.
+    Returns float64 arrays ``(n_lo, n_hi)`` of fp16 values, equal wherever that interval
+    holds no fp16 rounding boundary, each clamped at the smallest positive fp16."""
+    v = np.asarray(V, dtype=np.float64)
+    s = np.sqrt((v * v).sum(axis=1))
+    eps = (v.shape[1] + 8) * 2.0 ** -24
+    tiny = float(np.float16(5.9604645e-8))
+    lo = np.maximum((s * (1.0 - eps)).astype(np.float16).astype(np.float64), tiny)
+    hi = np.maximum((s * (1.0 + eps)).astype(np.float16).astype(np.float64), tiny)
+    return lo, hi
+
+
+def maxsim_residual_kernel_envelope(Q, codes, residuals, centroids, bucket_weights, nbits: int, offsets,
+                                    pids=None, pad_len: int = 0, form: str = "fused"):
+    """float64 scores in the arithmetic of this build's residual MaxSim kernels, as
+    ``(lo, hi, absref)`` per scored document (semantics of :func:`maxsim_residual`).
+
+    Both kernels form ``v = fp16(centroid + weight)`` and ``inv = fp32(1 / n)`` with
+    ``n`` one of :func:`norm_candidates`' values. ``form="fused"`` (the single-query
+    kernel) scores ``<q, v> * inv``; ``form="batched"`` scores ``<q, x>`` with
+    ``x = fp16(fp32(v) * inv)``. Neither rounds ``v / n`` to fp16 the way the codec's
+    decompression does. Where a token's fp16 norm can fall either way, ``lo`` / ``hi``
+    take each product's smaller / larger value over the two norms, so an exact-arithmetic
+    kernel score lies in [lo, hi]. ``absref`` is the same MaxSim over absolute values
+    (the fp32-accumulation bar's reference)."""
+    V = decompress_unnormalised(codes, residuals, centroids, bucket_weights, nbits)
+    Qd = np.asarray(Q, dtype=np.float64)
+    n_lo, n_hi = norm_candidates(V)
+    Vd = V.astype(np.float64)
+    prods, aprods = [], []
+    for n in (n_lo, n_hi):
+        inv = (np.float32(1.0) / n.astype(np.float32)).astype(np.float64)
+        if form == "fused":
+            prods.append((Vd @ Qd.T) * inv[:, None])
+            aprods.append((np.abs(Vd) @ np.abs(Qd).T) * inv[:, None])
+        elif form == "batched":
+            X = (V.astype(np.float32) * inv.astype(np.float32)[:, None]).astype(np.float16).astype(np.float64)
+            prods.append(X @ Qd.T)
+            aprods.append(np.abs(X) @ np.abs(Qd).T)
+        else:
+            raise ValueError(f"form must be 'fused' or 'batched', got {form!r}")
+    pmin, pmax = np.minimum(prods[0], prods[1]), np.maximum(prods[0], prods[1])
+    amax = np.maximum(aprods[0], aprods[1])
+    rows = doc_rows(offsets, pids)
+    out = np.empty((3, len(rows)), dtype=np.float64)
+    for i, se in enumerate(rows):
+        if se is None or se[1] > V.shape[0]:
+            out[:, i] = np.nan
+            continue
+        s, e = se
+        if e == s:
+            out[:, i] = 0.0 if (pad_len > 0 and Qd.shape[0] > 0) else (-np.inf if Qd.shape[0] > 0 else 0.0)
+            continue
+        ms = [pmin[s:e].max(axis=0), pmax[s:e].max(axis=0), amax[s:e].max(axis=0)]
+        if pad_len > 0 and e - s < pad_len:
+            ms[0], ms[1] = np.maximum(ms[0], 0.0), np.maximum(ms[1], 0.0)
+        out[:, i] = [m.sum() for m in ms]
+    return out[0], out[1], out[2]
 
 
 def maxsim_residual_f32(Q, codes, residuals, centroids, bucket_weights, nbits: int, offsets, pids=None,

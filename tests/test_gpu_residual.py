@@ -4,8 +4,21 @@
   (same half add, fp32 norm, fp32 division) up to 1 fp16 ulp; only the fp32 summation
   order of the norm differs, and it can move a rounding boundary;
 * tms_maxsim_residual: |score - oracle| <= 1e-3 relative + 1e-3 absolute, the scoring
-  bar of every path; the oracle scores the decompressed fp16 tokens in float64.
+  bar of every path; the oracle scores the decompressed fp16 tokens in float64;
+* and, tighter, each kernel against its own arithmetic restated in float64
+  (``residual_oracle.maxsim_residual_kernel_envelope``): the single-query kernel scores
+  <q, v> / fp16(|v|) without rounding the normalised token to fp16, the batched kernel
+  rounds x = fp16(v * fp32(1 / fp16(|v|))); where a token's fp16 norm can round either
+  way (its fp32 sum of squares depends on the order) both are taken. The score must lie
+  in that envelope widened by the fp32-accumulation bar ``accum_bar.bound``.
+  Against the codec's decompress-then-score, a norm that rounds the other way rescales
+  a whole token by one fp16 ulp, and the unrounded token differs from the codec's by up
+  to half an ulp per element, so the seeded sweep's codec check adds 3 * 2^-11 *
+  MaxSim(|Q|, |X|) to the 1e-3 bar (a one-token document whose 64 query maxima cancel
+  to 0.08 moved by 1.1e-3 that way).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -47,6 +60,32 @@ def _index(rng, T, d, nbits, ncent):
 def _gpu(x):
     import torch
     return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _form(nQ, nq):
+    """The kernel tms_maxsim_residual_batched takes: the batched one for at most 4 query
+    blocks of 32 tokens per query and at least 2 blocks in all, else one query at a time."""
+    nbq = (nq + 31) // 32
+    return "batched" if nbq <= 4 and nQ * nbq >= 2 else "fused"
+
+
+def _assert_kernel(got, Q, idx_np, offsets, pids, pad_len, form, what=""):
+    """got within [lo, hi] of the kernel's own arithmetic, widened by the fp32-accumulation
+    bar (two more roundings for the multiply by 1 / |v|)."""
+    import accum_bar as bar
+    codes, res, C, w, nbits = idx_np
+    lo, hi, absref = ro.maxsim_residual_kernel_envelope(Q, codes, res, C, w, nbits, offsets, pids, pad_len, form=form)
+    got = np.asarray(got, dtype=np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(lo)), f"{what}: NaN pattern differs"
+    assert np.array_equal(np.isinf(got), np.isinf(lo)), f"{what}: inf pattern differs"
+    assert np.all(got[np.isinf(lo)] == lo[np.isinf(lo)]), what
+    fin = np.isfinite(lo)
+    b = bar.bound(absref, Q.shape[1] + 2, Q.shape[0])
+    below, above = got[fin] < lo[fin] - b[fin], got[fin] > hi[fin] + b[fin]
+    assert not below.any() and not above.any(), (
+        f"{what}: {int(below.sum() + above.sum())} scores outside the {form} envelope, worst "
+        f"{float(np.max(np.maximum(lo[fin] - got[fin], got[fin] - hi[fin]) / b[fin])):.2f} x the bar")
+    return absref
 
 
 def _assert_scores(got, ref, what=""):
@@ -141,6 +180,8 @@ def test_fused_maxsim_matches_oracle(cuda, fused_path, nbits, d, nq, padding):
     pad_len = int(lens.max()) if padding == "zeros" else 0
     ref = ro.maxsim_residual(Q, codes, res, C, w, nbits, offsets, None, pad_len)
     _assert_scores(got, ref, f"nbits={nbits} d={d} nq={nq} {padding}")
+    _assert_kernel(got, Q, (codes, res, C, w, nbits), offsets, None, pad_len, "fused",
+                   f"nbits={nbits} d={d} nq={nq} {padding}")
 
 
 @pytest.mark.parametrize("nbits,d", [(1, 128), (2, 128), (4, 128), (2, 64), (4, 64), (1, 32), (2, 96)])
@@ -334,6 +375,8 @@ def test_batched_maxsim_matches_oracle(cuda, nQ, nq):
         for q in range(nQ):
             ref = ro.maxsim_residual(Qs[q], codes, res, C, w, nbits, offsets, None, pad_len)
             _assert_scores(got[q], ref, f"batched nQ={nQ} nq={nq} q={q} {padding}")
+            _assert_kernel(got[q], Qs[q], (codes, res, C, w, nbits), offsets, None, pad_len, _form(nQ, nq),
+                           f"batched nQ={nQ} nq={nq} q={q} {padding}")
         one = flashmaxsim_score_residual(_gpu(Qs[nQ - 1]), *idx, padding=padding).cpu().numpy()
         _assert_scores(got[nQ - 1], one, "batched vs one query")
 
@@ -400,3 +443,63 @@ def test_batched_candidates_invalid_and_edges(cuda):
     assert got.shape == (7, ndocs) and np.all(got == 0.0)
     assert flashmaxsim_score_residual_batched(_gpu(Qs[:0]), *idx).shape == (0, ndocs)
     assert flashmaxsim_score_residual_batched(_gpu(Qs), *idx, pids=_gpu(np.zeros(0, np.int64))).shape == (7, 0)
+
+
+N_RANDOM = int(os.environ.get("TMS_RANDOM_SEEDS", "160")) // 4
+
+
+@pytest.mark.parametrize("seed", range(N_RANDOM))
+def test_random_residual_case(cuda, seed):
+    """Seeded sweep (``TMS_RANDOM_SEEDS=N`` runs N/4 seeds, default 40): nbits, width,
+    query length, document count and lengths (with empty documents), centroid count,
+    padding, candidate pids (repeats, unsorted) or all documents, and the entry point
+    (one query at every fused dispatch, or several queries through the batched kernel),
+    against the float64 oracle on the decompressed tokens."""
+    from tilemaxsim_amd import _lib, flashmaxsim_score_residual, flashmaxsim_score_residual_batched
+    rng = np.random.default_rng(90_000 + seed)
+    nbits = int(rng.choice([1, 2, 4]))
+    d = int(rng.choice([32, 64, 96, 128]))
+    nq = int(rng.choice([1, 5, 20, 32, 33, 64, 70]))
+    ndocs = int(rng.integers(1, 400))
+    lens = rng.integers(0, int(rng.choice([2, 17, 64, 180, 300])), ndocs)
+    lens[rng.random(ndocs) < 0.1] = 0
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = max(int(offsets[-1]), 1)
+    ncent = int(rng.choice([1, 7, 300, 4096]))
+    C, codes, res, w = _index(rng, T, d, nbits, ncent)
+    padding = str(rng.choice(["zeros", "mask"]))
+    pids = None
+    if seed % 3 == 0:
+        pids = rng.integers(0, ndocs, int(rng.integers(0, 2 * ndocs))).astype(np.int64)
+    nQ = 1 if seed % 2 == 0 else int(rng.integers(2, 7))
+    what = f"seed={seed} nbits={nbits} d={d} nq={nq} ndocs={ndocs} ncent={ncent} {padding} nQ={nQ} pids={pids is not None}"
+    print(what, flush=True)
+    Qs = _queries(rng, nQ, nq, d)
+    idx = (_gpu(codes), _gpu(res), _gpu(C), _gpu(w), nbits, _gpu(offsets))
+    pid_t = None if pids is None else _gpu(pids)
+    rows = lens if pids is None else lens[pids]
+    pad_len = int(rows.max()) if padding == "zeros" and len(rows) else 0
+    refs = [ro.maxsim_residual(Qs[q], codes, res, C, w, nbits, offsets, pids, pad_len) for q in range(nQ)]
+    idx_np = (codes, res, C, w, nbits)
+
+    def check(got, q, form, label):
+        absref = _assert_kernel(got, Qs[q], idx_np, offsets, pids, pad_len, form, label)
+        ref = refs[q]
+        fin = np.isfinite(ref)
+        assert np.array_equal(np.isfinite(got), fin), label
+        assert np.all((got[~fin] == ref[~fin]) | np.isnan(ref[~fin])), label
+        slack = 1e-3 * np.abs(ref[fin]) + 1e-3 + 3 * 2.0 ** -11 * absref[fin]
+        assert np.all(np.abs(got[fin] - ref[fin]) <= slack), f"{label}: codec check"
+
+    if nQ == 1:
+        for limit in (None, 1 << 40, 0):
+            if limit is None:
+                got = flashmaxsim_score_residual(_gpu(Qs[0]), *idx, pids=pid_t, padding=padding).cpu().numpy()
+            else:
+                with _lib.rerank_limit(limit):
+                    got = flashmaxsim_score_residual(_gpu(Qs[0]), *idx, pids=pid_t, padding=padding).cpu().numpy()
+            check(got, 0, "fused", f"{what} limit={limit}")
+    else:
+        got = flashmaxsim_score_residual_batched(_gpu(Qs), *idx, pids=pid_t, padding=padding).cpu().numpy()
+        for q in range(nQ):
+            check(got[q], q, _form(nQ, nq), f"{what} q={q}")

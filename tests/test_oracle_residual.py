@@ -198,3 +198,104 @@ def test_planted_missing_normalisation_is_caught():
     res = ro.pack_buckets(np.zeros((1, 16), dtype=np.uint8), 2)
     raw = ro.decompress_unnormalised(np.array([0], np.int32), res, C, np.zeros(4, np.float16), 2)[0]
     assert raw[0] != np.float16(0.6)  # skipping the normalisation fails the closed form
+
+
+def _kernel_index(rng, T, d, nbits, ncent):
+    C = rng.standard_normal((ncent, d)).astype(np.float32)
+    C /= np.linalg.norm(C, axis=1, keepdims=True)
+    codes = rng.integers(0, ncent, T).astype(np.int32)
+    buckets = rng.integers(0, 1 << nbits, (T, d)).astype(np.uint8)
+    w = np.sort(rng.normal(0, 0.05, 1 << nbits)).astype(np.float16)
+    return C.astype(np.float16), codes, ro.pack_buckets(buckets, nbits), w
+
+
+def test_kernel_envelope_closed_forms():
+    """One token v = (3, 4, 0, ...) (zero bucket weights): |v| = 5 exactly, so both norms
+    are 5 and inv = fp32(1/5). The fused form scores <q, v> * inv; the batched form rounds
+    x = fp16(v * inv) first: fp16(0.6000000089) = 0.60009765625, fp16(0.8000000119) =
+    0.7998046875."""
+    d, nbits = 32, 2
+    C = np.zeros((1, d), np.float16)
+    C[0, 0], C[0, 1] = 3, 4
+    w = np.zeros(4, np.float16)
+    codes = np.zeros(1, np.int32)
+    res = ro.pack_buckets(np.zeros((1, d), np.uint8), nbits)
+    Q = np.zeros((2, d), np.float16)
+    Q[0, 0], Q[0, 1] = 0.5, 0.25
+    Q[1, 1] = -1.0
+    offs = np.array([0, 1], np.int64)
+    n_lo, n_hi = ro.norm_candidates(ro.decompress_unnormalised(codes, res, C, w, nbits))
+    assert n_lo.tolist() == [5.0] and n_hi.tolist() == [5.0]
+    inv = float(np.float32(1) / np.float32(5))
+    lo, hi, a = ro.maxsim_residual_kernel_envelope(Q, codes, res, C, w, nbits, offs, form="fused")
+    assert lo[0] == hi[0] == 2.5 * inv + (-4.0) * inv
+    assert a[0] == 2.5 * inv + 4.0 * inv
+    lo, hi, a = ro.maxsim_residual_kernel_envelope(Q, codes, res, C, w, nbits, offs, form="batched")
+    x0, x1 = 0.60009765625, 0.7998046875
+    assert np.float16(3 * np.float32(inv)) == x0 and np.float16(4 * np.float32(inv)) == x1
+    assert lo[0] == hi[0] == (0.5 * x0 + 0.25 * x1) + (-x1)
+
+
+def test_norm_candidates_cover_every_fp32_summation_order():
+    """The norms a kernel forms from fp32 sums of the squares in any order (here: 24
+    random orders per token, sequential fp32 sums, fp32 square root, fp16 rounding) are
+    always one of the two candidates; where the two differ they are adjacent fp16
+    values, and some tokens of a random index do fall on a boundary."""
+    rng = np.random.default_rng(41)
+    C, codes, res, w = _kernel_index(rng, 6000, 64, 2, 50)
+    V = ro.decompress_unnormalised(codes, res, C, w, 2)
+    n_lo, n_hi = ro.norm_candidates(V)
+    sq = V.astype(np.float32) ** 2
+    for _ in range(24):
+        perm = rng.permutation(V.shape[1])
+        n2 = np.zeros(V.shape[0], np.float32)
+        for k in perm:
+            n2 = (n2 + sq[:, k]).astype(np.float32)
+        n = np.sqrt(n2).astype(np.float16).astype(np.float64)
+        assert np.all((n == n_lo) | (n == n_hi))
+    two = n_lo != n_hi
+    assert 0 < two.sum() < 0.05 * len(two)
+    assert np.all(np.nextafter(n_lo[two].astype(np.float16), np.float16(np.inf)).astype(np.float64) == n_hi[two])
+
+
+@pytest.mark.parametrize("form", ["fused", "batched"])
+def test_kernel_envelope_holds_simulated_kernels(form):
+    """A float32 simulation of each kernel (norm from an fp32 sum of squares in a random
+    order, fp32 dot products, the fused form's fp32 multiply by inv, the batched form's
+    fp16 rounding of x) over a random index with ragged and empty documents lies within
+    the envelope widened by the fp32-accumulation bar. The codec's decompress-then-score
+    differs from the fused form by more than that bar somewhere (the fused kernel never
+    rounds v / n to fp16), so its envelope is not the codec's oracle under another name;
+    the batched form rounds x as the codec does (by a multiply where the codec divides)."""
+    import accum_bar as bar
+    rng = np.random.default_rng(7 if form == "fused" else 8)
+    d, nbits, nq = 64, 2, 20
+    lens = rng.integers(0, 12, 300)
+    lens[::17] = 0
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    C, codes, res, w = _kernel_index(rng, int(offs[-1]), d, nbits, 40)
+    Q = rng.standard_normal((nq, d)).astype(np.float32)
+    Q = (Q / np.linalg.norm(Q, axis=1, keepdims=True)).astype(np.float16)
+    lo, hi, absref = ro.maxsim_residual_kernel_envelope(Q, codes, res, C, w, nbits, offs, form=form)
+    V = ro.decompress_unnormalised(codes, res, C, w, nbits).astype(np.float32)
+    perm = rng.permutation(d)
+    n2 = np.zeros(V.shape[0], np.float32)
+    for k in perm:
+        n2 = (n2 + V[:, k] * V[:, k]).astype(np.float32)
+    n = np.maximum(np.sqrt(n2).astype(np.float16).astype(np.float32), np.float32(5.9604645e-8))
+    inv = (np.float32(1) / n).astype(np.float32)
+    Qf = Q.astype(np.float32)
+    if form == "fused":
+        P = (V @ Qf.T).astype(np.float32) * inv[:, None]
+    else:
+        X = (V * inv[:, None]).astype(np.float16).astype(np.float32)
+        P = (X @ Qf.T).astype(np.float32)
+    sim = np.array([P[s:e].max(axis=0).sum(dtype=np.float32) if e > s else -np.inf
+                    for s, e in zip(offs[:-1], offs[1:])])
+    b = bar.bound(absref, d, nq)
+    fin = np.isfinite(lo)
+    assert np.array_equal(np.isinf(sim), ~fin)
+    assert np.all(sim[fin] >= lo[fin] - b[fin]) and np.all(sim[fin] <= hi[fin] + b[fin])
+    if form == "fused":
+        codec = ro.maxsim_residual(Q, codes, res, C, w, nbits, offs)
+        assert np.any(np.abs(codec[fin] - sim[fin]) > b[fin])
