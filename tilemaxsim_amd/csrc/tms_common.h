@@ -176,6 +176,81 @@ __device__ __forceinline__ float row_sum16(float s) {
   return s;
 }
 
+// Document end of the shared-tile kernels: NB query blocks of two 16-token halves, each
+// half's running max rmax[j][h] in the MFMA accumulator layout (lane (c, g): the max over
+// its rows of query token c). The row swaps move two accumulators at a time: register P
+// holds blocks 2P and 2P + 1 (block 0 alone when NB == 1), and its 16-lane row k ends with
+// the document's max of accumulator (2P + (k & 1), k >> 1) (of (0, k >> 1) when NB == 1),
+// so the query masks and scales of each lane's row are picked once, by init(). Each block
+// sums (0 + half 0) + half 1 per query token and then its 16 tokens by row_sum16: the bits
+// of reducing every accumulator on its own.
+template <int NB, bool QSCALE>
+struct DocEnd {
+  static constexpr int NPK = NB == 1 ? 1 : NB / 2;
+  bool qv_pk[NPK];
+  float qinv_pk[QSCALE ? NPK : 1];
+
+  __device__ __forceinline__ void init(const bool (&qv)[NB][2], const float (&qinv)[QSCALE ? NB : 1][2], int lane) {
+    const int krow = lane >> 4;
+#pragma unroll
+    for (int P = 0; P < NPK; P++) {
+      qv_pk[P] = false;
+      if constexpr (QSCALE) qinv_pk[P] = 1.f;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int j = NB == 1 ? 0 : 2 * P + (k & 1), h = k >> 1;
+        if (krow == k) {
+          qv_pk[P] = qv[j][h];
+          if constexpr (QSCALE) qinv_pk[P] = qinv[j][h];
+        }
+      }
+    }
+  }
+  // rows 0-1: max over x's two 32-lane halves; rows 2-3: over y's
+  __device__ static __forceinline__ float swap_max32(float x, float y) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, y),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1]));
+  }
+  // rows: max(x0, x1), max(y0, y1), max(x2, x3), max(y2, y3)
+  __device__ static __forceinline__ float swap_max16(float x, float y) {
+    const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, y),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (unsigned)q[0]), __builtin_bit_cast(float, (unsigned)q[1]));
+  }
+  // Lane doc_lane of pend[j] gets block j's score; every running max restarts at -inf.
+  __device__ __forceinline__ void finish(float (&rmax)[NB][2], bool padded, int lane, int doc_lane,
+                                         float (&pend)[NB]) const {
+#pragma unroll
+    for (int P = 0; P < NPK; P++) {
+      float x;
+      if constexpr (NB == 1) {
+        const float p0 = swap_max32(rmax[0][0], rmax[0][1]);
+        x = swap_max16(p0, p0);
+      } else {
+        const float p0 = swap_max32(rmax[2 * P][0], rmax[2 * P][1]);
+        const float p1 = swap_max32(rmax[2 * P + 1][0], rmax[2 * P + 1][1]);
+        x = swap_max16(p0, p1);
+      }
+      if constexpr (QSCALE) x *= qinv_pk[P];  // exact: a power of two
+      if (padded) x = fmaxf(x, 0.f);
+      x = 0.f + (qv_pk[P] ? x : 0.f);
+      const auto q = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, x),
+                                                      false, false);
+      const float sm = row_sum16(__builtin_bit_cast(float, (unsigned)q[0]) + __builtin_bit_cast(float, (unsigned)q[1]));
+#pragma unroll
+      for (int b = 0; b < (NB == 1 ? 1 : 2); b++) {
+        const int j = NB == 1 ? 0 : 2 * P + b;
+        const float v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sm), 16 * b));
+        pend[j] = lane == doc_lane ? v : pend[j];
+      }
+    }
+    const float NEG_INF = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < NB; j++) rmax[j][0] = rmax[j][1] = NEG_INF;
+  }
+};
+
 // Per-thread last-error text behind tms_last_error().
 void set_error(const char* fmt, ...);
 int fail(int code, const char* fmt, ...);

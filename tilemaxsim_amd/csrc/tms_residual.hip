@@ -711,21 +711,13 @@ __global__ void __launch_bounds__(64 * kResBatchedWaves, 1) residual_batched_ker
     float rmax[NB][2];
 #pragma unroll
     for (int j = 0; j < NB; j++) rmax[j][0] = rmax[j][1] = NEG_INF;
+    DocEnd<NB, false> doc_end;
+    {
+      const float no_scale[1][2] = {{1.f, 1.f}};
+      doc_end.init(qv, no_scale, lane);
+    }
     auto finish = [&]() {  // the document of wc ends with this tile
-      const bool padded = wc.len < a.pad_len;
-#pragma unroll
-      for (int j = 0; j < NB; j++) {
-        float s = 0.f;
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-          float m = cross_row_max(rmax[j][h]);
-          if (padded) m = fmaxf(m, 0.f);
-          s += qv[j][h] ? m : 0.f;
-          rmax[j][h] = NEG_INF;
-        }
-        s = row_sum16(s);
-        pend[j] = lane == (int)(wc.b - b_begin) ? s : pend[j];
-      }
+      doc_end.finish(rmax, wc.len < a.pad_len, lane, (int)(wc.b - b_begin), pend);
     };
     auto step = [&](auto slot) -> bool {
       constexpr int i = decltype(slot)::value;  // step index mod 6

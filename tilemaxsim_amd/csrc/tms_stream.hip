@@ -610,6 +610,9 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 2) batched_tile_kernel
 #pragma unroll
     for (int j = 0; j < NB; j++) rmax[j][0] = rmax[j][1] = NEG_INF;
 
+    DocEnd<NB, QSCALE> doc_end;
+    doc_end.init(qv, qinv, lane);
+
     auto step = [&](auto slot) -> bool {
       constexpr int i = decltype(slot)::value;  // step index mod NS
       constexpr int s1 = (i + 1) % NS;
@@ -652,20 +655,7 @@ __global__ void __launch_bounds__(64 * TMS_BATCHED_WAVES, 2) batched_tile_kernel
           rmax[j][h] = fmaxf(fmaxf(fmaxf(fmaxf(rmax[j][h], acc[j][h][0]), acc[j][h][1]), acc[j][h][2]), acc[j][h][3]);
       if (wc.t0 + 16 >= wc.len) {  // document wc.b ends with this tile
         const bool padded = wc.len < a.pad_len;
-#pragma unroll
-        for (int j = 0; j < NB; j++) {
-          float s = 0.f;
-#pragma unroll
-          for (int h = 0; h < 2; h++) {
-            float m = cross_row_max(rmax[j][h]);
-            if constexpr (QSCALE) m *= qinv[j][h];  // exact: a power of two
-            if (padded) m = fmaxf(m, 0.f);
-            s += qv[j][h] ? m : 0.f;
-            rmax[j][h] = NEG_INF;
-          }
-          s = row_sum16(s);
-          pend[j] = lane == (int)(wc.b - b_begin) ? s : pend[j];
-        }
+        doc_end.finish(rmax, padded, lane, (int)(wc.b - b_begin), pend);
       }
       advance(wc, true);
       return wc.b >= b_end;
