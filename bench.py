@@ -67,7 +67,7 @@ def parse():
                    help="--config c2b: fp32 queries against the --dtype documents (split, never rounded)")
     p.add_argument("--ncent", type=int, default=1 << 18,
                    help="--config c6 / c6b: centroids in the index (2^18, ColBERT's choice for ~332M tokens)")
-    p.add_argument("--lds-pattern", type=int, default=None, choices=range(10),
+    p.add_argument("--lds-pattern", type=int, default=None, choices=range(12),
                    help="--config ldsprobe: time this pattern alone (default: pattern 1 timed, all ten reported)")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -850,24 +850,30 @@ class ReadProbe:
 
 class LdsProbe:
     """LDS gather probe (tms_lds_probe): the cost of a ds_read_b128 wave-instruction when
-    16 consecutive lanes hit 16 different bank groups (pattern 0), when they read random
-    rows of one codebook subspace as the PQ kernel's gathers do (pattern 1, the timed
-    one), when they all hit one bank group (pattern 2), and when each bank group gets
-    four lanes of every 16 (pattern 3); patterns 4 to 7 repeat them at the PQ kernel's
-    occupancy and footprint (two 8-wave workgroups per CU, 64 KiB each), and patterns 8
-    and 9 repeat 5 and 4 with the PQ kernel's matrix work beside the gathers (two MFMAs
-    per gathered fragment, random fp16 data). ``--lds-pattern`` times one pattern alone
+    lane l hits bank group l % 16 (pattern 0), when the 16 lanes of an MFMA lane group
+    read random rows of one codebook subspace as the PQ kernel's gathers do (pattern 1,
+    the timed one), when they all hit one bank group (pattern 2), and when each bank
+    group gets four lanes of every 16 (pattern 3); patterns 4 to 7 repeat them at the PQ
+    kernel's occupancy and footprint (two 8-wave workgroups per CU, 64 KiB each), patterns
+    8 and 9 repeat 5 and 4 with the PQ kernel's matrix work beside the gathers (two MFMAs
+    per gathered fragment, random fp16 data), and patterns 10 and 11 tell the part's pass
+    rule (four passes of the 16 lanes that share lane bit 5 and the parity of lane bits
+    2-4) from passes of 16 consecutive lanes. ``--lds-pattern`` times one pattern alone
     (for counter runs). LDS bytes, not HBM bytes."""
     kernel = "lds_probe_kernel"
     _P = {0: "conflict-free (lane l -> bank group l % 16, random rows)",
           1: "PQ codebook gather (one subspace per 16-lane group, random codes)",
           2: "one bank group per 16-lane group, random rows",
-          3: "lane l -> bank group (l / 4) % 16: balanced over the wave, 4-way within 16 lanes"}
+          3: "lane l -> bank group (l / 4) % 16: balanced over the wave, 4-way in every pass"}
     PATTERNS = {**{p: f"{w}; one 16-wave workgroup per CU, 128 KiB" for p, w in _P.items()},
                 **{p + 4: f"{w}; two 8-wave workgroups per CU, 64 KiB each (the PQ kernel's shape)"
                    for p, w in _P.items()},
                 8: f"{_P[1]}; the PQ kernel's shape, two MFMAs per gathered fragment",
-                9: f"{_P[0]}; the PQ kernel's shape, two MFMAs per gathered fragment"}
+                9: f"{_P[0]}; the PQ kernel's shape, two MFMAs per gathered fragment",
+                10: "lane l -> bank group l % 8 + 8 * bit 4 of l: conflict-free by the pass rule, 2-way in passes "
+                    "of 16 consecutive lanes; one 16-wave workgroup per CU, 128 KiB",
+                11: "lane l -> bank group l % 8 + 8 * parity of bits 2-4 of l: 2-way by the pass rule, "
+                    "conflict-free in passes of 16 consecutive lanes; one 16-wave workgroup per CU, 128 KiB"}
 
     def __init__(self, torch, pattern=None):
         self.pattern = pattern
@@ -894,7 +900,7 @@ class LdsProbe:
 
     def config(self):
         return {"workload": "ldsprobe: 4,096 waves x 65,536 ds_read_b128 per wave, 16 waves per CU (one "
-                            "workgroup over 128 KiB, or two over 64 KiB each), four lane -> address patterns, "
+                            "workgroup over 128 KiB, or two over 64 KiB each), six lane -> address patterns, "
                             "and two of them with MFMAs beside the gathers",
                 "pattern": self.pattern}
 

@@ -115,7 +115,9 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     rc, msg = _c_call("tms_pq_score_batched", 16, 2, 32, 16, 16, 256, 8, 2, 16, 10, 5, 16, None)
     assert rc == 2 and "dtype" in msg
     # the LDS probe checks its pattern and buffers before launching
-    rc, msg = _c_call("tms_lds_probe", 10, 16, 4096, 16, 4096 * 64, None)
+    rc, msg = _c_call("tms_lds_probe", 12, 16, 4096, 16, 4096 * 64, None)
+    assert rc == 1 and "pattern" in msg
+    rc, msg = _c_call("tms_lds_probe", -1, 16, 4096, 16, 4096 * 64, None)
     assert rc == 1 and "pattern" in msg
     rc, msg = _c_call("tms_lds_probe", 1, 16, 100, 16, 4096 * 64, None)
     assert rc == 1 and "cycles" in msg

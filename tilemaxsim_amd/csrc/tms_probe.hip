@@ -57,19 +57,25 @@ extern "C" int tms_read_probe(const void* buf, int64_t bytes, uint32_t* sink, in
 }
 
 // ---------------------------------------------------------------------------------
-// LDS gather probe: the cost of one ds_read_b128 wave-instruction for four lane ->
-// address patterns over a 128 KiB LDS buffer (one 16-wave workgroup per CU, every
-// offset masked into the buffer), and the same four patterns (4 to 7) at the PQ
-// kernel's occupancy and footprint: two 8-wave workgroups per CU, each over its own
-// 64 KiB buffer (a codebook's size). It backs the PQ kernel's floor: its codebook
-// gathers are pattern 1 (5). Not part of the scoring path; no reference counterpart.
-//   0: 16 consecutive lanes read 16 different 16-byte bank groups of random 256-byte
-//      rows (lane l -> group l % 16): conflict-free;
+// LDS gather probe: the cost of one ds_read_b128 wave-instruction for a lane -> address
+// pattern over a 128 KiB LDS buffer (one 16-wave workgroup per CU, every offset masked
+// into the buffer), and patterns 0 to 3 again (4 to 7) at the PQ kernel's occupancy and
+// footprint: two 8-wave workgroups per CU, each over its own 64 KiB buffer (a codebook's
+// size). It backs the PQ kernel's floor: its codebook gathers are pattern 1 (5). Not
+// part of the scoring path; no reference counterpart. A wave-instruction is served in
+// four passes of 16 lanes, the lanes that share lane bit 5 and the parity of lane bits
+// 2-4 (patterns 10 and 11 tell this apart from passes of 16 consecutive lanes); a pass
+// costs the largest number of distinct rows it puts on one 16-byte bank group.
+//   0: lane l -> bank group l % 16, random 256-byte rows: conflict-free;
 //   1: the PQ gather: the 16 lanes of an MFMA lane group read random 16-byte rows of one
 //      4 KiB subspace block (bank group = row % 16, random);
 //   2: the 16 lanes of a lane group all read one bank group at random rows;
 //   3: lane l -> bank group (l / 4) % 16 at random rows: every bank group gets exactly
-//      four lanes of the wave, but four lanes of each 16-lane group share one.
+//      four lanes of the wave, and four lanes of every pass share one;
+//   10: lane l -> bank group l % 8 + 8 * (bit 4 of l): conflict-free by the pass rule,
+//       two lanes per bank group in every pass of 16 consecutive lanes;
+//   11: lane l -> bank group l % 8 + 8 * (parity of bits 2-4 of l): two lanes per bank
+//       group in every pass by the rule, conflict-free in passes of 16 consecutive lanes.
 // Patterns 8 and 9 run patterns 1 and 0 at the PQ kernel's shape with the PQ kernel's
 // matrix work beside the gathers (two MFMAs per gathered fragment, random fp16 data):
 // the gather rate this part holds under that mix, with no HBM traffic.
@@ -120,7 +126,9 @@ __global__ void __launch_bounds__(NT) lds_probe_kernel(int pattern, int64_t* __r
     if (pattern == 0) u = (h % 512u) * 16u + (uint32_t)(lane & 15);
     else if (pattern == 1) u = (uint32_t)((j + 4 * (lane >> 4)) & 15) * 256u + (h % 256u);
     else if (pattern == 2) u = (h % 512u) * 16u + (uint32_t)(lane >> 4);
-    else u = (h % 512u) * 16u + (uint32_t)((lane >> 2) & 15);
+    else if (pattern == 3) u = (h % 512u) * 16u + (uint32_t)((lane >> 2) & 15);
+    else if (pattern == 4) u = (h % 512u) * 16u + (uint32_t)((lane & 7) + 8 * ((lane >> 4) & 1));
+    else u = (h % 512u) * 16u + (uint32_t)((lane & 7) + 8 * (((lane >> 2) ^ (lane >> 3) ^ (lane >> 4)) & 1));
     o[j] = u & (UNITS - 1);
   }
   __syncthreads();
@@ -168,14 +176,14 @@ __global__ void __launch_bounds__(NT) lds_probe_kernel(int pattern, int64_t* __r
 extern "C" int tms_lds_probe(int pattern, int64_t* cycles, int64_t cycle_words, uint32_t* sink, int64_t sink_words,
                              void* stream) {
   const char* fn = "tms_lds_probe";
-  if (pattern < 0 || pattern > 9) return fail(TMS_ERR_INVALID, "%s: pattern=%d must be 0 to 9", fn, pattern);
+  if (pattern < 0 || pattern > 11) return fail(TMS_ERR_INVALID, "%s: pattern=%d must be 0 to 11", fn, pattern);
   if (!cycles || cycle_words < TMS_LDS_PROBE_WAVES)
     return fail(TMS_ERR_INVALID, "%s: cycles needs %d words", fn, TMS_LDS_PROBE_WAVES);
   if (!sink || sink_words < TMS_LDS_PROBE_WAVES * 64)
     return fail(TMS_ERR_INVALID, "%s: the sink needs %d words", fn, TMS_LDS_PROBE_WAVES * 64);
-  if (pattern < 4)  // one 16-wave workgroup per CU over 128 KiB
+  if (pattern < 4 || pattern >= 10)  // one 16-wave workgroup per CU over 128 KiB
     hipLaunchKernelGGL((lds_probe_kernel<1024, kLdsProbeUnits, false>), dim3(TMS_LDS_PROBE_WAVES / 16), dim3(1024),
-                       kLdsProbeUnits * 16, (hipStream_t)stream, pattern, cycles, sink);
+                       kLdsProbeUnits * 16, (hipStream_t)stream, pattern < 4 ? pattern : pattern - 6, cycles, sink);
   else if (pattern < 8)  // the PQ kernel's shape: two 8-wave workgroups per CU, 64 KiB each
     hipLaunchKernelGGL((lds_probe_kernel<512, kLdsProbeUnits / 2, false>), dim3(TMS_LDS_PROBE_WAVES / 8), dim3(512),
                        kLdsProbeUnits * 8, (hipStream_t)stream, pattern - 4, cycles, sink);
